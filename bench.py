@@ -1,0 +1,283 @@
+"""Benchmark: the full N=1 decode matvec set of the 36-layer trunk plus the
+tied Q8_0 output head, on one MI355X.
+
+Workload (synthetic, seeded, random-init weights of the real shapes):
+  per layer, VQ dim 4, nc 4096, 2 residual stages, DQV3, bf16 activations:
+    q 4096x2560, k 1024x2560, v 1024x2560, head gate 16x2560   (one launch, shared x)
+    o 2560x4096                                                 (one launch)
+    gate 10240x2560, up 10240x2560                              (one launch, shared x)
+    down 2560x10240                                             (one launch)
+  head: Q8_0 151936x2560 (one launch)
+A step is one token: the 145 launches in forward order on one stream,
+replayed as one HIP graph (native plan, sparkmv_plan_*). Weights and inputs
+are resident in HBM before timing starts.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--mode graph|eager]
+                    [--workload decode-set|ffn-up|q6k-down|verify8|prefill512]
+
+Prints one JSON line (rank 0). The metric is time per token (lower is
+better); achieved GB/s over the algorithmic bytes (container + bf16 x + f32 y
+per matvec) and the VQ kernel's roofline fraction come with it, plus the
+oracle's CPU time for a bounded sample of the same set.
+"""
+import argparse
+import concurrent.futures
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "spark-x2.6-4b-q6k_amd"))
+
+PEAK_GBPS = 8000.0
+PEAK_F16_TFLOPS = 2500.0
+
+LAYERS, HIDDEN, FFN, QD, KVD, NHEAD = 36, 2560, 10240, 4096, 1024, 16
+VOCAB = 151936
+VQ = dict(dim=4, nc=4096, nstages=2, v3=1)
+METRIC = "decode matvec µs/token (36-layer trunk, N=1) + achieved HBM GB/s vs peak"
+
+# per layer: (name, rows, cols, launch group)
+LAYER_MATS = [("q", QD, HIDDEN, 0), ("k", KVD, HIDDEN, 0), ("v", KVD, HIDDEN, 0), ("g", NHEAD, HIDDEN, 0),
+              ("o", HIDDEN, QD, 1), ("gate", FFN, HIDDEN, 2), ("up", FFN, HIDDEN, 2), ("down", HIDDEN, FFN, 3)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def seed_of(layer, idx):
+    return 0x5EED0000 + 97 * layer + idx
+
+
+def gen_layer(sm, layer):
+    return [sm.synth_container(seed_of(layer, i), r, c, VQ["dim"], VQ["nc"], VQ["nstages"], VQ["v3"])
+            for i, (_, r, c, _) in enumerate(LAYER_MATS)]
+
+
+def algorithmic_bytes_vq(nbytes_container, rows, cols, ncol=1):
+    """Container bytes + bf16 x + f32 y of one matvec."""
+    return nbytes_container + 2 * cols * ncol + 4 * rows * ncol
+
+
+def build_decode_set(sm, torch, dev, ncol=1, head_rows=VOCAB, layers=LAYERS):
+    """Generate, upload and record the per-token chain. Returns the plan and
+    the byte accounting per op."""
+    t0 = time.time()
+    with concurrent.futures.ThreadPoolExecutor(min(16, os.cpu_count() or 4)) as ex:
+        hosts = list(ex.map(lambda l: gen_layer(sm, l), range(layers)))
+        head_future = ex.submit(sm.synth_q8_0, 0x4EAD, head_rows, HIDDEN)
+        head = head_future.result()
+    log(f"generated {layers} layers + head in {time.time() - t0:.1f} s")
+    xs = {c: torch.from_numpy(sm.synth_bf16(c, ncol * c).view(np.int16).reshape(ncol, c).copy()).to(dev)
+          for c in (HIDDEN, QD, FFN)}
+    plan = sm.Plan()
+    op_bytes, op_kind = [], []
+    devs = []
+    for l in range(layers):
+        mats = [sm.DeviceContainer(h, dev) for h in hosts[l]]
+        devs.append(mats)
+        ys = [torch.zeros(ncol, r, device=dev) for (_, r, _, _) in LAYER_MATS]
+        for grp in range(4):
+            idx = [i for i, m in enumerate(LAYER_MATS) if m[3] == grp]
+            cols = LAYER_MATS[idx[0]][2]
+            if len(set(LAYER_MATS[i][1] for i in idx)) > 1 and ncol > 1:
+                # one ldy per launch: give every matrix of the group a buffer of the widest row count
+                w = max(LAYER_MATS[i][1] for i in idx)
+                for i in idx:
+                    ys[i] = torch.zeros(ncol, w, device=dev)
+            plan.add_vq([mats[i] for i in idx], xs[cols], [ys[i] for i in idx], ncols=ncol, accumulate=False,
+                        label=f"L{l}:" + "+".join(LAYER_MATS[i][0] for i in idx))
+            op_bytes.append(sum(algorithmic_bytes_vq(hosts[l][i].nbytes, LAYER_MATS[i][1], cols, ncol) for i in idx))
+            op_kind.append("vq")
+        hosts[l] = None
+    hb = torch.from_numpy(head).to(dev)
+    logits = torch.zeros(ncol, head_rows, device=dev)
+    plan.add_kquant("q8_0", hb, head_rows, HIDDEN, xs[HIDDEN], logits, ncols=ncol, label="head")
+    op_bytes.append(head.nbytes + 2 * HIDDEN * ncol + 4 * head_rows * ncol)
+    op_kind.append("q8_0")
+    plan.keep.append((devs, hb, logits, xs))
+    torch.cuda.synchronize()
+    log(f"uploaded in {time.time() - t0:.1f} s total")
+    return plan, np.array(op_bytes, dtype=np.float64), op_kind
+
+
+def time_steps(plan, torch, stream, steps, warmup, mode):
+    if mode == "graph":
+        plan.run(stream)                  # one-time launch setup outside the capture
+        torch.cuda.synchronize()
+        plan.capture(stream)
+    run = plan.launch if mode == "graph" else plan.run
+    for _ in range(warmup):
+        run(stream)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        run(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline_decode_set(sample_layers=2, head_rows=8192, reps=5):
+    """The oracle's runtime path (model.rs:209-234): containers decoded to f32
+    once, then a row-parallel 8-lane dot per matvec, all host threads. Timed
+    on a bounded sample (a few layers and a slice of the head) and scaled to
+    one token of the full set."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import sparkmv as sm
+    import sparkref as ref
+    nth = ref.threads()
+    per_layer = []
+    for l in range(sample_layers):
+        hosts = gen_layer(sm, l)
+        Ws = [ref.decode(h) for h in hosts]
+        xs = {c: sm.bf16_to_f32(sm.synth_bf16(c, c)) for c in (HIDDEN, QD, FFN)}
+        best = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            for (_, r, c, _), W in zip(LAYER_MATS, Ws):
+                ref.matvec(W, xs[c], nth)
+            best.append(time.perf_counter() - t)
+        per_layer.append(np.median(best))
+        del Ws
+    blocks = sm.synth_q8_0(0x4EAD, head_rows, HIDDEN)
+    Wh = ref.q8_0_dequant(blocks, head_rows, HIDDEN)
+    xh = sm.bf16_to_f32(sm.synth_bf16(HIDDEN, HIDDEN))
+    th = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        ref.matvec(Wh, xh, nth)
+        th.append(time.perf_counter() - t)
+    us = (np.mean(per_layer) * LAYERS + np.median(th) * VOCAB / head_rows) * 1e6
+    return {"value": round(float(us), 1), "unit": "us/token", "cores": int(nth), "kind": "port",
+            "sample": f"oracle decode-to-f32 + row-parallel 8-lane dot (model.rs:209-234) on {sample_layers} of 36 "
+                      f"layers and {head_rows} of {VOCAB} head rows, median of {reps}, scaled to one token"}
+
+
+def bench_decode_set(args, sm, torch, dev):
+    stream = torch.cuda.Stream(device=dev)
+    ncol = 8 if args.workload == "verify8" else 1
+    with torch.cuda.stream(stream):
+        plan, op_bytes, op_kind = build_decode_set(sm, torch, dev, ncol=ncol, head_rows=args.head_rows)
+        ms = time_steps(plan, torch, stream, args.steps, args.warmup, args.mode)
+        op_ms = plan.time_ops(stream, iters=max(3, min(args.steps, 10)))
+    total_bytes = float(op_bytes.sum())
+    vq = np.array([k == "vq" for k in op_kind])
+    vq_bytes, vq_ms = float(op_bytes[vq].sum()), float(op_ms[vq].sum())
+    n_vq = int(vq.sum())
+    achieved = vq_bytes / (vq_ms * 1e-3) / 1e9
+    head_ms = float(op_ms[~vq].sum())
+    groups = {}
+    for lab, b, t in zip(plan.labels, op_bytes, op_ms):
+        key = lab.split(":")[-1]
+        g = groups.setdefault(key, [0.0, 0.0, 0])
+        g[0] += b
+        g[1] += t
+        g[2] += 1
+    for k, (b, t, n) in groups.items():
+        log(f"  {k:16s} {n:3d} launches  {t / n * 1e3:8.2f} us/launch  {b / (t * 1e-3) / 1e9:8.1f} GB/s")
+    log(f"  step {ms * 1e3:.1f} us ({args.mode}); sum of op times {op_ms.sum() * 1e3:.1f} us")
+    workload = ("36-layer N=8 verify matvec set (trunk + Q8_0 head), weights decoded once per step"
+                if ncol == 8 else "36-layer N=1 decode matvec set + tied Q8_0 head")
+    out = {
+        "metric": METRIC,
+        "value": round(ms * 1e3, 2),
+        "unit": "us/token" if ncol == 1 else "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16xf16->f32 (bf16 x)",
+        "data": "synthetic (seeded, random-init weights of the real shapes)",
+        "config": {"workload": workload, "layers": LAYERS, "hidden": HIDDEN, "ffn": FFN, "q_dim": QD, "kv_dim": KVD,
+                   "vq": "dim 4, nc 4096, 2 stages, DQV3 12-bit", "head": f"Q8_0 {args.head_rows}x{HIDDEN}",
+                   "columns": ncol, "launches_per_step": len(op_ms), "mode": args.mode},
+        "achieved_gbps": round(total_bytes / (ms * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(total_bytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
+        "algorithmic_bytes_per_step": int(total_bytes),
+        "roofline": {"bound": "hbm", "kernel": "vq_mfma_kernel", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": round(vq_bytes / n_vq), "avg_launch_us": round(vq_ms / n_vq * 1e3, 3),
+                     "head_q8_0": {"us": round(head_ms * 1e3, 2),
+                                   "gbps": round(float(op_bytes[~vq].sum()) / (head_ms * 1e-3) / 1e9, 1)}},
+    }
+    return out
+
+
+def bench_single(args, sm, torch, dev):
+    """ffn-up: one VQ GEMV 10240x2560 (N=1); q6k-down: one Q6_K GEMV
+    2560x10240; prefill512: VQ GEMM 10240x2560 against 512 bf16 tokens."""
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        plan = sm.Plan()
+        if args.workload == "ffn-up":
+            data = sm.synth_container(1, FFN, HIDDEN)
+            m = sm.DeviceContainer(data, dev)
+            x = torch.from_numpy(sm.synth_bf16(2, HIDDEN).view(np.int16).reshape(1, HIDDEN).copy()).to(dev)
+            y = torch.zeros(1, FFN, device=dev)
+            plan.add_vq([m], x, [y])
+            nbytes = algorithmic_bytes_vq(data.nbytes, FFN, HIDDEN)
+            plan.keep.append(m)
+        elif args.workload == "q6k-down":
+            blocks = torch.from_numpy(sm.synth_q6k(3, HIDDEN, FFN)).to(dev)
+            x = torch.from_numpy(sm.synth_bf16(4, FFN).view(np.int16).reshape(1, FFN).copy()).to(dev)
+            y = torch.zeros(1, HIDDEN, device=dev)
+            plan.add_kquant("q6_k", blocks, HIDDEN, FFN, x, y)
+            nbytes = blocks.numel() + 2 * FFN + 4 * HIDDEN
+        else:
+            raise SystemExit(f"unknown workload {args.workload}")
+        ms = time_steps(plan, torch, stream, args.steps, args.warmup, args.mode)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"metric": METRIC, "value": round(ms * 1e3, 3), "unit": "us/call", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f16xf16->f32 (bf16 x)", "data": "synthetic",
+            "config": {"workload": args.workload}, "achieved_gbps": round(gbps, 1),
+            "frac_of_peak": round(gbps / PEAK_GBPS, 4), "algorithmic_bytes_per_step": int(nbytes)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
+    ap.add_argument("--workload", default="decode-set",
+                    choices=["decode-set", "verify8", "ffn-up", "q6k-down"])
+    ap.add_argument("--head-rows", type=int, default=VOCAB)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: the matvec path runs on a single MI355X, and "
+                                   "multi-GPU sharding (by output rows, zero exchange) is described, not built",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    import sparkmv as sm
+    sm.lib()
+    if not torch.cuda.is_available():
+        sys.exit("no GPU visible")
+    dev = torch.device("cuda:0")
+    name = torch.cuda.get_device_name(0)
+    log(f"device {name}")
+    if args.workload in ("decode-set", "verify8"):
+        out = bench_decode_set(args, sm, torch, dev)
+        if not args.no_cpu_baseline and args.workload == "decode-set":
+            t = time.time()
+            out["cpu_baseline"] = cpu_baseline_decode_set()
+            log(f"cpu baseline took {time.time() - t:.1f} s")
+    else:
+        out = bench_single(args, sm, torch, dev)
+    out["device"] = name
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,221 @@
+/* sparkmv.h — C-ABI of the MI355X (gfx950) quantized matvec library.
+ *
+ * Two groups of entry points:
+ *
+ *  1. vqg_*: drop-in replacements for the reference's CUDA C-ABI
+ *     (tools/vq/gpu/decode-gpu.cu:765-1140), same names, argument meaning,
+ *     return convention and error text channel. Each declaration cites the
+ *     reference function it replaces. As there:
+ *       - `payload` is a device pointer to ONE stage payload (DQVQ or DQV3),
+ *         not to the container;
+ *       - x and y are device f32 pointers; y ACCUMULATES (y += W x), so a
+ *         caller zeroes it or adds into a residual on purpose;
+ *       - 0 = success, -1 = failure with a message in vqg_decode_error();
+ *       - *_launch* entry points are asynchronous on the default (null)
+ *         stream; timed entry points synchronize and report the best of
+ *         `iters` runs in *ms;
+ *       - not thread-safe (one static error buffer).
+ *     Slack contract: the reference requires 8 zeroed bytes past every stage
+ *     payload (decode-gpu.cu:95-102). This library never reads past a stage's
+ *     index stream, so the slack is accepted but not needed.
+ *
+ *  2. sparkmv_*: the same operations with what the reference's ABI lacks:
+ *     bf16 activations, N <= 16 activation columns decoded once
+ *     (speculative verify), every stage of a container in one launch, several
+ *     matrices sharing one x in one launch, Q6_K and Q8_0 GEMV, token-major
+ *     prefill, and an explicit hipStream_t (passed as void *, NULL = default).
+ *     Same return and error convention.
+ *
+ * Variant numbers for the VQ GEMV (vqg_gemv_ready / _t / _launch_t):
+ *   0 auto (fastest ready kernel)    1 generic wave-per-row kernel
+ *   2 wave-per-row, codebook in LDS  3 DQV3 dim-4 MFMA block kernel
+ * In the reference, `vqg_gemv_t` variant 0 named its shared-memory kernel;
+ * every kernel here keeps the codebook on chip, so 0 means auto everywhere.
+ * Launch widths (`threads`) must be multiples of 64 (wave64).
+ */
+#ifndef SPARKMV_H
+#define SPARKMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================= reference-compatible ABI ========================= */
+
+/* decode-gpu.cu:23 vqg_decode_error */
+const char * vqg_decode_error(void);
+/* decode-gpu.cu:769-775 vqg_device_name */
+int vqg_device_name(char * out, int n);
+/* decode-gpu.cu:779-783 vqg_driver_version (HIP's encoding) */
+int vqg_driver_version(void);
+
+/* decode-gpu.cu:788-797 vqg_gemv_ready */
+int vqg_gemv_ready(int dim, int nc, int rows, int cols, int v3, int variant);
+/* decode-gpu.cu:865-906 vqg_gemv_t */
+int vqg_gemv_t(const void * payload, int dim, int nc, int rows, int cols, int v3,
+               const float * x, float * y, int variant, int threads, int iters, double * ms);
+/* decode-gpu.cu:908-911 vqg_gemv */
+int vqg_gemv(const void * payload, int dim, int nc, int rows, int cols, int v3,
+             const float * x, float * y, int variant, int iters, double * ms);
+/* decode-gpu.cu:916-921 vqg_gemv_launch_t */
+int vqg_gemv_launch_t(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                      const float * x, float * y, int variant, int threads);
+/* decode-gpu.cu:923-928 vqg_gemv_launch */
+int vqg_gemv_launch(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                    const float * x, float * y, int variant);
+/* decode-gpu.cu:835-857 vqg_dequant: decode one stage into out (accumulates) */
+int vqg_dequant(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                float * out, int iters, double * ms);
+/* decode-gpu.cu:947-956 vqg_row_dequant: one row of one stage (accumulates) */
+int vqg_row_dequant(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                    int row, float * out);
+
+/* Prefill: xT is [cols][ntok], y is [ntok][rows], both device f32; y accumulates.
+ * Variants: 0 auto, 1 and 2 the MFMA tile kernel (tile from the table below),
+ * 3 the one-thread-per-(row, token) kernel (any geometry). */
+/* decode-gpu.cu:995-1005 vqg_prefill_ready */
+int vqg_prefill_ready(int dim, int nc, int rows, int cols, int v3, int variant);
+/* decode-gpu.cu:1008 vqg_prefill_cfg_count */
+int vqg_prefill_cfg_count(void);
+/* decode-gpu.cu:1010-1015 vqg_prefill_cfg */
+int vqg_prefill_cfg(int idx, int * bn, int * bk);
+/* decode-gpu.cu:1020-1025 vqg_prefill_cfg_ready */
+int vqg_prefill_cfg_ready(int dim, int nc, int rows, int cols, int v3, int bn, int bk, int variant);
+/* decode-gpu.cu:1030-1043 vqg_prefill */
+int vqg_prefill(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                const float * xT, int ntok, float * y, int iters, double * ms, int variant);
+/* decode-gpu.cu:1046-1060 vqg_prefill_tile */
+int vqg_prefill_tile(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                     const float * xT, int ntok, float * y, int iters, double * ms,
+                     int bn, int bk, int variant);
+/* decode-gpu.cu:1066-1089 vqg_prefill_launch */
+int vqg_prefill_launch(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                       const float * xT, int ntok, float * y, int variant);
+/* decode-gpu.cu:1094-1117 vqg_prefill_launch_tile */
+int vqg_prefill_launch_tile(const void * payload, int dim, int nc, int rows, int cols, int v3,
+                            const float * xT, int ntok, float * y, int bn, int bk, int variant);
+/* decode-gpu.cu:1119-1138 vqg_gemv_f32: y[r] += dot(w row r, x), f32 */
+int vqg_gemv_f32(const float * w, const float * x, float * y, int rows, int cols, int iters, double * ms);
+
+/* ============================ sparkmv ABI ================================= */
+
+#define SPARKMV_X_BF16 0   /* activations are bf16 bit patterns (uint16) */
+#define SPARKMV_X_F32  1   /* activations are f32 */
+
+/* Parsed RQVQ container, as tools/vq-format/src/lib.rs:240-306 validates it. */
+typedef struct {
+    int dim, nc, nstages, rows, cols, v3, nbit;
+    uint64_t payload_bytes;
+    uint64_t stage_offset[4];   /* byte offset of each stage payload in the file */
+    uint64_t stage_bytes;       /* bytes per stage payload */
+} sparkmv_container_info;
+
+/* Validate a container held in HOST memory and locate its stages; refusals
+ * and their messages follow Container::open (lib.rs:240-306). No counterpart
+ * entry point in the reference's C-ABI: its loaders parse headers themselves
+ * (tools/vq/gpu/vq-model-gpu.cu:230-328). */
+int sparkmv_container_open(const void * bytes, size_t len, sparkmv_container_info * info);
+
+/* Bytes of one stage payload for a geometry (tools/vq/decode.c:107-125). */
+size_t sparkmv_stage_bytes(int v3, int rows, int cols, int dim, int nc);
+
+/* Fused VQ GEMV over every stage of one matrix in one launch:
+ *   y[n*ldy + r] (+)= sum_s g_s[r] * sum_i cb_s[idx_s(r,i)] . x[n*ldx + dim*i ..]
+ * stages[s] are device pointers to the stage payloads (host array of
+ * nstages <= 4 pointers); x has ncols <= 16 columns; accumulate 1 adds into y,
+ * 0 overwrites it. Replaces the per-stage loop of tools/vq/gpu/vq-model-gpu.cu:651-660
+ * (gemv) with the bf16 / N-column forms the reference lacks. variant as above. */
+int sparkmv_vq_gemv(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                    const void * x, int x_dtype, int ldx, int ncols, float * y, int ldy,
+                    int accumulate, int variant, void * stream);
+
+/* One matrix of a multi-matrix launch. */
+typedef struct {
+    const void * stages[4];
+    float * y;
+    int rows;
+} sparkmv_vq_matrix;
+
+/* Several VQ matrices that share dim, nc, cols, format, stage count and x in
+ * one launch (q/k/v/gate of a layer, or gate/up): the forward's call sites
+ * tools/vq-runtime/src/model.rs:481-482 and :570-571 issue them back to back
+ * on the same input. nmat <= 8. */
+int sparkmv_vq_gemv_multi(const sparkmv_vq_matrix * mats, int nmat, int nstages, int dim, int nc, int cols,
+                          int v3, const void * x, int x_dtype, int ldx, int ncols, int ldy,
+                          int accumulate, int variant, void * stream);
+
+/* Bit-exact decode of every stage into out (rows x cols f32, row-major):
+ * out (+)= sum_s cb_s[idx] * g_s, stage 0 first (lib.rs:197-211, :309-315). */
+int sparkmv_vq_dequant(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                       float * out, int accumulate, void * stream);
+
+/* ggml Q6_K GEMV: blocks are row-major [rows][cols/256] block_q6_K (210 B:
+ * ql[128] qh[64] int8 scales[16] fp16 d). cols % 256 == 0. y as above.
+ * No reference implementation exists (tools/vq/quant_err.c:38-43 calls
+ * llama.cpp, absent); block size from tools/kquant/stubs.c:30,:44. */
+int sparkmv_q6k_gemv(const void * blocks, int rows, int cols, const void * x, int x_dtype, int ldx, int ncols,
+                     float * y, int ldy, int accumulate, void * stream);
+/* ggml Q8_0 GEMV: [rows][cols/32] block_q8_0 (34 B: fp16 d, int8 qs[32]);
+ * the tied head (tools/dspark/src/gguf.rs:201; tools/kquant/stubs.c:25,:39). */
+int sparkmv_q8_0_gemv(const void * blocks, int rows, int cols, const void * x, int x_dtype, int ldx, int ncols,
+                      float * y, int ldy, int accumulate, void * stream);
+/* Exact dequant of Q6_K / Q8_0 rows into f32 (overwrites out). */
+int sparkmv_q6k_dequant(const void * blocks, int rows, int cols, float * out, void * stream);
+int sparkmv_q8_0_dequant(const void * blocks, int rows, int cols, float * out, void * stream);
+
+/* Prefill GEMM over every stage, token-major: x is [ntok][ldx] (bf16 or f32),
+ * y is [ntok][ldy] f32, y (+)= W x_t for each token t. Replaces the
+ * transpose + vqg_prefill_launch_tile route of tools/vq/gpu/vq-model-gpu.cu:838-851, :899-900. */
+int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                       const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy,
+                       int accumulate, void * stream);
+
+/* ---- decode-set plan: a recorded chain of matvec launches ----
+ * The per-token matvec chain of the forward (tools/vq/gpu/vq-model-gpu.cu:776-835
+ * issues it launch by launch from the host; the Rust runtime calls matvec at
+ * tools/vq-runtime/src/model.rs:481-482, :559, :570-571, :575, :585-590).
+ * A plan records the chain once with its device pointers and issues it
+ * eagerly (sparkmv_plan_run) or replays it as one HIP graph
+ * (sparkmv_plan_capture, then sparkmv_plan_launch). Ops run in record order
+ * on one stream. No op clears memory with a memset, so capture is safe. */
+void * sparkmv_plan_create(void);
+void sparkmv_plan_destroy(void * plan);
+int sparkmv_plan_size(void * plan);
+/* Append one VQ launch over nmat matrices sharing x (as sparkmv_vq_gemv_multi). */
+int sparkmv_plan_add_vq(void * plan, const sparkmv_vq_matrix * mats, int nmat, int nstages, int dim, int nc, int cols,
+                        int v3, const void * x, int x_dtype, int ldx, int ncols, int ldy, int accumulate,
+                        int variant);
+/* Append one k-quant GEMV: kind 6 = Q6_K, 8 = Q8_0 (as sparkmv_q6k_gemv / _q8_0_gemv). */
+int sparkmv_plan_add_kquant(void * plan, int kind, const void * blocks, int rows, int cols, const void * x,
+                            int x_dtype, int ldx, int ncols, float * y, int ldy, int accumulate);
+int sparkmv_plan_run(void * plan, void * stream);
+/* Capture on a created (non-null) stream; run the plan eagerly once first. */
+int sparkmv_plan_capture(void * plan, void * stream);
+int sparkmv_plan_launch(void * plan, void * stream);
+/* Average device milliseconds of each op over `iters` eager runs, timed with
+ * events on `stream`; op_ms receives sparkmv_plan_size(plan) values. */
+int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms);
+
+/* ---- synthetic workloads (host memory; no reference counterpart) ----
+ * A named, seeded generator so every test and benchmark can rebuild the same
+ * inputs: xoshiro256** seeded through splitmix64; normals by Box-Muller in
+ * f64, rounded to nearest-even. */
+size_t sparkmv_synth_container_bytes(int rows, int cols, int dim, int nc, int nstages, int v3);
+/* An RQVQ container: per stage a codebook ~N(0, 0.02) in fp16, gains
+ * ~U(0.5, 1.5) in fp16, indices uniform in [0, nc). */
+int sparkmv_synth_vq_container(uint64_t seed, int rows, int cols, int dim, int nc, int nstages, int v3,
+                               void * out, size_t len);
+/* Q6_K blocks: ql, qh uniform bytes, scales uniform in [-32, 31], d ~U(1e-4, 1e-3). */
+int sparkmv_synth_q6k(uint64_t seed, int rows, int cols, void * out);
+/* Q8_0 blocks: qs uniform in [-128, 127], d ~U(1e-4, 1e-3). */
+int sparkmv_synth_q8_0(uint64_t seed, int rows, int cols, void * out);
+/* n bf16 values ~N(0, 1). */
+int sparkmv_synth_bf16_normal(uint64_t seed, size_t n, uint16_t * out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,372 @@
+/* abi.cpp — the extern "C" surface declared in include/sparkmv.h.
+ *
+ * The vqg_* functions keep the reference's C-ABI (tools/vq/gpu/decode-gpu.cu:765-1140):
+ * one stage payload per call, f32 x and y, y accumulates, the default stream,
+ * 0 / -1 returns with the message in vqg_decode_error(). They route to the
+ * same kernels as the sparkmv_* functions, which add bf16 x, N columns, whole
+ * containers, several matrices per launch and explicit streams.
+ */
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/sparkmv.h"
+#include "common.h"
+#include "host/vq_format.hpp"
+#include "kq.h"
+#include "prefill.h"
+#include "vq.h"
+
+namespace sparkmv {
+
+static char g_err[512];
+
+void set_error(const char * fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+int fail_hip(const char * what, hipError_t e) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return -1;
+}
+
+int cu_count() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+static int width_ok(int v3, int nc) {
+    if (v3 && bits_for(nc) > 13) {
+        set_error("DQV3 carries 13 index bits, nc %d needs %d", nc, bits_for(nc));
+        return 0;
+    }
+    return 1;
+}
+
+static int geometry_ok(int dim, int nc, int rows, int cols) {
+    if (dim <= 0 || nc <= 0 || rows <= 0 || cols <= 0 || cols % dim) {
+        set_error("geometry dim %d, nc %d, %d x %d is inconsistent", dim, nc, rows, cols);
+        return 0;
+    }
+    return 1;
+}
+
+/* Time `iters` runs of `launch` on the default stream with events; best ms. */
+template <class F>
+static int timed(F launch, int iters, double * ms) {
+    hipEvent_t a, b;
+    hipError_t e;
+    if ((e = hipEventCreate(&a)) != hipSuccess) return fail_hip("event create", e);
+    if ((e = hipEventCreate(&b)) != hipSuccess) { hipEventDestroy(a); return fail_hip("event create", e); }
+    float best = 1e30f;
+    int rc = 0;
+    for (int it = 0; it < (iters > 0 ? iters : 1); it++) {
+        hipEventRecord(a, 0);
+        if (launch()) { rc = -1; break; }
+        hipEventRecord(b, 0);
+        if ((e = hipEventSynchronize(b)) != hipSuccess) { rc = fail_hip("timed launch", e); break; }
+        float t = 0;
+        hipEventElapsedTime(&t, a, b);
+        if (t < best) best = t;
+    }
+    hipEventDestroy(a);
+    hipEventDestroy(b);
+    if (!rc && ms) *ms = best;
+    return rc;
+}
+
+static int one_stage_gemv(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x,
+                          float * y, int variant, int threads) {
+    if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
+    if (variant < 0 || variant > 3) { set_error("unknown gemv variant %d", variant); return -1; }
+    if (!payload) { set_error("payload is null"); return -1; }
+    VqMatDesc m;
+    memset(&m, 0, sizeof m);
+    m.stages[0] = payload;
+    m.y = y;
+    m.rows = rows;
+    VqCall c;
+    memset(&c, 0, sizeof c);
+    c.dim = dim; c.nc = nc; c.cols = cols; c.v3 = v3; c.nst = 1;
+    c.mats = &m; c.nmat = 1;
+    c.x = x; c.ldx = cols; c.xf32 = 1; c.ncol = 1; c.ldy = rows; c.accumulate = 1;
+    c.stream = 0;
+    c.variant = variant;
+    c.threads = threads;
+    return vq_launch(c);
+}
+
+}  // namespace sparkmv
+
+using namespace sparkmv;
+
+extern "C" {
+
+const char * vqg_decode_error(void) { return g_err; }
+
+int vqg_device_name(char * out, int n) {
+    if (!out || n <= 0) { set_error("device name buffer is empty"); return -1; }
+    hipDeviceProp_t p;
+    memset(&p, 0, sizeof p);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) return fail_hip("device properties", e);
+    snprintf(out, (size_t) n, "%s (%s)", p.name, p.gcnArchName);
+    return 0;
+}
+
+int vqg_driver_version(void) {
+    int v = 0;
+    if (hipDriverGetVersion(&v) != hipSuccess) return -1;
+    return v;
+}
+
+int vqg_gemv_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
+    return vq_variant_ready(dim, nc, rows, cols, v3, variant);
+}
+
+int vqg_gemv_t(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x, float * y,
+               int variant, int threads, int iters, double * ms) {
+    if (!width_ok(v3, nc)) return -1;
+    if (rows <= 0 || cols <= 0) { set_error("gemv needs a non-empty matrix"); return -1; }
+    return timed([&] { return one_stage_gemv(payload, dim, nc, rows, cols, v3, x, y, variant, threads); }, iters, ms);
+}
+
+int vqg_gemv(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x, float * y,
+             int variant, int iters, double * ms) {
+    return vqg_gemv_t(payload, dim, nc, rows, cols, v3, x, y, variant, 0, iters, ms);
+}
+
+int vqg_gemv_launch_t(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x, float * y,
+                      int variant, int threads) {
+    if (!width_ok(v3, nc)) return -1;
+    if (rows <= 0 || cols <= 0) { set_error("gemv needs a non-empty matrix"); return -1; }
+    return one_stage_gemv(payload, dim, nc, rows, cols, v3, x, y, variant, threads);
+}
+
+int vqg_gemv_launch(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x, float * y,
+                    int variant) {
+    return vqg_gemv_launch_t(payload, dim, nc, rows, cols, v3, x, y, variant, 0);
+}
+
+int vqg_dequant(const void * payload, int dim, int nc, int rows, int cols, int v3, float * out, int iters,
+                double * ms) {
+    if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
+    if (!payload || !out) { set_error("null pointer passed to dequant"); return -1; }
+    const Layout L = make_layout(dim, nc, rows, cols, v3);
+    return timed([&] { return vq_dequant_launch(payload, L, out, 1, 0); }, iters, ms);
+}
+
+int vqg_row_dequant(const void * payload, int dim, int nc, int rows, int cols, int v3, int row, float * out) {
+    if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
+    if (row < 0 || row >= rows) { set_error("row %d is outside %d", row, rows); return -1; }
+    if (!payload || !out) { set_error("null pointer passed to row dequant"); return -1; }
+    return vq_row_dequant_launch(payload, make_layout(dim, nc, rows, cols, v3), row, out, 0);
+}
+
+/* ---- prefill (reference layout: xT [cols][ntok], y [ntok][rows]) ---- */
+
+struct PreCfg { int bn, bk; };
+static const PreCfg k_pre_cfg[] = { { 64, 64 }, { 128, 64 } };
+static const int k_pre_ncfg = (int) (sizeof k_pre_cfg / sizeof k_pre_cfg[0]);
+
+int vqg_prefill_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
+    if (dim <= 0 || nc <= 0 || rows <= 0 || cols <= 0 || cols % dim) return 0;
+    if (v3 && bits_for(nc) > 13) return 0;
+    const Layout L = make_layout(dim, nc, rows, cols, v3);
+    switch (variant) {
+        case 0: return 1;
+        case 3: return L.nidx_row * 2 <= 64 * 1024;
+        default: return 0;
+    }
+}
+
+int vqg_prefill_cfg_count(void) { return k_pre_ncfg; }
+
+int vqg_prefill_cfg(int idx, int * bn, int * bk) {
+    if (idx < 0 || idx >= k_pre_ncfg || !bn || !bk) return -1;
+    *bn = k_pre_cfg[idx].bn;
+    *bk = k_pre_cfg[idx].bk;
+    return 0;
+}
+
+int vqg_prefill_cfg_ready(int dim, int nc, int rows, int cols, int v3, int bn, int bk, int variant) {
+    (void) bn; (void) bk;
+    if (variant == 3) return vqg_prefill_ready(dim, nc, rows, cols, v3, 3);
+    return 0;
+}
+
+static int prefill_ref_layout(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * xT,
+                              int ntok, float * y, int variant) {
+    if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
+    if (ntok <= 0) { set_error("prefill needs at least one token"); return -1; }
+    if (!payload || !xT || !y) { set_error("null pointer passed to prefill"); return -1; }
+    if (variant == 0) variant = 3;
+    if (variant != 3) { set_error("prefill variant %d does not take this geometry", variant); return -1; }
+    const Layout L = make_layout(dim, nc, rows, cols, v3);
+    const void * st[1] = { payload };
+    return prefill_simple_launch(st, 1, L, xT, 1, 1, (size_t) ntok, ntok, y, rows, 1, 0);
+}
+
+int vqg_prefill(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * xT, int ntok,
+                float * y, int iters, double * ms, int variant) {
+    return timed([&] { return prefill_ref_layout(payload, dim, nc, rows, cols, v3, xT, ntok, y, variant); }, iters, ms);
+}
+
+int vqg_prefill_tile(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * xT, int ntok,
+                     float * y, int iters, double * ms, int bn, int bk, int variant) {
+    if (!vqg_prefill_cfg_ready(dim, nc, rows, cols, v3, bn, bk, variant)) {
+        set_error("tile %dx%d with variant %d does not fit this geometry", bn, bk, variant);
+        return -1;
+    }
+    return vqg_prefill(payload, dim, nc, rows, cols, v3, xT, ntok, y, iters, ms, variant);
+}
+
+int vqg_prefill_launch(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * xT, int ntok,
+                       float * y, int variant) {
+    return prefill_ref_layout(payload, dim, nc, rows, cols, v3, xT, ntok, y, variant);
+}
+
+int vqg_prefill_launch_tile(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * xT,
+                            int ntok, float * y, int bn, int bk, int variant) {
+    if (!vqg_prefill_cfg_ready(dim, nc, rows, cols, v3, bn, bk, variant)) {
+        set_error("tile %dx%d with variant %d does not fit this geometry", bn, bk, variant);
+        return -1;
+    }
+    return prefill_ref_layout(payload, dim, nc, rows, cols, v3, xT, ntok, y, variant);
+}
+
+int vqg_gemv_f32(const float * w, const float * x, float * y, int rows, int cols, int iters, double * ms) {
+    if (!w || !x || !y || rows <= 0 || cols <= 0) { set_error("gemv f32 needs a non-empty matrix and pointers"); return -1; }
+    return timed([&] { return f32_gemv_launch(w, x, y, rows, cols, 0); }, iters, ms);
+}
+
+/* ------------------------------ sparkmv_* --------------------------------- */
+
+int sparkmv_container_open(const void * bytes, size_t len, sparkmv_container_info * info) {
+    if (!bytes || !info) { set_error("null pointer passed to container open"); return -1; }
+    fmt::ContainerView c;
+    std::string err;
+    if (!fmt::open_container((const uint8_t *) bytes, len, c, err)) {
+        set_error("%s", err.c_str());
+        return -1;
+    }
+    if (c.stages.size() > 4) { set_error("%zu stages: at most 4 are supported", c.stages.size()); return -1; }
+    memset(info, 0, sizeof *info);
+    info->dim = c.dim; info->nc = c.nc; info->nstages = (int) c.stages.size();
+    info->rows = c.rows; info->cols = c.cols; info->v3 = c.v3; info->nbit = c.nbit;
+    info->payload_bytes = c.payload;
+    info->stage_bytes = c.stride;
+    for (size_t s = 0; s < c.stages.size(); s++) info->stage_offset[s] = 32 + s * c.stride;
+    return 0;
+}
+
+size_t sparkmv_stage_bytes(int v3, int rows, int cols, int dim, int nc) {
+    if (dim <= 0 || nc <= 0 || rows <= 0 || cols <= 0 || cols % dim) return 0;
+    return make_layout(dim, nc, rows, cols, v3).bytes;
+}
+
+int sparkmv_vq_gemv_multi(const sparkmv_vq_matrix * mats, int nmat, int nstages, int dim, int nc, int cols, int v3,
+                          const void * x, int x_dtype, int ldx, int ncols, int ldy, int accumulate, int variant,
+                          void * stream) {
+    if (!mats || nmat < 1 || nmat > kMaxMats) { set_error("matrix count %d is outside 1..%d", nmat, kMaxMats); return -1; }
+    if (x_dtype != SPARKMV_X_BF16 && x_dtype != SPARKMV_X_F32) { set_error("unknown x dtype %d", x_dtype); return -1; }
+    if (nstages < 1 || nstages > kMaxStages) { set_error("stage count %d is outside 1..%d", nstages, kMaxStages); return -1; }
+    VqMatDesc m[kMaxMats];
+    memset(m, 0, sizeof m);
+    for (int i = 0; i < nmat; i++) {
+        for (int s = 0; s < nstages; s++) m[i].stages[s] = mats[i].stages[s];
+        m[i].y = mats[i].y;
+        m[i].rows = mats[i].rows;
+        if (!geometry_ok(dim, nc, mats[i].rows, cols)) return -1;
+    }
+    VqCall c;
+    memset(&c, 0, sizeof c);
+    c.dim = dim; c.nc = nc; c.cols = cols; c.v3 = v3; c.nst = nstages;
+    c.mats = m; c.nmat = nmat;
+    c.x = x; c.ldx = ldx; c.xf32 = x_dtype == SPARKMV_X_F32; c.ncol = ncols; c.ldy = ldy;
+    c.accumulate = accumulate ? 1 : 0;
+    c.stream = (hipStream_t) stream;
+    c.variant = variant;
+    return vq_launch(c);
+}
+
+int sparkmv_vq_gemv(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                    const void * x, int x_dtype, int ldx, int ncols, float * y, int ldy, int accumulate, int variant,
+                    void * stream) {
+    if (!stages) { set_error("stage pointer array is null"); return -1; }
+    if (nstages < 1 || nstages > kMaxStages) { set_error("stage count %d is outside 1..%d", nstages, kMaxStages); return -1; }
+    sparkmv_vq_matrix m;
+    memset(&m, 0, sizeof m);
+    for (int s = 0; s < nstages; s++) m.stages[s] = stages[s];
+    m.y = y;
+    m.rows = rows;
+    return sparkmv_vq_gemv_multi(&m, 1, nstages, dim, nc, cols, v3, x, x_dtype, ldx, ncols, ldy, accumulate, variant,
+                                 stream);
+}
+
+int sparkmv_vq_dequant(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                       float * out, int accumulate, void * stream) {
+    if (!stages || !out) { set_error("null pointer passed to dequant"); return -1; }
+    if (nstages < 1 || nstages > kMaxStages) { set_error("stage count %d is outside 1..%d", nstages, kMaxStages); return -1; }
+    if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
+    hipStream_t s = (hipStream_t) stream;
+    const Layout L = make_layout(dim, nc, rows, cols, v3);
+    for (int i = 0; i < nstages; i++)
+        if (!stages[i]) { set_error("stage %d payload is null", i); return -1; }
+    for (int i = 0; i < nstages; i++)
+        if (vq_dequant_launch(stages[i], L, out, i > 0 || accumulate, s)) return -1;
+    return 0;
+}
+
+int sparkmv_q6k_gemv(const void * blocks, int rows, int cols, const void * x, int x_dtype, int ldx, int ncols,
+                     float * y, int ldy, int accumulate, void * stream) {
+    if (x_dtype != SPARKMV_X_BF16 && x_dtype != SPARKMV_X_F32) { set_error("unknown x dtype %d", x_dtype); return -1; }
+    return kq_gemv_launch(6, blocks, rows, cols, x, x_dtype == SPARKMV_X_F32, ldx, ncols, y, ldy, accumulate ? 1 : 0,
+                          (hipStream_t) stream);
+}
+
+int sparkmv_q8_0_gemv(const void * blocks, int rows, int cols, const void * x, int x_dtype, int ldx, int ncols,
+                      float * y, int ldy, int accumulate, void * stream) {
+    if (x_dtype != SPARKMV_X_BF16 && x_dtype != SPARKMV_X_F32) { set_error("unknown x dtype %d", x_dtype); return -1; }
+    return kq_gemv_launch(8, blocks, rows, cols, x, x_dtype == SPARKMV_X_F32, ldx, ncols, y, ldy, accumulate ? 1 : 0,
+                          (hipStream_t) stream);
+}
+
+int sparkmv_q6k_dequant(const void * blocks, int rows, int cols, float * out, void * stream) {
+    return kq_dequant_launch(6, blocks, rows, cols, out, (hipStream_t) stream);
+}
+
+int sparkmv_q8_0_dequant(const void * blocks, int rows, int cols, float * out, void * stream) {
+    return kq_dequant_launch(8, blocks, rows, cols, out, (hipStream_t) stream);
+}
+
+int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                       const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy, int accumulate,
+                       void * stream) {
+    if (!stages || !x || !y) { set_error("null pointer passed to prefill"); return -1; }
+    if (x_dtype != SPARKMV_X_BF16 && x_dtype != SPARKMV_X_F32) { set_error("unknown x dtype %d", x_dtype); return -1; }
+    if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
+    if (ldx < cols || ldy < rows) { set_error("ldx/ldy below the matrix extent"); return -1; }
+    for (int i = 0; i < nstages && i < kMaxStages; i++)
+        if (!stages[i]) { set_error("stage %d payload is null", i); return -1; }
+    const Layout L = make_layout(dim, nc, rows, cols, v3);
+    return prefill_simple_launch(stages, nstages, L, x, x_dtype == SPARKMV_X_F32, (size_t) ldx, 1, ntok, y, ldy,
+                                 accumulate ? 1 : 0, (hipStream_t) stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+/* vq.h — host-side launchers of the VQ kernels (vq_kernels.hip). */
+#pragma once
+
+#include "common.h"
+
+namespace sparkmv {
+
+/* One matrix of a VQ launch: a device pointer per residual stage payload and
+ * its output, y[n * ldy + r] for column n. */
+struct VqMatDesc {
+    const void * stages[kMaxStages];
+    float * y;
+    int rows;
+};
+
+constexpr int kMaxMats = 8;   /* matrices one launch may share an x between */
+
+/* A fused VQ GEMV call: every matrix shares dim, nc, cols, format, stage count
+ * and the activations x[n * ldx + c] (bf16 bits, or f32 when xf32), n < ncol.
+ * accumulate = 1 adds into y (the reference's convention); 0 overwrites. */
+struct VqCall {
+    int dim, nc, cols, v3, nst;
+    const VqMatDesc * mats;
+    int nmat;
+    const void * x;
+    int ldx, xf32, ncol, ldy, accumulate;
+    hipStream_t stream;
+    int variant;   /* 0 auto, 1 generic, 2 LDS-codebook wave kernel, 3 MFMA block kernel */
+    int threads;   /* workgroup width, a multiple of 64; 0 = the default */
+    int grid;      /* workgroups; 0 = the default */
+};
+
+/* Whether a kernel variant runs this geometry (same numbering as VqCall). */
+int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant);
+/* Validate and launch; returns 0, or -1 with the message set. */
+int vq_launch(const VqCall & c);
+
+/* Decode one stage into out (row-major rows x cols f32); accumulate 0 writes
+ * the stage's values as if adding into zeros. */
+int vq_dequant_launch(const void * payload, const Layout & L, float * out, int accumulate, hipStream_t s);
+/* Decode one row of one stage into out (cols f32), accumulating. */
+int vq_row_dequant_launch(const void * payload, const Layout & L, int row, float * out, hipStream_t s);
+/* y[r] += dot(W row r, x): the plain f32 bandwidth yardstick. */
+int f32_gemv_launch(const float * w, const float * x, float * y, int rows, int cols, hipStream_t s);
+
+}  // namespace sparkmv

@@ -1,0 +1,132 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol the header
+declares, and its host-side code (container validation, synthetic packing)
+agrees with the oracle. No GPU call is made here."""
+import ctypes
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, ROOT
+
+HEADER = os.path.join(ROOT, "include", "sparkmv.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b((?:vqg|sparkmv)_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_reference_abi():
+    names = declared_functions()
+    for ref_name in ["vqg_decode_error", "vqg_device_name", "vqg_driver_version", "vqg_gemv_ready", "vqg_gemv_t",
+                     "vqg_gemv", "vqg_gemv_launch_t", "vqg_gemv_launch", "vqg_dequant", "vqg_row_dequant",
+                     "vqg_prefill_ready", "vqg_prefill_cfg_count", "vqg_prefill_cfg", "vqg_prefill_cfg_ready",
+                     "vqg_prefill", "vqg_prefill_tile", "vqg_prefill_launch", "vqg_prefill_launch_tile",
+                     "vqg_gemv_f32"]:
+        assert ref_name in names
+
+
+def test_library_exports_every_declared_symbol(sm):
+    L = ctypes.CDLL(sm.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_every_declared_symbol(sm):
+    assert set(declared_functions()) <= set(sm.SIGNATURES)
+
+
+def test_readiness_rules(sm):
+    L = sm.lib()
+    assert L.vqg_gemv_ready(4, 4096, 10240, 2560, 1, 3) == 1
+    assert L.vqg_gemv_ready(4, 8192, 16, 2560, 1, 3) == 1
+    assert L.vqg_gemv_ready(4, 1024, 64, 2560, 1, 3) == 0      # 10-bit stream: not the block kernel
+    assert L.vqg_gemv_ready(8, 4096, 64, 2560, 1, 3) == 0      # dim 8
+    assert L.vqg_gemv_ready(4, 4096, 64, 2500, 1, 3) == 0      # 625 indices per row, not whole 32-index steps
+    assert L.vqg_gemv_ready(4, 4096, 64, 2560, 0, 3) == 0      # DQVQ
+    assert L.vqg_gemv_ready(4, 16384, 64, 2560, 1, 1) == 0     # DQV3 is at most 13 bits
+    assert L.vqg_gemv_ready(4, 16384, 64, 2560, 0, 1) == 1     # DQVQ has no such limit
+    for v in (0, 1, 2):
+        assert L.vqg_gemv_ready(4, 4096, 37, 12, 1, v) == 1
+    assert L.vqg_gemv_ready(4, 4096, 1, 10, 1, 0) == 0         # cols not a multiple of dim
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))))
+def test_container_open_agrees_with_oracle(sm, ref, path):
+    with np.load(path, allow_pickle=False) as z:
+        data = z["container"]
+        seed, rows, cols, dim, nc, ns, v3 = [int(v) for v in z["geometry"]]
+    c = sm.Container(data)
+    assert (c.rows, c.cols, c.dim, c.nc, c.nstages, c.v3) == (rows, cols, dim, nc, ns, v3)
+    ok, msg, info = ref.container_check(data)
+    assert ok and info["stride"] == c.stage_bytes
+    variants = [data[:-1], np.concatenate([data, np.zeros(1, np.uint8)])]
+    e = data.copy(); e[24] ^= 1; variants.append(e)
+    f = data.copy(); f[36:38] = np.frombuffer(np.uint16(2 * dim).tobytes(), np.uint8); variants.append(f)
+    g = data.copy(); g[0] = 0; variants.append(g)
+    h = data.copy(); h[4:6] = 0; variants.append(h)
+    i = data.copy(); i[6:8] = np.frombuffer(np.uint16(16384).tobytes(), np.uint8)
+    i[38:40] = np.frombuffer(np.uint16(16384).tobytes(), np.uint8); variants.append(i)
+    for v in variants:
+        ok, msg, _ = ref.container_check(v)
+        with pytest.raises(sm.SparkmvError) as exc:
+            sm.Container(v)
+        if not ok:
+            assert msg in str(exc.value)
+        else:  # pragma: no cover - every variant above is refused
+            pytest.fail("oracle accepted a damaged container")
+
+
+@pytest.mark.parametrize("rows,cols,dim,nc,ns,v3", [(7, 64, 4, 4096, 2, 1), (3, 40, 4, 8192, 1, 1),
+                                                    (5, 36, 4, 1024, 1, 1), (4, 48, 8, 300, 2, 1),
+                                                    (6, 20, 4, 256, 1, 0), (3, 24, 4, 600, 2, 0),
+                                                    (2, 4, 4, 4096, 1, 1)])
+def test_synth_packing_matches_reference_writer(sm, ref, rows, cols, dim, nc, ns, v3):
+    """The product's seeded writer lays indices out exactly as the reference's
+    writers (build-vq-gpu.c:71-111 / vq_qc.h:241-264, restated in the oracle)."""
+    data = sm.synth_container(1234 + rows, rows, cols, dim, nc, ns, v3)
+    ok, msg, info = ref.container_check(data)
+    assert ok, msg
+    stride = info["stride"]
+    for s in range(ns):
+        payload = data[32 + s * stride:32 + (s + 1) * stride]
+        idx = ref.stage_indices(payload)
+        assert idx.max() < nc
+        hdr = 24 if v3 else 16
+        cb = payload[hdr:hdr + nc * dim * 2].view(np.uint16)
+        gains = payload[hdr + nc * dim * 2:hdr + nc * dim * 2 + rows * 2].view(np.uint16)
+        again = ref.pack(v3, cb, idx.ravel(), gains, rows, cols, dim, nc)
+        assert np.array_equal(again, payload)
+
+
+def test_synth_distributions(sm):
+    data = sm.synth_container(7, 512, 256, 4, 4096, 1, 1)
+    cb = data[32 + 24:32 + 24 + 4096 * 8].view(np.float16).astype(np.float64)
+    assert abs(cb.std() - 0.02) < 0.001 and abs(cb.mean()) < 0.001
+    g = data[32 + 24 + 4096 * 8:32 + 24 + 4096 * 8 + 1024].view(np.float16).astype(np.float64)
+    assert g.min() >= 0.5 and g.max() <= 1.5 and abs(g.mean() - 1.0) < 0.05
+    x = sm.bf16_to_f32(sm.synth_bf16(3, 100000))
+    assert abs(x.mean()) < 0.02 and abs(x.std() - 1.0) < 0.02
+    q8 = sm.synth_q8_0(5, 64, 256)
+    d = np.concatenate([q8[i * 34:i * 34 + 2] for i in range(64 * 8)]).view(np.float16).astype(np.float64)
+    assert d.min() >= 1e-4 and d.max() <= 1e-3
+    q6 = sm.synth_q6k(5, 16, 512)
+    sc = np.concatenate([q6[i * 210 + 192:i * 210 + 208] for i in range(32)]).view(np.int8)
+    assert sc.min() >= -32 and sc.max() <= 31
+
+
+def test_synth_is_deterministic(sm):
+    a = sm.synth_container(42, 33, 128, 4, 4096, 2, 1)
+    b = sm.synth_container(42, 33, 128, 4, 4096, 2, 1)
+    c = sm.synth_container(43, 33, 128, 4, 4096, 2, 1)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+
+
+def test_stage_bytes_agree(sm, ref):
+    for args in [(1, 10240, 2560, 4, 4096), (1, 16, 2560, 4, 8192), (0, 3, 16, 4, 512), (1, 5, 12, 4, 1024)]:
+        assert sm.lib().sparkmv_stage_bytes(*args) == ref.stage_bytes(*args)

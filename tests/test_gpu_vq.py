@@ -1,0 +1,250 @@
+"""GPU parity of the VQ path through the C-ABI against the oracle.
+
+Tolerances: decoded weights bit-exact; GEMV outputs within 1e-3 relative L2
+of the f64 matvec of the oracle's decoded matrix (the stated bar). The MFMA
+path's products are exact, so the tests also hold it to 1e-5 to catch
+regressions long before the bar.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+BAR = 1e-3
+TIGHT = 1e-5
+
+
+def rel_l2(got, want):
+    want = np.asarray(want, np.float64)
+    return float(np.linalg.norm(np.asarray(got, np.float64) - want) / max(np.linalg.norm(want), 1e-300))
+
+
+def _x(sm, seed, ncol, cols, f32):
+    import torch
+    xb = sm.synth_bf16(seed, ncol * cols).reshape(ncol, cols)
+    xf = sm.bf16_to_f32(xb).reshape(ncol, cols)
+    if f32:   # an f32 activation that is not bf16-representable
+        xf = (xf * np.float32(1.0 + 2.0 ** -12)).astype(np.float32)
+        return torch.from_numpy(xf.copy()).cuda(), xf
+    return torch.from_numpy(xb.view(np.int16).copy()).cuda(), xf
+
+
+GEOMS = [
+    # rows, cols, dim, nc, stages, v3
+    (64, 256, 4, 4096, 2, 1),
+    (37, 256, 4, 4096, 2, 1),
+    (16, 2560, 4, 4096, 2, 1),
+    (100, 384, 4, 8192, 2, 1),
+    (48, 192, 4, 1024, 2, 1),
+    (24, 64, 4, 256, 2, 0),
+    (16, 128, 8, 4096, 1, 1),
+    (5, 12, 4, 4096, 2, 1),
+    (40, 128, 4, 3000, 1, 1),
+]
+
+
+@pytest.mark.parametrize("geom", GEOMS, ids=[f"{g[0]}x{g[1]}_d{g[2]}_nc{g[3]}_s{g[4]}_v{g[5]}" for g in GEOMS])
+@pytest.mark.parametrize("f32", [False, True], ids=["bf16x", "f32x"])
+def test_gemv_all_variants(sm, ref, dev, geom, f32):
+    import torch
+    rows, cols, dim, nc, ns, v3 = geom
+    data = sm.synth_container(rows * 7 + cols, rows, cols, dim, nc, ns, v3)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    for ncol in (1, 3, 8):
+        xt, xf = _x(sm, 5 + ncol, ncol, cols, f32)
+        want = xf.astype(np.float64) @ W.T          # [ncol, rows]
+        for variant in (0, 1, 2, 3):
+            if not sm.lib().vqg_gemv_ready(dim, nc, rows, cols, v3, variant):
+                continue
+            y = torch.full((ncol, rows), float("nan"), device=dev)
+            dc.gemv(xt, y, ncols=ncol, accumulate=False, variant=variant)
+            got = y.cpu().numpy()
+            err = rel_l2(got, want)
+            print(f"rows {rows} cols {cols} nc {nc} ncol {ncol} variant {variant} f32 {f32}: relL2 {err:.2e}")
+            assert err <= BAR
+            assert err <= TIGHT
+
+
+def test_accumulate_adds_into_y(sm, ref, dev):
+    import torch
+    rows, cols = 96, 512
+    data = sm.synth_container(3, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    xt, xf = _x(sm, 8, 1, cols, False)
+    y0 = np.random.default_rng(0).standard_normal((1, rows)).astype(np.float32)
+    y = torch.from_numpy(y0.copy()).to(dev)
+    dc.gemv(xt, y, accumulate=True)
+    want = y0.astype(np.float64) + xf.astype(np.float64) @ W.T
+    assert rel_l2(y.cpu().numpy(), want) <= TIGHT
+
+
+def test_batched_columns_equal_single_columns(sm, dev):
+    """Decode-once N=8 gives each column what an N=1 call gives it."""
+    import torch
+    rows, cols = 256, 2560
+    dc = sm.DeviceContainer(sm.synth_container(21, rows, cols))
+    xt, _ = _x(sm, 9, 8, cols, False)
+    y8 = torch.zeros(8, rows, device=dev)
+    dc.gemv(xt, y8, ncols=8)
+    for n in range(8):
+        y1 = torch.zeros(1, rows, device=dev)
+        dc.gemv(xt[n:n + 1], y1, ncols=1)
+        a, b = y8[n].cpu().numpy(), y1[0].cpu().numpy()
+        assert rel_l2(a, b) <= 1e-6, n
+
+
+def test_reference_abi_per_stage(sm, ref, dev):
+    """vqg_gemv_launch per stage payload, f32 x, y accumulating across stages:
+    the reference runtime's calling pattern (vq-model-gpu.cu:651-660)."""
+    import torch
+    rows, cols = 80, 640
+    data = sm.synth_container(31, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    x = np.sin(np.arange(cols, dtype=np.float32) * 0.001).astype(np.float32)   # the reference gate's x
+    xd = torch.from_numpy(x).to(dev)
+    L = sm.lib()
+    for variant in (0, 1, 2, 3):
+        y = torch.zeros(rows, device=dev)
+        for p in dc.stage_ptrs:
+            sm.check(L.vqg_gemv_launch(p, 4, 4096, rows, cols, 1, xd.data_ptr(), y.data_ptr(), variant), "launch")
+        torch.cuda.synchronize()
+        assert rel_l2(y.cpu().numpy(), W @ x.astype(np.float64)) <= TIGHT
+        ms = ctypes.c_double()
+        y.zero_()
+        sm.check(L.vqg_gemv_t(dc.stage_ptrs[0], 4, 4096, rows, cols, 1, xd.data_ptr(), y.data_ptr(), variant, 128, 3,
+                              ctypes.byref(ms)), "timed")
+        assert ms.value > 0
+
+
+def test_reference_abi_errors(sm, dev):
+    import torch
+    L = sm.lib()
+    dc = sm.DeviceContainer(sm.synth_container(2, 32, 128))
+    x = torch.zeros(128, device=dev)
+    y = torch.zeros(32, device=dev)
+    p = dc.stage_ptrs[0]
+    assert L.vqg_gemv_launch(p, 4, 16384, 32, 128, 1, x.data_ptr(), y.data_ptr(), 0) == -1
+    assert "13 index bits" in sm.last_error()
+    assert L.vqg_gemv_launch(p, 4, 4096, 0, 128, 1, x.data_ptr(), y.data_ptr(), 0) == -1
+    assert L.vqg_gemv_launch(p, 4, 4096, 32, 128, 1, x.data_ptr(), y.data_ptr(), 9) == -1
+    assert L.vqg_gemv_launch_t(p, 4, 4096, 32, 128, 1, x.data_ptr(), y.data_ptr(), 3, 96) == -1
+    assert "multiple of 64" in sm.last_error()
+    assert L.vqg_gemv_launch(p, 4, 1024, 32, 128, 1, x.data_ptr(), y.data_ptr(), 3) == -1
+    assert L.vqg_row_dequant(p, 4, 4096, 32, 128, 1, 32, y.data_ptr()) == -1
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("geom", GEOMS, ids=[f"{g[0]}x{g[1]}_d{g[2]}_nc{g[3]}_s{g[4]}_v{g[5]}" for g in GEOMS])
+def test_dequant_bit_exact(sm, ref, dev, geom):
+    import torch
+    rows, cols, dim, nc, ns, v3 = geom
+    data = sm.synth_container(rows + 11 * cols, rows, cols, dim, nc, ns, v3)
+    want = ref.decode(data)
+    dc = sm.DeviceContainer(data)
+    out = torch.full((rows, cols), float("nan"), device=dev)
+    dc.dequant(out, accumulate=False)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the reference entry points: stage by stage into zeros, and single rows
+    L = sm.lib()
+    out.zero_()
+    ms = ctypes.c_double()
+    for p in dc.stage_ptrs:
+        sm.check(L.vqg_dequant(p, dim, nc, rows, cols, v3, out.data_ptr(), 1, ctypes.byref(ms)), "vqg_dequant")
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    row = torch.zeros(cols, device=dev)
+    r = rows // 2
+    for p in dc.stage_ptrs:
+        sm.check(L.vqg_row_dequant(p, dim, nc, rows, cols, v3, r, row.data_ptr()), "row dequant")
+    torch.cuda.synchronize()
+    assert np.array_equal(row.cpu().numpy().view(np.uint32), want[r].view(np.uint32))
+
+
+def test_golden_fixtures_on_gpu(sm, dev):
+    """The reference decoder's own dumps, reproduced by the GPU dequant."""
+    import glob
+    import os
+    import torch
+    from conftest import GOLDEN
+    for path in sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))):
+        with np.load(path, allow_pickle=False) as z:
+            data, want = z["container"], z["decoded"]
+        dc = sm.DeviceContainer(data)
+        out = torch.zeros(want.shape, device=dev)
+        dc.dequant(out)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), path
+
+
+def test_multi_matrix_launch(sm, ref, dev):
+    """q, k, v and the head gate of one layer (scaled down) in one launch,
+    with one and with two activation columns (one ldy for every matrix)."""
+    import torch
+    cols = 512
+    shapes = [256, 64, 64, 16]
+    datas = [sm.synth_container(100 + i, r, cols) for i, r in enumerate(shapes)]
+    mats = [sm.DeviceContainer(d) for d in datas]
+    Ws = [ref.decode(d).astype(np.float64) for d in datas]
+    for ncol in (1, 2):
+        xt, xf = _x(sm, 4 + ncol, ncol, cols, False)
+        ys = [torch.full((ncol, max(shapes)), float("nan"), device=dev) for _ in shapes]
+        sm.gemv_multi(mats, xt, ys, ncols=ncol)
+        torch.cuda.synchronize()
+        for W, y, r in zip(Ws, ys, shapes):
+            got = y[:, :r].cpu().numpy()
+            assert rel_l2(got, xf.astype(np.float64) @ W.T) <= TIGHT
+
+
+@pytest.mark.parametrize("ntok", [1, 37, 130])
+def test_prefill_token_major(sm, ref, dev, ntok):
+    import torch
+    rows, cols = 64, 256
+    data = sm.synth_container(55, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    xt, xf = _x(sm, 12, ntok, cols, False)
+    y = torch.full((ntok, rows), float("nan"), device=dev)
+    dc.prefill(xt, y)
+    assert rel_l2(y.cpu().numpy(), xf.astype(np.float64) @ W.T) <= BAR
+
+
+def test_prefill_reference_layout(sm, ref, dev):
+    import torch
+    rows, cols, ntok = 48, 128, 20
+    data = sm.synth_container(56, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    x = np.random.default_rng(1).standard_normal((ntok, cols)).astype(np.float32)
+    xT = torch.from_numpy(np.ascontiguousarray(x.T)).to(dev)
+    y = torch.zeros(ntok, rows, device=dev)
+    L = sm.lib()
+    for p in dc.stage_ptrs:
+        sm.check(L.vqg_prefill_launch(p, 4, 4096, rows, cols, 1, xT.data_ptr(), ntok, y.data_ptr(), 0), "prefill")
+    torch.cuda.synchronize()
+    assert rel_l2(y.cpu().numpy(), x.astype(np.float64) @ W.T) <= BAR
+
+
+def test_full_size_ffn_up(sm, ref, dev):
+    """10240 x 2560, dim 4, nc 4096, 2 stages, bf16 x: the single-GEMV workload
+    at its real size, against the oracle's decode and an f64 matvec."""
+    import torch
+    rows, cols = 10240, 2560
+    data = sm.synth_container(2024, rows, cols)
+    W = ref.decode(data)
+    dc = sm.DeviceContainer(data)
+    xt, xf = _x(sm, 77, 1, cols, False)
+    y = torch.zeros(1, rows, device=dev)
+    dc.gemv(xt, y)
+    y64 = ref.matvec_f64(W, xf[0])
+    err = rel_l2(y.cpu().numpy()[0], y64)
+    print(f"10240x2560 relL2 vs f64 {err:.3e}")
+    assert err <= TIGHT
+    yr = ref.matvec(W, xf[0])          # the runtime's own f32 dot (model.rs:209-234)
+    assert rel_l2(y.cpu().numpy()[0], yr) <= TIGHT
+    out = torch.zeros(rows, cols, device=dev)
+    dc.dequant(out)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), W.view(np.uint32))
