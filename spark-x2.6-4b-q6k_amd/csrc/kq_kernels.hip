@@ -58,50 +58,105 @@ __device__ __forceinline__ float sum16(float v) {
     return v;
 }
 
+typedef _Float16 kq_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 kq_h4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ kq_h2 as_h2(uint32_t v) {
+    kq_h2 r;
+    __builtin_memcpy(&r, &v, 4);
+    return r;
+}
+
+/* Two f16 pairs holding the four bytes of w (each biased by 1024: the f16
+ * with exponent field 25 and the byte as significand is exactly 1024 + b)
+ * minus `bias`: exact integers in f16. */
+__device__ __forceinline__ void bytes_to_h2(uint32_t w, _Float16 bias, kq_h2 & lo, kq_h2 & hi) {
+    const kq_h2 b2 = {bias, bias};
+    lo = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u)) - b2;
+    hi = as_h2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030402u)) - b2;
+}
+
+/* Activations staged once per workgroup as f16, 32 columns per 72-byte slot
+ * (64 bytes of data and 8 of pad, so the 16 lanes of a row, 16 slots apart,
+ * hit distinct LDS banks). f32 activations also stage the residual
+ * lo = f16(x - hi) one array further on, and the dot runs over both. */
+template <int XF32>
+__device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
+    for (int e = threadIdx.x; e < ncol * cols; e += blockDim.x) {
+        const int n = e / cols, k = e - n * cols;
+        const float v = kq_x(x, XF32, (size_t) n * ldx + k);
+        const _Float16 hi = (_Float16) v;
+        const int off = (k >> 5) * 72 + 2 * (k & 31);
+        *(_Float16 *) (lds + n * xst + off) = hi;
+        if (XF32) *(_Float16 *) (lds + (ncol + n) * xst + off) = (_Float16) (v - (float) hi);
+    }
+}
+
 /* ---------------------------------- Q8_0 --------------------------------- */
 
+template <int NC, int XF32>
 __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, int rows, int cols, const void * x,
-                                                        int xf32, int ldx, int ncol, float * y, int ldy, int accumulate) {
+                                                        int ldx, int ncol, float * y, int ldy, int accumulate) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bpr = cols / 32, xst = bpr * 72;
+    kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
+    __syncthreads();
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-    const int bpr = cols / 32;
     const size_t total = (size_t) rows * bpr;
     const int row_step = gridDim.x * (blockDim.x >> 6) * 4;
     for (int r0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 4; r0 < rows; r0 += row_step) {
-        const int row = r0 + g;
-        float acc[kMaxCols];
+        const int row = r0 + g, rowc = min(row, rows - 1);
+        float acc[NC];
 #pragma unroll
-        for (int n = 0; n < kMaxCols; n++) acc[n] = 0.0f;
-        if (row < rows) {
-            for (int c = j; c < bpr; c += 16) {
-                const size_t b = (size_t) row * bpr + c;
-                const uint8_t * blk = blocks + b * 34;
-                const float d = kq_f16(*(const uint16_t *) blk);
-                uint32_t q[8];
-                load_stream<8>(blk + 2, q, b + 1 < total);
-                float qf[32];
+        for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+        for (int cb = j; cb < bpr; cb += 64) {
+            uint32_t qw[4][8];
+            float d[4];
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) qf[4 * k + e] = (float) (int) (int8_t) (q[k] >> (8 * e));
+            for (int u = 0; u < 4; u++) {
+                const int c = cb + 16 * u;
+                if (c < bpr) {
+                    const size_t b = (size_t) rowc * bpr + c;
+                    const uint8_t * blk = blocks + b * 34;
+                    d[u] = kq_f16(*(const uint16_t *) blk);
+                    load_stream<8>(blk + 2, qw[u], b + 1 < total);
                 }
+            }
 #pragma unroll
-                for (int n = 0; n < kMaxCols; n++) {
-                    if (n < ncol) {
-                        float s = 0.0f;
+            for (int u = 0; u < 4; u++) {
+                const int c = cb + 16 * u;
+                if (c < bpr) {
 #pragma unroll
-                        for (int e = 0; e < 32; e++) s += qf[e] * kq_x(x, xf32, (size_t) n * ldx + 32 * (size_t) c + e);
-                        acc[n] += d * s;
+                    for (int n = 0; n < NC; n++) {
+                        if (n < ncol) {
+                            const uint8_t * xp = lds + n * xst + c * 72;
+                            float s = 0.0f;
+#pragma unroll
+                            for (int k = 0; k < 8; k++) {
+                                kq_h2 qa, qb;
+                                bytes_to_h2(qw[u][k] ^ 0x80808080u, (_Float16) 1152.0f, qa, qb);
+                                const kq_h4 xv = *(const kq_h4 *) (xp + 8 * k);
+                                s = __builtin_amdgcn_fdot2(qa, kq_h2{xv[0], xv[1]}, s, false);
+                                s = __builtin_amdgcn_fdot2(qb, kq_h2{xv[2], xv[3]}, s, false);
+                                if (XF32) {
+                                    const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * k);
+                                    s = __builtin_amdgcn_fdot2(qa, kq_h2{xl[0], xl[1]}, s, false);
+                                    s = __builtin_amdgcn_fdot2(qb, kq_h2{xl[2], xl[3]}, s, false);
+                                }
+                            }
+                            acc[n] += d[u] * s;
+                        }
                     }
                 }
             }
         }
 #pragma unroll
-        for (int n = 0; n < kMaxCols; n++) {
+        for (int n = 0; n < NC; n++) {
             if (n < ncol) {
-                const float s = sum16(acc[n]);
+                const float v = sum16(acc[n]);
                 if (j == 0 && row < rows) {
                     float * yp = y + (size_t) n * ldy + row;
-                    *yp = (accumulate ? *yp : 0.0f) + s;
+                    *yp = (accumulate ? *yp : 0.0f) + v;
                 }
             }
         }
@@ -110,61 +165,75 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, 
 
 /* ---------------------------------- Q6_K --------------------------------- */
 
+/* A unit is one 128-weight half of a superblock: 64 ql bytes, 32 qh bytes,
+ * 8 scales. Weight (quarter k, l) is lo4(ql[l + 32(k&1)] >> 4(k>>1)) |
+ * ((qh[l] >> 2k) & 3) << 4, minus 32, times d * scale[l/16 + 2k]. */
+template <int NC, int XF32>
 __global__ __launch_bounds__(256) void q6k_gemv_kernel(const uint8_t * blocks, int rows, int cols, const void * x,
-                                                       int xf32, int ldx, int ncol, float * y, int ldy, int accumulate) {
+                                                       int ldx, int ncol, float * y, int ldy, int accumulate) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72;
+    kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
+    __syncthreads();
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-    const int bpr = cols / 256, units = 2 * bpr;   /* a unit is one 128-weight half */
     const int row_step = gridDim.x * (blockDim.x >> 6) * 4;
     for (int r0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 4; r0 < rows; r0 += row_step) {
-        const int row = r0 + g;
-        float acc[kMaxCols];
+        const int row = r0 + g, rowc = min(row, rows - 1);
+        float acc[NC];
 #pragma unroll
-        for (int n = 0; n < kMaxCols; n++) acc[n] = 0.0f;
-        if (row < rows) {
-            for (int u = j; u < units; u += 16) {
-                const int sb = u >> 1, h = u & 1;
-                const uint8_t * blk = blocks + ((size_t) row * bpr + sb) * 210;
-                const float d = kq_f16(*(const uint16_t *) (blk + 208));
-                uint32_t ql[16], qh[8], scw[2];
-                load_stream<16>(blk + 64 * h, ql, true);
-                load_stream<8>(blk + 128 + 32 * h, qh, true);
-                load_stream<2>(blk + 192 + 8 * h, scw, true);
-                const size_t col0 = (size_t) sb * 256 + 128 * h;
+        for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+        for (int u = j; u < units; u += 16) {
+            const int sb = u >> 1, h = u & 1;
+            const uint8_t * blk = blocks + ((size_t) rowc * bpr + sb) * 210;
+            const float d = kq_f16(*(const uint16_t *) (blk + 208));
+            uint32_t ql[16], qh[8], scw[2];
+            load_stream<16>(blk + 64 * h, ql, true);
+            load_stream<8>(blk + 128 + 32 * h, qh, true);
+            load_stream<2>(blk + 192 + 8 * h, scw, true);
+            const int chunk0 = (sb * 256 + 128 * h) >> 5;   /* first 32-column LDS slot of the unit */
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
+            for (int k = 0; k < 4; k++) {
 #pragma unroll
-                    for (int p = 0; p < 2; p++) {
-                        const int sci = p + 2 * k;
-                        const float dsc = d * (float) (int) (int8_t) (scw[sci >> 2] >> (8 * (sci & 3)));
-                        float qf[16];
+                for (int p = 0; p < 2; p++) {
+                    const int sci = p + 2 * k;
+                    const float dsc = d * (float) (int) (int8_t) (scw[sci >> 2] >> (8 * (sci & 3)));
+                    kq_h2 qv[8];
 #pragma unroll
-                        for (int e = 0; e < 16; e++) {
-                            const int l = 16 * p + e;
-                            const uint32_t lo = (ql[(l + 32 * (k & 1)) >> 2] >> (8 * (l & 3) + 4 * (k >> 1))) & 15u;
-                            const uint32_t hi = (qh[l >> 2] >> (8 * (l & 3) + 2 * k)) & 3u;
-                            qf[e] = (float) ((int) (lo | (hi << 4)) - 32);
-                        }
+                    for (int w = 0; w < 4; w++) {
+                        const int l = 16 * p + 4 * w;   /* four consecutive l in one dword */
+                        const uint32_t lo = (ql[(l + 32 * (k & 1)) >> 2] >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
+                        const uint32_t hi = ((qh[l >> 2] >> (2 * k)) & 0x03030303u) << 4;
+                        bytes_to_h2(lo | hi, (_Float16) 1056.0f, qv[2 * w], qv[2 * w + 1]);
+                    }
 #pragma unroll
-                        for (int n = 0; n < kMaxCols; n++) {
-                            if (n < ncol) {
-                                float s = 0.0f;
+                    for (int n = 0; n < NC; n++) {
+                        if (n < ncol) {
+                            const uint8_t * xp = lds + n * xst + (chunk0 + k) * 72 + 32 * p;
+                            float s = 0.0f;
 #pragma unroll
-                                for (int e = 0; e < 16; e++)
-                                    s += qf[e] * kq_x(x, xf32, (size_t) n * ldx + col0 + 32 * k + 16 * p + e);
-                                acc[n] += dsc * s;
+                            for (int w = 0; w < 4; w++) {
+                                const kq_h4 xv = *(const kq_h4 *) (xp + 8 * w);
+                                s = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xv[0], xv[1]}, s, false);
+                                s = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xv[2], xv[3]}, s, false);
+                                if (XF32) {
+                                    const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * w);
+                                    s = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xl[0], xl[1]}, s, false);
+                                    s = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xl[2], xl[3]}, s, false);
+                                }
                             }
+                            acc[n] += dsc * s;
                         }
                     }
                 }
             }
         }
 #pragma unroll
-        for (int n = 0; n < kMaxCols; n++) {
+        for (int n = 0; n < NC; n++) {
             if (n < ncol) {
-                const float s = sum16(acc[n]);
+                const float v = sum16(acc[n]);
                 if (j == 0 && row < rows) {
                     float * yp = y + (size_t) n * ldy + row;
-                    *yp = (accumulate ? *yp : 0.0f) + s;
+                    *yp = (accumulate ? *yp : 0.0f) + v;
                 }
             }
         }
@@ -208,15 +277,29 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
     if (ncol > 1 && (ldx < cols || ldy < rows)) { set_error("ldx/ldy below the matrix extent"); return -1; }
     const int threads = 256;
     const int rows_per_block = (threads / 64) * 4;
+    const size_t lds = (size_t) (xf32 ? 2 : 1) * ncol * (cols / 32) * 72;
+    if (lds > 160 * 1024) { set_error("%d activation columns of %d do not fit LDS", ncol, cols); return -1; }
     int grid = (rows + rows_per_block - 1) / rows_per_block;
-    const int cap = cu_count() * 8;
+    const int cap = cu_count() * 16;
     if (grid > cap) grid = cap;
-    if (kind == 6)
-        hipLaunchKernelGGL(q6k_gemv_kernel, dim3(grid), dim3(threads), 0, s, (const uint8_t *) blocks, rows, cols, x,
-                           xf32, ldx, ncol, y, ldy, accumulate);
-    else
-        hipLaunchKernelGGL(q8_0_gemv_kernel, dim3(grid), dim3(threads), 0, s, (const uint8_t *) blocks, rows, cols, x,
-                           xf32, ldx, ncol, y, ldy, accumulate);
+    const uint8_t * bp = (const uint8_t *) blocks;
+#define KQ_LAUNCH(K, NC, XF) hipLaunchKernelGGL((K<NC, XF>), dim3(grid), dim3(threads), lds, s, bp, rows, cols, x, \
+                                                ldx, ncol, y, ldy, accumulate)
+#define KQ_PICK(K, XF)                          \
+    do {                                        \
+        if (ncol == 1) KQ_LAUNCH(K, 1, XF);     \
+        else if (ncol <= 4) KQ_LAUNCH(K, 4, XF); \
+        else KQ_LAUNCH(K, 16, XF);              \
+    } while (0)
+    if (kind == 6) {
+        if (xf32) KQ_PICK(q6k_gemv_kernel, 1);
+        else KQ_PICK(q6k_gemv_kernel, 0);
+    } else {
+        if (xf32) KQ_PICK(q8_0_gemv_kernel, 1);
+        else KQ_PICK(q8_0_gemv_kernel, 0);
+    }
+#undef KQ_PICK
+#undef KQ_LAUNCH
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("k-quant gemv launch", e);
 }

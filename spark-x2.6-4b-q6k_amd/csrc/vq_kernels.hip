@@ -49,22 +49,38 @@ __device__ __forceinline__ float load_x(const void * x, int xf32, size_t k) {
 /* Variant 3: the MFMA block kernel.                                         */
 /* ------------------------------------------------------------------------ */
 
+/* Work decomposition. A tile is 16/S rows of one matrix. Row m of the MFMA A
+ * operand is tile row m/S restricted to part m%S of the row's K range (the
+ * row's macro steps split into S equal parts); B column n = h*NC + c holds
+ * part h of activation column c (NC activation columns, S*NC <= 16). Entry
+ * C[m][n] with m%S == n/NC is then row m/S's dot over part n/NC, and the
+ * epilogue adds the S parts: the split of K lives in the N columns a single
+ * activation column would leave idle, so short matrices still fill the chip.
+ * A tile's K may further split into C chunks worked by sibling waves of the
+ * workgroup, and a workgroup holds T tiles at a time (T*C waves). Partial sums
+ * meet in LDS and are added in a fixed order, so results are deterministic. */
+
 struct FastMat {
     const uint8_t * st[2];
     float * y;
     int rows;
-    int group0;   /* first tile group of this matrix within the launch */
+    int tiles;   /* ceil(rows * S / 16) */
+    int wg0;     /* first workgroup of this matrix */
+    int nwg;     /* workgroups of this matrix */
 };
 
 struct FastArgs {
     FastMat mat[kMaxMats];
     const void * x;
-    int nmat, ngroups, cols, nc, ncol, ldx, ldy, accumulate;
+    int nmat, cols, nc, ncol, ldx, ldy, accumulate;
     uint32_t gain_off;   /* 24 + nc * 8: the same for every matrix of a launch */
     uint32_t mrow, prow;
-    int kc;              /* columns per LDS x chunk, a multiple of 128 */
-    int xstride;         /* bytes per x column row in LDS (kc * 2 + 8: the pad spreads N over banks) */
+    int lgS, C, T;       /* log2 of the parts per MFMA, wave chunks per tile, tiles per workgroup pass */
+    int M;               /* 32-index macro steps per row */
+    int xstride;         /* LDS bytes per activation column: 264 per 128 columns, plus 8 */
 };
+
+constexpr int kRedStride = 16 * 17;   /* floats per wave of the LDS reduction area */
 
 /* Byte address (index * 8) of field t of the 8 12-bit indices packed
  * LSB-first into three little-endian words. */
@@ -88,6 +104,8 @@ struct Words {
     uint32_t pb[NST];
 };
 
+/* Index words of one macro step: 12 bytes (8 indices) per lane quarter of
+ * each stage's row stream, and for 13-bit indices the plane byte. */
 template <int NST, int EXT>
 __device__ __forceinline__ void load_words(Words<NST, EXT> & W, const uint8_t * const * rp,
                                            const uint8_t * const * pp, int ms) {
@@ -101,138 +119,257 @@ __device__ __forceinline__ void load_words(Words<NST, EXT> & W, const uint8_t * 
     }
 }
 
-/* One macro-step: 32 indices of each of the wave's 16 rows, 8 per lane
- * quarter, 8 MFMAs per stage. k-slot (quarter q, step t) holds index
- * 32 * msl + 8q + t of the chunk, i.e. columns 4 * that .. + 3; A and B use the
- * same assignment, so the contraction is over the row's true columns. */
-template <int NST, int XF32, int EXT, int T>
-__device__ __forceinline__ void mstep_t(const Words<NST, EXT> & W, const uint8_t * lds, uint32_t cbb,
-                                        const uint8_t * xb, const uint8_t * xbl, f4 * acc) {
-    const h4 b = *(const h4 *) (xb + 8 * T);
-    h4 bl;
-    if (XF32) bl = *(const h4 *) (xbl + 8 * T);
-#pragma unroll
-    for (int s = 0; s < NST; s++) {
-        uint32_t a = cw_addr<T>(W.w[s][0], W.w[s][1], W.w[s][2]);
-        if (EXT) a |= (W.pb[s] << (15 - T)) & 0x8000u;
-        const h4 cw = *(const h4 *) (lds + (uint32_t) s * cbb + a);
-        acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw, b, acc[s], 0, 0, 0);
-        if (XF32) acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw, bl, acc[s], 0, 0, 0);
-    }
+/* One macro step: 8 MFMA steps per stage. k-slot (quarter q, step t) is
+ * index 8q + t of the macro step, i.e. columns 4 * that .. + 3; A (the
+ * codeword) and B (the activations) use the same assignment. Every LDS read
+ * of the step (8 B reads, 8 * NST codeword gathers) is issued before the
+ * first MFMA, so the gathers' latency overlaps. */
+template <int T, int NST, int EXT>
+__device__ __forceinline__ uint32_t step_addr(const Words<NST, EXT> & W, int s, uint32_t cbb) {
+    uint32_t a = cw_addr<T>(W.w[s][0], W.w[s][1], W.w[s][2]);
+    if (EXT) a |= (W.pb[s] << (15 - T)) & 0x8000u;
+    return (uint32_t) s * cbb + a;
 }
 
 template <int NST, int XF32, int EXT>
 __device__ __forceinline__ void mstep(const Words<NST, EXT> & W, const uint8_t * lds, uint32_t cbb,
                                       const uint8_t * xb, const uint8_t * xbl, f4 * acc) {
-    mstep_t<NST, XF32, EXT, 0>(W, lds, cbb, xb, xbl, acc);
-    mstep_t<NST, XF32, EXT, 1>(W, lds, cbb, xb, xbl, acc);
-    mstep_t<NST, XF32, EXT, 2>(W, lds, cbb, xb, xbl, acc);
-    mstep_t<NST, XF32, EXT, 3>(W, lds, cbb, xb, xbl, acc);
-    mstep_t<NST, XF32, EXT, 4>(W, lds, cbb, xb, xbl, acc);
-    mstep_t<NST, XF32, EXT, 5>(W, lds, cbb, xb, xbl, acc);
-    mstep_t<NST, XF32, EXT, 6>(W, lds, cbb, xb, xbl, acc);
-    mstep_t<NST, XF32, EXT, 7>(W, lds, cbb, xb, xbl, acc);
-}
-
-/* Cooperative conversion of x columns [c0, c1) of every activation column to
- * f16 in LDS (hi, and for f32 input also the residual lo = f16(x - hi)). */
-template <int XF32>
-__device__ __forceinline__ void stage_x(const FastArgs & A, uint8_t * lx, int c0, int c1) {
-    const int w = c1 - c0;
-    for (int e = threadIdx.x; e < A.ncol * w; e += blockDim.x) {
-        const int n = e / w, cc = e - n * w;
-        const float v = load_x(A.x, XF32, (size_t) n * A.ldx + c0 + cc);
-        const _Float16 h = (_Float16) v;
-        *(_Float16 *) (lx + n * A.xstride + 2 * cc) = h;
-        if (XF32) *(_Float16 *) (lx + (A.ncol + n) * A.xstride + 2 * cc) = (_Float16) (v - (float) h);
+    h4 cw[8][NST], b[8], bl[8];
+#pragma unroll
+    for (int s = 0; s < NST; s++) {
+        cw[0][s] = *(const h4 *) (lds + step_addr<0, NST, EXT>(W, s, cbb));
+        cw[1][s] = *(const h4 *) (lds + step_addr<1, NST, EXT>(W, s, cbb));
+        cw[2][s] = *(const h4 *) (lds + step_addr<2, NST, EXT>(W, s, cbb));
+        cw[3][s] = *(const h4 *) (lds + step_addr<3, NST, EXT>(W, s, cbb));
+        cw[4][s] = *(const h4 *) (lds + step_addr<4, NST, EXT>(W, s, cbb));
+        cw[5][s] = *(const h4 *) (lds + step_addr<5, NST, EXT>(W, s, cbb));
+        cw[6][s] = *(const h4 *) (lds + step_addr<6, NST, EXT>(W, s, cbb));
+        cw[7][s] = *(const h4 *) (lds + step_addr<7, NST, EXT>(W, s, cbb));
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        b[t] = *(const h4 *) (xb + 8 * t);
+        if (XF32) bl[t] = *(const h4 *) (xbl + 8 * t);
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+#pragma unroll
+        for (int s = 0; s < NST; s++) {
+            acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw[t][s], b[t], acc[s], 0, 0, 0);
+            if (XF32) acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw[t][s], bl[t], acc[s], 0, 0, 0);
+        }
     }
 }
 
-template <int NST, int XF32, int EXT>
-__global__ __launch_bounds__(512) void vq_mfma_kernel(const FastArgs A) {
+template <int NST, int XF32, int EXT, int D>
+__global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) A.nc * 8u;
     uint8_t * lx = lds + NST * cbb;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const int r16 = lane & 15, q = lane >> 4;
-    const int ncx = (A.cols + A.kc - 1) / A.kc;
-    const int g0 = (int) (((long long) A.ngroups * blockIdx.x) / gridDim.x);
-    const int g1 = (int) (((long long) A.ngroups * (blockIdx.x + 1)) / gridDim.x);
-    const int bn = r16 < A.ncol ? r16 : A.ncol - 1;
-    int m = 0, loaded = -1;
-    for (int g = g0; g < g1; g++) {
-        while (m + 1 < A.nmat && g >= A.mat[m + 1].group0) m++;
-        if (m != loaded) {
-            __syncthreads();
-            /* codebooks: nc * 8 bytes per stage, 16 bytes per thread step
-             * and the last 8 bytes when nc is odd */
-            const int n16 = (int) (cbb >> 4);
+    float * red = (float *) (lx + (XF32 ? 2 : 1) * A.ncol * A.xstride);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m16 = lane & 15, q = lane >> 4;
+    int mi = 0;
+    while (mi + 1 < A.nmat && (int) blockIdx.x >= A.mat[mi + 1].wg0) mi++;
+    const int rows = A.mat[mi].rows;
+    const uint32_t tiles = (uint32_t) A.mat[mi].tiles, nwg = (uint32_t) A.mat[mi].nwg;
+    const uint32_t wl = blockIdx.x - (uint32_t) A.mat[mi].wg0;
+    const int t0 = (int) (tiles * wl / nwg), t1 = (int) (tiles * (wl + 1) / nwg);
+    const int S = 1 << A.lgS, C = A.C, T = A.T, ncol = A.ncol;
+    const int rpt = 16 >> A.lgS;                   /* rows per tile */
+    const int j = wave / C, c = wave - j * C;      /* tile slot, K chunk */
+    const int MP = A.M >> A.lgS, MS = MP / C;      /* macro steps per part, per unit */
+    const int r_in = m16 >> A.lgS, h = m16 & (S - 1);  /* A side: tile row, part */
+    const int hp = m16 / ncol, cn = m16 - hp * ncol;   /* B side: part, activation column */
+    const bool bval = hp < S;
+    const int msa = h * MP + c * MS;
+    const int msb = (bval ? hp : 0) * MP + c * MS;
+    /* x in LDS: 128 columns (one macro step) per 264 bytes, the 8-byte pad
+     * putting the parts that lanes read at once on different banks */
+    const uint8_t * xb = lx + (bval ? cn : 0) * A.xstride + 264 * msb + 64 * q;
+    const uint8_t * xbl = xb + ncol * A.xstride;
+    const int iters = (t1 - t0 + T - 1) / T;
+    const uint32_t stream_off = A.gain_off + (uint32_t) rows * 2u;
+
+    const uint8_t * rp[NST];
+    const uint8_t * pp[NST];
+    /* a ring of D macro steps of index words, D >= the unit's steps in the
+     * usual shapes, so a wave requests its whole unit at once; every load is
+     * issued unconditionally (steps past the unit re-read its last step), so
+     * the number of loads in flight is static and each use waits only for its
+     * own words */
+    Words<NST, EXT> w[D];
+    auto ld = [&](Words<NST, EXT> & W, int ms) { load_words<NST, EXT>(W, rp, pp, ms < MS ? ms : MS - 1); };
+    auto ld_all = [&]() {
 #pragma unroll
-            for (int s = 0; s < NST; s++) {
-                const uint32_t * src = (const uint32_t *) (A.mat[m].st[s] + 24);
-                uint32_t * dst = (uint32_t *) (lds + s * cbb);
-                for (int i = threadIdx.x; i < n16; i += blockDim.x) {
-                    const uint32_t a0 = src[4 * i], a1 = src[4 * i + 1], a2 = src[4 * i + 2], a3 = src[4 * i + 3];
-                    dst[4 * i] = a0; dst[4 * i + 1] = a1; dst[4 * i + 2] = a2; dst[4 * i + 3] = a3;
-                }
-                if ((cbb & 8u) && threadIdx.x < 2) dst[4 * n16 + threadIdx.x] = src[4 * n16 + threadIdx.x];
-            }
-            if (loaded < 0 && ncx == 1) stage_x<XF32>(A, lx, 0, A.cols);
-            __syncthreads();
-            loaded = m;
-        }
-        const int rows = A.mat[m].rows;
-        const int trow = (g - A.mat[m].group0) * nwave * 16 + wave * 16;
-        const bool active = trow < rows;
-        const int row = min(trow + r16, rows - 1);
-        const uint8_t * rp[NST];
-        const uint8_t * pp[NST];
+        for (int u = 0; u < D; u++) ld(w[u], u);
+    };
+    auto point = [&](int tile) {
+        const int row = min(tile * rpt + r_in, rows - 1);
 #pragma unroll
         for (int s = 0; s < NST; s++) {
-            const uint8_t * sbase = A.mat[m].st[s] + A.gain_off + (size_t) rows * 2;
-            rp[s] = sbase + (size_t) row * A.mrow + 12 * q;
-            pp[s] = sbase + (size_t) rows * A.mrow + (size_t) row * A.prow + q;
+            const uint8_t * sb = A.mat[mi].st[s] + stream_off;
+            rp[s] = sb + (size_t) row * A.mrow + 48 * msa + 12 * q;
+            pp[s] = sb + (size_t) rows * A.mrow + (size_t) row * A.prow + 4 * msa + q;
         }
+    };
+    /* gains of the rows this lane's C entries belong to, per stage */
+    uint32_t gw[NST][4];
+    auto ld_gains = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = min(tile * rpt + ((4 * q + i) >> A.lgS), rows - 1);
+#pragma unroll
+            for (int s = 0; s < NST; s++) gw[s][i] = *(const uint16_t *) (A.mat[mi].st[s] + A.gain_off + 2 * (size_t) row);
+        }
+    };
+
+    /* Staging: codebooks (16-byte chunks) and activations (4-byte words)
+     * go to LDS. For one activation column every thread issues all its
+     * staging loads at once, then the first unit's index words and gains,
+     * then the LDS stores: the prologue costs one memory latency and the
+     * unit's loads are in flight when the main loop starts. */
+    const int n16 = (int) (cbb >> 4);              /* 16-byte chunks per stage */
+    const int ncb = NST * n16;
+    const bool xpair = !XF32 && !(A.cols & 1) && !(A.ldx & 1) && !((uintptr_t) A.x & 3);
+    const int xpr = xpair ? A.cols >> 1 : A.cols;  /* 4-byte words per activation column */
+    auto cb_load = [&](int i, uint32_t * v) {
+        const int s = NST > 1 && i >= n16 ? 1 : 0;
+        const uint32_t * src = (const uint32_t *) (A.mat[mi].st[s] + 24) + 4 * (i - s * n16);
+        v[0] = src[0]; v[1] = src[1]; v[2] = src[2]; v[3] = src[3];
+    };
+    auto cb_store = [&](int i, const uint32_t * v) {
+        const int s = NST > 1 && i >= n16 ? 1 : 0;
+        uint32_t * dst = (uint32_t *) (lds + s * cbb) + 4 * (i - s * n16);
+        dst[0] = v[0]; dst[1] = v[1]; dst[2] = v[2]; dst[3] = v[3];
+    };
+    auto x_load = [&](int n, int k) -> uint32_t {
+        if (XF32) return ((const uint32_t *) A.x)[(size_t) n * A.ldx + k];
+        if (xpair) return ((const uint32_t *) A.x)[((size_t) n * A.ldx >> 1) + k];
+        return ((const uint16_t *) A.x)[(size_t) n * A.ldx + k];
+    };
+    auto x_store = [&](int n, int k, uint32_t v) {
+        if (XF32) {
+            const float f = __uint_as_float(v);
+            const _Float16 hi = (_Float16) f;
+            const int off = 264 * (k >> 7) + 2 * (k & 127);
+            *(_Float16 *) (lx + n * A.xstride + off) = hi;
+            *(_Float16 *) (lx + (ncol + n) * A.xstride + off) = (_Float16) (f - (float) hi);
+        } else if (xpair) {
+            const int e = 2 * k;
+            const int off = 264 * (e >> 7) + 2 * (e & 127);
+            const _Float16 lo16 = (_Float16) __uint_as_float(v << 16), hi16 = (_Float16) __uint_as_float(v & 0xffff0000u);
+            *(_Float16 *) (lx + n * A.xstride + off) = lo16;
+            *(_Float16 *) (lx + n * A.xstride + off + 2) = hi16;
+        } else {
+            *(_Float16 *) (lx + n * A.xstride + 264 * (k >> 7) + 2 * (k & 127)) = (_Float16) __uint_as_float(v << 16);
+        }
+    };
+    const int first = min(t0 + j, t1 - 1);
+    constexpr int K = 8;
+    const int bd = blockDim.x, tid = threadIdx.x;
+    if (ncol == 1 && ncb <= K * bd && xpr <= K * bd) {
+        uint32_t cv[K][4], xv[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = k * bd + tid;
+            if (i < ncb) cb_load(i, cv[k]);
+            if (i < xpr) xv[k] = x_load(0, i);
+        }
+        point(first);
+        ld_all();
+        ld_gains(first);
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = k * bd + tid;
+            if (i < ncb) cb_store(i, cv[k]);
+            if (i < xpr) x_store(0, i, xv[k]);
+        }
+    } else {
+        for (int base = 0; base < ncb; base += K * bd) {
+            uint32_t cv[K][4];
+#pragma unroll
+            for (int k = 0; k < K; k++)
+                if (base + k * bd + tid < ncb) cb_load(base + k * bd + tid, cv[k]);
+#pragma unroll
+            for (int k = 0; k < K; k++)
+                if (base + k * bd + tid < ncb) cb_store(base + k * bd + tid, cv[k]);
+        }
+        for (int n = 0; n < ncol; n++) {
+            for (int base = 0; base < xpr; base += K * bd) {
+                uint32_t xv[K];
+#pragma unroll
+                for (int k = 0; k < K; k++)
+                    if (base + k * bd + tid < xpr) xv[k] = x_load(n, base + k * bd + tid);
+#pragma unroll
+                for (int k = 0; k < K; k++)
+                    if (base + k * bd + tid < xpr) x_store(n, base + k * bd + tid, xv[k]);
+            }
+        }
+        point(first);
+        ld_all();
+        ld_gains(first);
+    }
+    if ((cbb & 8u) && tid < 2 * NST) {   /* an odd codebook: the last codeword of each stage */
+        const int s = tid >> 1, k = tid & 1;
+        ((uint32_t *) (lds + s * cbb))[4 * n16 + k] = ((const uint32_t *) (A.mat[mi].st[s] + 24))[4 * n16 + k];
+    }
+    __syncthreads();
+
+    for (int it = 0; it < iters; it++) {
+        const int tile = t0 + it * T + j;
+        const bool active = tile < t1;
         f4 acc[NST];
 #pragma unroll
         for (int s = 0; s < NST; s++) acc[s] = f4{0.f, 0.f, 0.f, 0.f};
-        for (int c = 0; c < ncx; c++) {
-            const int c0 = c * A.kc, c1 = min(A.cols, c0 + A.kc);
-            if (ncx > 1) {
-                __syncthreads();
-                stage_x<XF32>(A, lx, c0, c1);
-                __syncthreads();
+        if (active) {
+            if (it > 0) {
+                point(tile);
+                ld_all();
+                ld_gains(tile);
             }
-            if (active) {
-                const int ms0 = c0 >> 7, ms1 = c1 >> 7;
-                const uint8_t * xb = lx + bn * A.xstride + 64 * q;
-                const uint8_t * xbl = lx + (A.ncol + bn) * A.xstride + 64 * q;
-                Words<NST, EXT> cur, nxt;
-                load_words<NST, EXT>(cur, rp, pp, ms0);
-                for (int ms = ms0; ms < ms1; ms++) {
-                    if (ms + 1 < ms1) load_words<NST, EXT>(nxt, rp, pp, ms + 1);
-                    const int off = 256 * (ms - ms0);
-                    mstep<NST, XF32, EXT>(cur, lds, cbb, xb + off, xbl + off, acc);
-                    cur = nxt;
+            for (int ms0 = 0; ms0 < MS; ms0 += D) {
+#pragma unroll
+                for (int u = 0; u < D; u++) {
+                    if (ms0 + u < MS)
+                        mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc);
+                    if (MS > D) ld(w[u], ms0 + u + D);
                 }
             }
         }
-        if (active && r16 < A.ncol) {
+        /* stages combine with their row gains; entry C[4q + i][m16] of this
+         * lane goes to the wave's reduction area */
+        float * R = red + wave * kRedStride;
+        if (active) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int r = trow + 4 * q + i;
-                if (r < rows) {
-                    float * yp = A.mat[m].y + (size_t) r16 * A.ldy + r;
-                    float v = A.accumulate ? *yp : 0.0f;
+                float v = 0.0f;
 #pragma unroll
-                    for (int s = 0; s < NST; s++) {
-                        const float gs = f16_to_f32(*(const uint16_t *) (A.mat[m].st[s] + A.gain_off + 2 * (size_t) r));
-                        v += gs * acc[s][i];
-                    }
-                    *yp = v;
+                for (int s = 0; s < NST; s++) v += f16_to_f32((uint16_t) gw[s][i]) * acc[s][i];
+                R[(4 * q + i) * 17 + m16] = v;
+            }
+        }
+        __syncthreads();
+        /* y[col][row] = sum over parts hh (and over the C chunk waves) of
+         * C[r*S + hh][hh*ncol + col], added in a fixed order */
+        if (active && c == 0) {
+            for (int e = lane; e < rpt * ncol; e += 64) {
+                const int r = ncol == 1 ? e : e / ncol, col = e - r * ncol;
+                const int row = tile * rpt + r;
+                float sum = 0.0f;
+                for (int hh = 0; hh < S; hh++) {
+                    const float * rr = red + wave * kRedStride + (r * S + hh) * 17 + hh * ncol + col;
+                    float part = rr[0];
+                    for (int cw = 1; cw < C; cw++) part += rr[cw * kRedStride];
+                    sum += part;
+                }
+                if (row < rows) {
+                    float * yp = A.mat[mi].y + (size_t) col * A.ldy + row;
+                    *yp = (A.accumulate ? *yp : 0.0f) + sum;
                 }
             }
         }
+        __syncthreads();
     }
 }
 
@@ -381,27 +518,87 @@ int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
 
 static int aligned4(const void * p) { return ((uintptr_t) p & 3u) == 0; }
 
-template <int NST, int XF32, int EXT>
+template <int NST, int XF32, int EXT, int D>
 static int launch_fast_t(const FastArgs & A, int grid, int threads, size_t lds, hipStream_t s) {
     static size_t opted = 0;
-    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT>;
+    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, D>;
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the VQ block kernel", e);
         opted = lds;
     }
-    hipLaunchKernelGGL((vq_mfma_kernel<NST, XF32, EXT>), dim3(grid), dim3(threads), lds, s, A);
+    hipLaunchKernelGGL((vq_mfma_kernel<NST, XF32, EXT, D>), dim3(grid), dim3(threads), lds, s, A);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip("VQ block kernel launch", e);
+    return 0;
+}
+
+/* The block kernel's launch shape for a call: parts per MFMA (S), wave chunks
+ * (C) and tiles per workgroup pass (T), so that about one workgroup per CU
+ * gets eight or more waves of work. */
+struct FastShape {
+    int S, C, T, W, nwg;
+    size_t lds;
+};
+
+/* LDS bytes per activation column: 264 bytes per 128 columns (256 of f16
+ * values and 8 of pad) and 8 more between columns. */
+static int fast_xstride(int cols, int S) { (void) S; return 264 * (cols / 128) + 8; }
+
+static size_t fast_lds(const VqCall & c, int nst, int S, int W) {
+    return (size_t) nst * c.nc * 8 + (size_t) (c.xf32 ? 2 : 1) * c.ncol * fast_xstride(c.cols, S) +
+           (size_t) W * kRedStride * 4;
+}
+
+static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
+    const int M = c.cols / 4 / 32;
+    const int G = cu_count();
+    const int want = G * 8;
+    long total_rows = 0;
+    for (int m = 0; m < c.nmat; m++) total_rows += c.mats[m].rows;
+    auto tiles_for = [&](int S) {
+        long t = 0;
+        for (int m = 0; m < c.nmat; m++) t += (c.mats[m].rows * (long) S + 15) / 16;
+        return t;
+    };
+    int S = 0;
+    for (int s = 1; s <= 16; s *= 2) {
+        if (s * c.ncol > 16 || M % s) continue;
+        S = s;
+        if (tiles_for(s) >= want) break;
+    }
+    if (!S) { set_error("no MFMA part split fits %d columns and %d macro steps", c.ncol, M); return -1; }
+    const long tiles = tiles_for(S);
+    int C = 1;
+    if (tiles < want) {
+        const int MP = M / S;
+        for (int cc = 2; cc <= 10; cc++) {
+            if (MP % cc || MP / cc < 2) continue;
+            C = cc;
+            if (tiles * cc >= want) break;
+        }
+    }
+    int T = (int) ((tiles + G - 1) / G);
+    if (T < 1) T = 1;
+    if (T * C > 10) T = 10 / C > 0 ? 10 / C : 1;
+    if (T * C > 10) { C = 10; T = 1; }
+    sh.S = S; sh.C = C; sh.T = T; sh.W = T * C;
+    sh.nwg = 0;
+    for (int m = 0; m < c.nmat; m++) sh.nwg += (int) (((c.mats[m].rows * (long) S + 15) / 16 + T - 1) / T);
+    sh.lds = fast_lds(c, nst, S, sh.W);
+    (void) total_rows;
     return 0;
 }
 
 static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
     const Layout L0 = make_layout(c.dim, c.nc, c.mats[0].rows, c.cols, 1);
     const int ext = L0.nbit > 12;
-    const int threads = c.threads ? c.threads : 512;
-    if (threads > 512) { set_error("the VQ block kernel runs at most 512 threads per workgroup, not %d", threads); return -1; }
-    const int nwave = threads / 64;
+    FastShape sh;
+    if (fast_shape(c, nst, sh)) return -1;
+    if (sh.lds > (size_t) kLdsMax) {
+        set_error("codebooks and %d activation columns of %d need %zu bytes of LDS", c.ncol, c.cols, sh.lds);
+        return -1;
+    }
     FastArgs A;
     memset(&A, 0, sizeof A);
     A.x = c.x;
@@ -415,47 +612,41 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
     A.gain_off = (uint32_t) L0.gain_off;
     A.mrow = (uint32_t) L0.mrow;
     A.prow = (uint32_t) L0.prow;
-    int groups = 0;
+    A.lgS = 0;
+    while ((1 << A.lgS) < sh.S) A.lgS++;
+    A.C = sh.C; A.T = sh.T;
+    A.M = c.cols / 4 / 32;
+    A.xstride = fast_xstride(c.cols, sh.S);
+    int wg = 0;
     for (int m = 0; m < c.nmat; m++) {
         for (int s = 0; s < nst; s++) A.mat[m].st[s] = (const uint8_t *) c.mats[m].stages[st0 + s];
         A.mat[m].y = c.mats[m].y;
         A.mat[m].rows = c.mats[m].rows;
-        A.mat[m].group0 = groups;
-        groups += (c.mats[m].rows + 16 * nwave - 1) / (16 * nwave);
+        A.mat[m].tiles = (int) ((c.mats[m].rows * (long) sh.S + 15) / 16);
+        A.mat[m].wg0 = wg;
+        A.mat[m].nwg = (A.mat[m].tiles + sh.T - 1) / sh.T;
+        wg += A.mat[m].nwg;
     }
-    A.ngroups = groups;
-    const size_t cbb = (size_t) nst * c.nc * 8;
-    const int xmul = c.xf32 ? 2 : 1;
-    /* x chunk: every column resident when it fits, else the widest multiple of
-     * 128 columns that does. */
-    const size_t room = kLdsMax - cbb;
-    int kc = c.cols;
-    if ((size_t) xmul * c.ncol * ((size_t) kc * 2 + 8) > room) {
-        kc = (int) (((room / ((size_t) xmul * c.ncol)) - 8) / 2);
-        kc &= ~127;
-        if (kc < 128) { set_error("x of %d columns does not fit LDS beside the codebooks", c.ncol); return -1; }
-    }
-    A.kc = kc;
-    A.xstride = kc * 2 + 8;
-    const size_t lds = cbb + (size_t) xmul * c.ncol * A.xstride;
-    int grid = c.grid;
-    if (grid <= 0) {
-        const int per_cu = (int) (kLdsMax / lds) > 0 ? (int) (kLdsMax / lds) : 1;
-        grid = cu_count() * (per_cu < 2 ? per_cu : 2);
-    }
-    if (grid > groups) grid = groups;
-    if (grid < 1) grid = 1;
+    const int threads = sh.W * 64;
+    const int MS = A.M / sh.S / sh.C;
     const int key = (nst == 2 ? 4 : 0) | (c.xf32 ? 2 : 0) | (ext ? 1 : 0);
-    switch (key) {
-        case 0: return launch_fast_t<1, 0, 0>(A, grid, threads, lds, c.stream);
-        case 1: return launch_fast_t<1, 0, 1>(A, grid, threads, lds, c.stream);
-        case 2: return launch_fast_t<1, 1, 0>(A, grid, threads, lds, c.stream);
-        case 3: return launch_fast_t<1, 1, 1>(A, grid, threads, lds, c.stream);
-        case 4: return launch_fast_t<2, 0, 0>(A, grid, threads, lds, c.stream);
-        case 5: return launch_fast_t<2, 0, 1>(A, grid, threads, lds, c.stream);
-        case 6: return launch_fast_t<2, 1, 0>(A, grid, threads, lds, c.stream);
-        default: return launch_fast_t<2, 1, 1>(A, grid, threads, lds, c.stream);
+#define FAST_D(D)                                                                   \
+    switch (key) {                                                                  \
+        case 0: return launch_fast_t<1, 0, 0, D>(A, wg, threads, sh.lds, c.stream); \
+        case 1: return launch_fast_t<1, 0, 1, D>(A, wg, threads, sh.lds, c.stream); \
+        case 2: return launch_fast_t<1, 1, 0, D>(A, wg, threads, sh.lds, c.stream); \
+        case 3: return launch_fast_t<1, 1, 1, D>(A, wg, threads, sh.lds, c.stream); \
+        case 4: return launch_fast_t<2, 0, 0, D>(A, wg, threads, sh.lds, c.stream); \
+        case 5: return launch_fast_t<2, 0, 1, D>(A, wg, threads, sh.lds, c.stream); \
+        case 6: return launch_fast_t<2, 1, 0, D>(A, wg, threads, sh.lds, c.stream); \
+        default: return launch_fast_t<2, 1, 1, D>(A, wg, threads, sh.lds, c.stream); \
     }
+    /* ring depth: the whole unit in one round when it has at most 12 steps
+     * (8 with the plane bytes of 13-bit indices, which would spill at 12) */
+    if (MS <= 4) FAST_D(4)
+    if (MS <= 8 || ext) FAST_D(8)
+    FAST_D(12)
+#undef FAST_D
 }
 
 static int launch_wave(const VqCall & c, int variant) {
@@ -512,10 +703,19 @@ int vq_launch(const VqCall & c) {
         }
         if (!fast_geometry_ok(c.dim, c.nc, c.mats[m].rows, c.cols, c.v3)) all_fast = 0;
     }
+    if (all_fast) {
+        /* the block kernel also needs its codebooks and x resident in LDS */
+        FastShape sh;
+        const int nst = c.nst < 2 ? c.nst : 2;
+        if (fast_shape(c, nst, sh) || sh.lds > (size_t) kLdsMax) all_fast = 0;
+    }
     int variant = c.variant;
     if (variant == 0) variant = all_fast ? 3 : ((size_t) c.nc * c.dim * 2 <= 65536 ? 2 : 1);
     if (variant == 3) {
-        if (!all_fast) { set_error("the VQ block kernel does not take this geometry or alignment"); return -1; }
+        if (!all_fast) {
+            set_error("the VQ block kernel does not take this geometry, alignment or LDS footprint");
+            return -1;
+        }
         for (int st0 = 0; st0 < c.nst; st0 += 2) {
             const int n = c.nst - st0 < 2 ? c.nst - st0 : 2;
             if (launch_fast(c, st0, n, st0 > 0 || c.accumulate)) return -1;

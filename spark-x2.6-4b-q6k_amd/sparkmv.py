@@ -91,11 +91,20 @@ SIGNATURES = {
 
 
 def lib():
-    """The loaded library; raises if it has not been built."""
+    """The loaded library; raises if it has not been built.
+
+    torch is imported first: it loads its own HIP runtime (libamdhip64,
+    soname libamdhip64.so.7), and libsparkmv's dependency on that soname then
+    binds to the same runtime. Loading libsparkmv first would bring a second
+    HIP runtime into the process, and the two do not share the device."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise SparkmvError(f"{LIB_PATH} is missing: build it with spark-x2.6-4b-q6k_amd/build.py")
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)
