@@ -161,8 +161,13 @@ __device__ __forceinline__ void mstep(const Words<NST, EXT> & W, const uint8_t *
     }
 }
 
-template <int NST, int XF32, int EXT, int D>
+template <int NST, int XF32, int EXT, int MSC>
 __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
+    /* MSC > 0: a unit is exactly MSC macro steps, known at compile time, so
+     * the whole unit runs as straight-line code and each step waits only for
+     * its own index words (a loop would make the compiler wait for all of a
+     * wave's loads at its head). MSC == 0: any unit length, a ring of D steps. */
+    constexpr int D = MSC > 0 ? MSC : 8;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) A.nc * 8u;
     uint8_t * lx = lds + NST * cbb;
@@ -178,7 +183,8 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     const int S = 1 << A.lgS, C = A.C, T = A.T, ncol = A.ncol;
     const int rpt = 16 >> A.lgS;                   /* rows per tile */
     const int j = wave / C, c = wave - j * C;      /* tile slot, K chunk */
-    const int MP = A.M >> A.lgS, MS = MP / C;      /* macro steps per part, per unit */
+    const int MP = A.M >> A.lgS;                   /* macro steps per part */
+    const int MS = MSC > 0 ? MSC : MP / C;         /* macro steps per unit */
     const int r_in = m16 >> A.lgS, h = m16 & (S - 1);  /* A side: tile row, part */
     const int hp = m16 / ncol, cn = m16 - hp * ncol;   /* B side: part, activation column */
     const bool bval = hp < S;
@@ -191,13 +197,15 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     const int iters = (t1 - t0 + T - 1) / T;
     const uint32_t stream_off = A.gain_off + (uint32_t) rows * 2u;
 
+    /* the matrix's stage payloads, read once (uniform) */
+    const uint8_t * stp[NST];
+#pragma unroll
+    for (int s = 0; s < NST; s++) stp[s] = A.mat[mi].st[s];
     const uint8_t * rp[NST];
     const uint8_t * pp[NST];
-    /* a ring of D macro steps of index words, D >= the unit's steps in the
-     * usual shapes, so a wave requests its whole unit at once; every load is
-     * issued unconditionally (steps past the unit re-read its last step), so
-     * the number of loads in flight is static and each use waits only for its
-     * own words */
+    /* index words of D macro steps; every load is issued unconditionally
+     * (steps past the unit re-read its last step), so the number of loads in
+     * flight is static and each use waits only for its own words */
     Words<NST, EXT> w[D];
     auto ld = [&](Words<NST, EXT> & W, int ms) { load_words<NST, EXT>(W, rp, pp, ms < MS ? ms : MS - 1); };
     auto ld_all = [&]() {
@@ -208,7 +216,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         const int row = min(tile * rpt + r_in, rows - 1);
 #pragma unroll
         for (int s = 0; s < NST; s++) {
-            const uint8_t * sb = A.mat[mi].st[s] + stream_off;
+            const uint8_t * sb = stp[s] + stream_off;
             rp[s] = sb + (size_t) row * A.mrow + 48 * msa + 12 * q;
             pp[s] = sb + (size_t) rows * A.mrow + (size_t) row * A.prow + 4 * msa + q;
         }
@@ -220,7 +228,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         for (int i = 0; i < 4; i++) {
             const int row = min(tile * rpt + ((4 * q + i) >> A.lgS), rows - 1);
 #pragma unroll
-            for (int s = 0; s < NST; s++) gw[s][i] = *(const uint16_t *) (A.mat[mi].st[s] + A.gain_off + 2 * (size_t) row);
+            for (int s = 0; s < NST; s++) gw[s][i] = *(const uint16_t *) (stp[s] + A.gain_off + 2 * (size_t) row);
         }
     };
 
@@ -228,14 +236,19 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
      * go to LDS. For one activation column every thread issues all its
      * staging loads at once, then the first unit's index words and gains,
      * then the LDS stores: the prologue costs one memory latency and the
-     * unit's loads are in flight when the main loop starts. */
+     * unit's loads are in flight when the main loop starts. Each workgroup
+     * walks the codebooks from its own starting chunk, so the workgroups of
+     * an XCD do not all ask the same L2 channel for the same line at once. */
     const int n16 = (int) (cbb >> 4);              /* 16-byte chunks per stage */
     const int ncb = NST * n16;
-    const bool xpair = !XF32 && !(A.cols & 1) && !(A.ldx & 1) && !((uintptr_t) A.x & 3);
-    const int xpr = xpair ? A.cols >> 1 : A.cols;  /* 4-byte words per activation column */
+    const int rot = (int) ((blockIdx.x * 328u) % (uint32_t) ncb);
+    auto rot_chunk = [&](int i) { const int r = i + rot; return r >= ncb ? r - ncb : r; };
+    /* bf16 x is read as pairs: the host sends only 4-byte aligned x with an
+     * even ldx here (cols is a multiple of 128) */
+    const int xpr = XF32 ? A.cols : A.cols >> 1;   /* 4-byte words per activation column */
     auto cb_load = [&](int i, uint32_t * v) {
-        const int s = NST > 1 && i >= n16 ? 1 : 0;
-        const uint32_t * src = (const uint32_t *) (A.mat[mi].st[s] + 24) + 4 * (i - s * n16);
+        const bool hi = NST > 1 && i >= n16;
+        const uint32_t * src = (const uint32_t *) ((hi ? stp[NST - 1] : stp[0]) + 24) + 4 * (hi ? i - n16 : i);
         v[0] = src[0]; v[1] = src[1]; v[2] = src[2]; v[3] = src[3];
     };
     auto cb_store = [&](int i, const uint32_t * v) {
@@ -245,8 +258,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     };
     auto x_load = [&](int n, int k) -> uint32_t {
         if (XF32) return ((const uint32_t *) A.x)[(size_t) n * A.ldx + k];
-        if (xpair) return ((const uint32_t *) A.x)[((size_t) n * A.ldx >> 1) + k];
-        return ((const uint16_t *) A.x)[(size_t) n * A.ldx + k];
+        return ((const uint32_t *) A.x)[((size_t) n * A.ldx >> 1) + k];
     };
     auto x_store = [&](int n, int k, uint32_t v) {
         if (XF32) {
@@ -255,45 +267,52 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
             const int off = 264 * (k >> 7) + 2 * (k & 127);
             *(_Float16 *) (lx + n * A.xstride + off) = hi;
             *(_Float16 *) (lx + (ncol + n) * A.xstride + off) = (_Float16) (f - (float) hi);
-        } else if (xpair) {
+        } else {
+            /* a pair never straddles a 128-column block: one 4-byte store */
             const int e = 2 * k;
             const int off = 264 * (e >> 7) + 2 * (e & 127);
             const _Float16 lo16 = (_Float16) __uint_as_float(v << 16), hi16 = (_Float16) __uint_as_float(v & 0xffff0000u);
-            *(_Float16 *) (lx + n * A.xstride + off) = lo16;
-            *(_Float16 *) (lx + n * A.xstride + off + 2) = hi16;
-        } else {
-            *(_Float16 *) (lx + n * A.xstride + 264 * (k >> 7) + 2 * (k & 127)) = (_Float16) __uint_as_float(v << 16);
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            *(h2 *) (lx + n * A.xstride + off) = h2{lo16, hi16};
         }
     };
     const int first = min(t0 + j, t1 - 1);
     constexpr int K = 8;
     const int bd = blockDim.x, tid = threadIdx.x;
-    if (ncol == 1 && ncb <= K * bd && xpr <= K * bd) {
+    if constexpr (MSC > 0) {
+        /* One activation column, an even codebook, and at most K staging
+         * chunks and words per thread (the host checks all three). Threads
+         * past the end load and store the last chunk or word again (one cache
+         * line per wave, the same bytes to the same place), so the prologue
+         * has no branches and the compiler counts every load exactly. */
         uint32_t cv[K][4], xv[K];
 #pragma unroll
         for (int k = 0; k < K; k++) {
             const int i = k * bd + tid;
-            if (i < ncb) cb_load(i, cv[k]);
-            if (i < xpr) xv[k] = x_load(0, i);
+            cb_load(rot_chunk(min(i, ncb - 1)), cv[k]);
+            xv[k] = x_load(0, min(i, xpr - 1));
         }
         point(first);
         ld_all();
         ld_gains(first);
+        /* keep the scheduler from pulling stores (and their waits) up
+         * between the loads */
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < K; k++) {
             const int i = k * bd + tid;
-            if (i < ncb) cb_store(i, cv[k]);
-            if (i < xpr) x_store(0, i, xv[k]);
+            cb_store(rot_chunk(min(i, ncb - 1)), cv[k]);
+            x_store(0, min(i, xpr - 1), xv[k]);
         }
     } else {
         for (int base = 0; base < ncb; base += K * bd) {
             uint32_t cv[K][4];
 #pragma unroll
             for (int k = 0; k < K; k++)
-                if (base + k * bd + tid < ncb) cb_load(base + k * bd + tid, cv[k]);
+                if (base + k * bd + tid < ncb) cb_load(rot_chunk(base + k * bd + tid), cv[k]);
 #pragma unroll
             for (int k = 0; k < K; k++)
-                if (base + k * bd + tid < ncb) cb_store(base + k * bd + tid, cv[k]);
+                if (base + k * bd + tid < ncb) cb_store(rot_chunk(base + k * bd + tid), cv[k]);
         }
         for (int n = 0; n < ncol; n++) {
             for (int base = 0; base < xpr; base += K * bd) {
@@ -310,30 +329,31 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         ld_all();
         ld_gains(first);
     }
-    if ((cbb & 8u) && tid < 2 * NST) {   /* an odd codebook: the last codeword of each stage */
+    if (MSC == 0 && (cbb & 8u) && tid < 2 * NST) {   /* an odd codebook: the last codeword of each stage */
         const int s = tid >> 1, k = tid & 1;
-        ((uint32_t *) (lds + s * cbb))[4 * n16 + k] = ((const uint32_t *) (A.mat[mi].st[s] + 24))[4 * n16 + k];
+        ((uint32_t *) (lds + s * cbb))[4 * n16 + k] = ((const uint32_t *) ((s ? stp[NST - 1] : stp[0]) + 24))[4 * n16 + k];
     }
     __syncthreads();
 
-    for (int it = 0; it < iters; it++) {
-        const int tile = t0 + it * T + j;
+    /* One unit: the tile's MS macro steps, then the epilogue. The index
+     * words and gains of the tile are already requested. */
+    auto unit = [&](int tile) {
         const bool active = tile < t1;
         f4 acc[NST];
 #pragma unroll
         for (int s = 0; s < NST; s++) acc[s] = f4{0.f, 0.f, 0.f, 0.f};
         if (active) {
-            if (it > 0) {
-                point(tile);
-                ld_all();
-                ld_gains(tile);
-            }
-            for (int ms0 = 0; ms0 < MS; ms0 += D) {
+            if (MSC > 0) {
 #pragma unroll
-                for (int u = 0; u < D; u++) {
-                    if (ms0 + u < MS)
-                        mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc);
-                    if (MS > D) ld(w[u], ms0 + u + D);
+                for (int u = 0; u < D; u++) mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc);
+            } else {
+                for (int ms0 = 0; ms0 < MS; ms0 += D) {
+#pragma unroll
+                    for (int u = 0; u < D; u++) {
+                        if (ms0 + u < MS)
+                            mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc);
+                        if (MS > D) ld(w[u], ms0 + u + D);
+                    }
                 }
             }
         }
@@ -349,7 +369,15 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
                 R[(4 * q + i) * 17 + m16] = v;
             }
         }
-        __syncthreads();
+        /* with one wave per tile the wave only reads its own area back: its
+         * LDS operations complete in order, no workgroup barrier needed */
+        if (C > 1) {
+            __syncthreads();
+        } else {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
         /* y[col][row] = sum over parts hh (and over the C chunk waves) of
          * C[r*S + hh][hh*ncol + col], added in a fixed order */
         if (active && c == 0) {
@@ -369,7 +397,23 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
                 }
             }
         }
-        __syncthreads();
+        if (C > 1) {
+            __syncthreads();
+        } else {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    };
+    /* the first unit's words were requested in the prologue; later units
+     * (only when a workgroup holds more tiles than waves) request their own */
+    unit(t0 + j);
+    for (int it = 1; it < iters; it++) {
+        const int tile = t0 + it * T + j;
+        point(min(tile, t1 - 1));
+        ld_all();
+        ld_gains(min(tile, t1 - 1));
+        unit(tile);
     }
 }
 
@@ -518,16 +562,16 @@ int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
 
 static int aligned4(const void * p) { return ((uintptr_t) p & 3u) == 0; }
 
-template <int NST, int XF32, int EXT, int D>
+template <int NST, int XF32, int EXT, int MSC>
 static int launch_fast_t(const FastArgs & A, int grid, int threads, size_t lds, hipStream_t s) {
     static size_t opted = 0;
-    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, D>;
+    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, MSC>;
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the VQ block kernel", e);
         opted = lds;
     }
-    hipLaunchKernelGGL((vq_mfma_kernel<NST, XF32, EXT, D>), dim3(grid), dim3(threads), lds, s, A);
+    hipLaunchKernelGGL((vq_mfma_kernel<NST, XF32, EXT, MSC>), dim3(grid), dim3(threads), lds, s, A);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip("VQ block kernel launch", e);
     return 0;
@@ -590,6 +634,28 @@ static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
     return 0;
 }
 
+/* Units of 1-6, 8 or 10 macro steps (the trunk's shapes give 2, 5 and 10)
+ * run the straight-line kernel for bf16 x; any other length, and f32 x, the
+ * ring kernel. Thirteen-bit indices hold plane bytes too, so their
+ * straight-line units stop at 8 steps (10 would spill). */
+template <int NST, int XF32, int EXT>
+static int launch_ms(const FastArgs & A, int MS, int grid, int threads, size_t lds, hipStream_t s) {
+    if constexpr (!XF32) {
+        switch (MS) {
+            case 1: return launch_fast_t<NST, 0, EXT, 1>(A, grid, threads, lds, s);
+            case 2: return launch_fast_t<NST, 0, EXT, 2>(A, grid, threads, lds, s);
+            case 3: return launch_fast_t<NST, 0, EXT, 3>(A, grid, threads, lds, s);
+            case 4: return launch_fast_t<NST, 0, EXT, 4>(A, grid, threads, lds, s);
+            case 5: return launch_fast_t<NST, 0, EXT, 5>(A, grid, threads, lds, s);
+            case 6: return launch_fast_t<NST, 0, EXT, 6>(A, grid, threads, lds, s);
+            case 8: return launch_fast_t<NST, 0, EXT, 8>(A, grid, threads, lds, s);
+            case 10: if (!EXT) return launch_fast_t<NST, 0, EXT, EXT ? 0 : 10>(A, grid, threads, lds, s); break;
+            default: break;
+        }
+    }
+    return launch_fast_t<NST, XF32, EXT, 0>(A, grid, threads, lds, s);
+}
+
 static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
     const Layout L0 = make_layout(c.dim, c.nc, c.mats[0].rows, c.cols, 1);
     const int ext = L0.nbit > 12;
@@ -628,25 +694,21 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
         wg += A.mat[m].nwg;
     }
     const int threads = sh.W * 64;
-    const int MS = A.M / sh.S / sh.C;
-    const int key = (nst == 2 ? 4 : 0) | (c.xf32 ? 2 : 0) | (ext ? 1 : 0);
-#define FAST_D(D)                                                                   \
-    switch (key) {                                                                  \
-        case 0: return launch_fast_t<1, 0, 0, D>(A, wg, threads, sh.lds, c.stream); \
-        case 1: return launch_fast_t<1, 0, 1, D>(A, wg, threads, sh.lds, c.stream); \
-        case 2: return launch_fast_t<1, 1, 0, D>(A, wg, threads, sh.lds, c.stream); \
-        case 3: return launch_fast_t<1, 1, 1, D>(A, wg, threads, sh.lds, c.stream); \
-        case 4: return launch_fast_t<2, 0, 0, D>(A, wg, threads, sh.lds, c.stream); \
-        case 5: return launch_fast_t<2, 0, 1, D>(A, wg, threads, sh.lds, c.stream); \
-        case 6: return launch_fast_t<2, 1, 0, D>(A, wg, threads, sh.lds, c.stream); \
-        default: return launch_fast_t<2, 1, 1, D>(A, wg, threads, sh.lds, c.stream); \
+    /* the straight-line kernels stage in one branch-free pass: one column, an
+     * even codebook, at most 8 chunks and words per thread */
+    const int n16 = c.nc * 8 / 16, xpr = c.xf32 ? c.cols : c.cols / 2;
+    const int one_pass = c.ncol == 1 && c.nc % 2 == 0 && nst * n16 <= 8 * threads && xpr <= 8 * threads;
+    const int MS = one_pass ? A.M / sh.S / sh.C : 0;
+    if (nst == 2) {
+        if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
+                               : launch_ms<2, 1, 0>(A, MS, wg, threads, sh.lds, c.stream);
+        return ext ? launch_ms<2, 0, 1>(A, MS, wg, threads, sh.lds, c.stream)
+                   : launch_ms<2, 0, 0>(A, MS, wg, threads, sh.lds, c.stream);
     }
-    /* ring depth: the whole unit in one round when it has at most 12 steps
-     * (8 with the plane bytes of 13-bit indices, which would spill at 12) */
-    if (MS <= 4) FAST_D(4)
-    if (MS <= 8 || ext) FAST_D(8)
-    FAST_D(12)
-#undef FAST_D
+    if (c.xf32) return ext ? launch_ms<1, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
+                           : launch_ms<1, 1, 0>(A, MS, wg, threads, sh.lds, c.stream);
+    return ext ? launch_ms<1, 0, 1>(A, MS, wg, threads, sh.lds, c.stream)
+               : launch_ms<1, 0, 0>(A, MS, wg, threads, sh.lds, c.stream);
 }
 
 static int launch_wave(const VqCall & c, int variant) {
@@ -703,6 +765,8 @@ int vq_launch(const VqCall & c) {
         }
         if (!fast_geometry_ok(c.dim, c.nc, c.mats[m].rows, c.cols, c.v3)) all_fast = 0;
     }
+    /* the block kernel reads bf16 x in aligned pairs */
+    if (!c.xf32 && (((uintptr_t) c.x & 3u) || (c.ncol > 1 && (c.ldx & 1)))) all_fast = 0;
     if (all_fast) {
         /* the block kernel also needs its codebooks and x resident in LDS */
         FastShape sh;
