@@ -168,6 +168,11 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
      * its own index words (a loop would make the compiler wait for all of a
      * wave's loads at its head). MSC == 0: any unit length, a ring of D steps. */
     constexpr int D = MSC > 0 ? MSC : 8;
+    /* straight-line units keep at most kLook macro steps of index words in
+     * flight per wave: with every step requested up front the memory system
+     * serves some CUs' words last, and those CUs then do their whole unit
+     * after the stream has ended */
+    constexpr int kLook = 3;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) A.nc * 8u;
     uint8_t * lx = lds + NST * cbb;
@@ -211,6 +216,12 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     auto ld_all = [&]() {
 #pragma unroll
         for (int u = 0; u < D; u++) ld(w[u], u);
+    };
+    /* the first kLook steps of a straight-line unit (all D of a ring) */
+    auto ld_head = [&]() {
+#pragma unroll
+        for (int u = 0; u < D; u++)
+            if (MSC == 0 || u < kLook) ld(w[u], u);
     };
     auto point = [&](int tile) {
         const int row = min(tile * rpt + r_in, rows - 1);
@@ -280,21 +291,32 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     constexpr int K = 8;
     const int bd = blockDim.x, tid = threadIdx.x;
     if constexpr (MSC > 0) {
-        /* One activation column, an even codebook, and at most K staging
-         * chunks and words per thread (the host checks all three). Threads
+        /* One 16-byte aligned activation column of at most 16 * blockDim
+         * columns, an even codebook of at most K chunks per thread (the host
+         * checks all of it). Threads
          * past the end load and store the last chunk or word again (one cache
          * line per wave, the same bytes to the same place), so the prologue
          * has no branches and the compiler counts every load exactly. */
-        uint32_t cv[K][4], xv[K];
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        constexpr int KX = 2;                      /* 16-byte x chunks (8 columns) per thread */
+        const int xq = A.cols >> 3;
+        uint32_t cv[K][4];
+        u4v xv[KX];
 #pragma unroll
         for (int k = 0; k < K; k++) {
             const int i = k * bd + tid;
             cb_load(rot_chunk(min(i, ncb - 1)), cv[k]);
-            xv[k] = x_load(0, min(i, xpr - 1));
+            if (k < KX) xv[k] = ((const u4v *) A.x)[min(i, xq - 1)];
         }
+        /* every wave's staging requests enter the CU's memory pipeline
+         * before any wave's index stream (which would otherwise hold them
+         * up behind the unit's bulk): an execution barrier, no wait */
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
         point(first);
-        ld_all();
         ld_gains(first);
+        ld_head();
         /* keep the scheduler from pulling stores (and their waits) up
          * between the loads */
         __builtin_amdgcn_sched_barrier(0);
@@ -302,7 +324,22 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         for (int k = 0; k < K; k++) {
             const int i = k * bd + tid;
             cb_store(rot_chunk(min(i, ncb - 1)), cv[k]);
-            x_store(0, min(i, xpr - 1), xv[k]);
+            if (k < KX) {
+                /* eight bf16 columns -> eight f16 in the padded layout */
+                const int e = 8 * min(i, xq - 1);
+                uint8_t * dst = lx + 264 * (e >> 7) + 2 * (e & 127);
+                h4 lo4, hi4;
+                lo4[0] = (_Float16) __uint_as_float(xv[k].x << 16);
+                lo4[1] = (_Float16) __uint_as_float(xv[k].x & 0xffff0000u);
+                lo4[2] = (_Float16) __uint_as_float(xv[k].y << 16);
+                lo4[3] = (_Float16) __uint_as_float(xv[k].y & 0xffff0000u);
+                hi4[0] = (_Float16) __uint_as_float(xv[k].z << 16);
+                hi4[1] = (_Float16) __uint_as_float(xv[k].z & 0xffff0000u);
+                hi4[2] = (_Float16) __uint_as_float(xv[k].w << 16);
+                hi4[3] = (_Float16) __uint_as_float(xv[k].w & 0xffff0000u);
+                *(h4 *) dst = lo4;
+                *(h4 *) (dst + 8) = hi4;
+            }
         }
     } else {
         for (int base = 0; base < ncb; base += K * bd) {
@@ -345,7 +382,10 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         if (active) {
             if (MSC > 0) {
 #pragma unroll
-                for (int u = 0; u < D; u++) mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc);
+                for (int u = 0; u < D; u++) {
+                    mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc);
+                    if (u + kLook < D) ld(w[u + kLook], u + kLook);
+                }
             } else {
                 for (int ms0 = 0; ms0 < MS; ms0 += D) {
 #pragma unroll
@@ -385,11 +425,24 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
                 const int r = ncol == 1 ? e : e / ncol, col = e - r * ncol;
                 const int row = tile * rpt + r;
                 float sum = 0.0f;
-                for (int hh = 0; hh < S; hh++) {
-                    const float * rr = red + wave * kRedStride + (r * S + hh) * 17 + hh * ncol + col;
-                    float part = rr[0];
-                    for (int cw = 1; cw < C; cw++) part += rr[cw * kRedStride];
-                    sum += part;
+                if (C == 1) {
+                    /* all S reads issued together (parts past S re-read the
+                     * last one and add nothing), added in part order */
+                    float part[16];
+#pragma unroll
+                    for (int hh = 0; hh < 16; hh++) {
+                        const int hc = hh < S ? hh : S - 1;
+                        part[hh] = red[wave * kRedStride + (r * S + hc) * 17 + hc * ncol + col];
+                    }
+#pragma unroll
+                    for (int hh = 0; hh < 16; hh++) sum += hh < S ? part[hh] : 0.0f;
+                } else {
+                    for (int hh = 0; hh < S; hh++) {
+                        const float * rr = red + wave * kRedStride + (r * S + hh) * 17 + hh * ncol + col;
+                        float part = rr[0];
+                        for (int cw = 1; cw < C; cw++) part += rr[cw * kRedStride];
+                        sum += part;
+                    }
                 }
                 if (row < rows) {
                     float * yp = A.mat[mi].y + (size_t) col * A.ldy + row;
@@ -411,8 +464,8 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     for (int it = 1; it < iters; it++) {
         const int tile = t0 + it * T + j;
         point(min(tile, t1 - 1));
-        ld_all();
         ld_gains(min(tile, t1 - 1));
+        ld_head();
         unit(tile);
     }
 }
@@ -694,10 +747,12 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
         wg += A.mat[m].nwg;
     }
     const int threads = sh.W * 64;
-    /* the straight-line kernels stage in one branch-free pass: one column, an
-     * even codebook, at most 8 chunks and words per thread */
-    const int n16 = c.nc * 8 / 16, xpr = c.xf32 ? c.cols : c.cols / 2;
-    const int one_pass = c.ncol == 1 && c.nc % 2 == 0 && nst * n16 <= 8 * threads && xpr <= 8 * threads;
+    /* the straight-line kernels stage in one branch-free pass: one 16-byte
+     * aligned bf16 column of at most 16 * threads values, an even codebook of
+     * at most 8 chunks per thread */
+    const int n16 = c.nc * 8 / 16;
+    const int one_pass = c.ncol == 1 && !c.xf32 && !((uintptr_t) c.x & 15u) && c.nc % 2 == 0 &&
+                         nst * n16 <= 8 * threads && c.cols <= 16 * threads;
     const int MS = one_pass ? A.M / sh.S / sh.C : 0;
     if (nst == 2) {
         if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
