@@ -123,7 +123,7 @@ def time_steps(plan, torch, stream, steps, warmup, mode):
     return start.elapsed_time(end) / steps
 
 
-def cpu_baseline_decode_set(sample_layers=2, head_rows=8192, reps=5):
+def cpu_baseline_decode_set(sample_layers=4, head_rows=16384, reps=9):
     """The oracle's runtime path (model.rs:209-234): containers decoded to f32
     once, then a row-parallel 8-lane dot per matvec, all host threads. Timed
     on a bounded sample (a few layers and a slice of the head) and scaled to
@@ -179,9 +179,12 @@ def bench_decode_set(args, sm, torch, dev):
         g[0] += b
         g[1] += t
         g[2] += 1
+    per_group = {}
     for k, (b, t, n) in groups.items():
-        log(f"  {k:16s} {n:3d} launches  {t / n * 1e3:8.2f} us/launch  {b / (t * 1e-3) / 1e9:8.1f} GB/s")
-    log(f"  step {ms * 1e3:.1f} us ({args.mode}); sum of op times {op_ms.sum() * 1e3:.1f} us")
+        log(f"  {k:16s} {n:3d} launches  {t / n * 1e3:8.2f} us/kernel  {b / (t * 1e-3) / 1e9:8.1f} GB/s")
+        per_group[k] = {"launches": n, "kernel_us": round(t / n * 1e3, 3), "bytes_per_launch": int(b / n),
+                        "gbps": round(b / (t * 1e-3) / 1e9, 1)}
+    log(f"  step {ms * 1e3:.1f} us ({args.mode}); sum of kernel times {op_ms.sum() * 1e3:.1f} us")
     workload = ("36-layer N=8 verify matvec set (trunk + Q8_0 head), weights decoded once per step"
                 if ncol == 8 else "36-layer N=1 decode matvec set + tied Q8_0 head")
     out = {
@@ -204,12 +207,40 @@ def bench_decode_set(args, sm, torch, dev):
         "frac_of_peak": round(total_bytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
         "algorithmic_bytes_per_step": int(total_bytes),
         "roofline": {"bound": "hbm", "kernel": "vq_mfma_kernel", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": recorded_traffic(ncol),
                      "bytes_per_launch": round(vq_bytes / n_vq), "avg_launch_us": round(vq_ms / n_vq * 1e3, 3),
+                     "timing": "kernel-exact: start/stop events carried by each dispatch (hipExtLaunchKernel) on the "
+                               "launch stream, averaged over eager runs of the plan",
+                     "per_group": per_group,
                      "head_q8_0": {"us": round(head_ms * 1e3, 2),
                                    "gbps": round(float(op_bytes[~vq].sum()) / (head_ms * 1e-3) / 1e9, 1)}},
     }
     return out
+
+
+def recorded_traffic(ncol):
+    """HBM bytes per VQ launch measured by rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE in separate runs, each scaled by the same counter's reading
+    for a copy of known size); the summary file under profiles/ says how."""
+    path = os.path.join(ROOT, "profiles", "traffic_decode-set.json")
+    if ncol != 1 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    return rec.get("vq_bytes_per_launch")
+
+
+def copy_calibration(torch, dev, mib):
+    """A plain device copy of `mib` MiB (read mib, write mib), run a few
+    times so a counter run sees a kernel of known traffic."""
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {mib} MiB copied 3 times")
 
 
 def bench_single(args, sm, torch, dev):
@@ -253,6 +284,8 @@ def main():
                     choices=["decode-set", "verify8", "ffn-up", "q6k-down"])
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB on the device (for counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the matvec path runs on a single MI355X, and "
@@ -267,6 +300,8 @@ def main():
     dev = torch.device("cuda:0")
     name = torch.cuda.get_device_name(0)
     log(f"device {name}")
+    if args.calibrate_copy:
+        copy_calibration(torch, dev, args.calibrate_copy)
     if args.workload in ("decode-set", "verify8"):
         out = bench_decode_set(args, sm, torch, dev)
         if not args.no_cpu_baseline and args.workload == "decode-set":

@@ -195,8 +195,10 @@ int sparkmv_plan_run(void * plan, void * stream);
 /* Capture on a created (non-null) stream; run the plan eagerly once first. */
 int sparkmv_plan_capture(void * plan, void * stream);
 int sparkmv_plan_launch(void * plan, void * stream);
-/* Average device milliseconds of each op over `iters` eager runs, timed with
- * events on `stream`; op_ms receives sparkmv_plan_size(plan) values. */
+/* Average device milliseconds of each op over `iters` eager runs on `stream`:
+ * the op's kernels carry start/stop events in their own dispatches
+ * (hipExtLaunchKernel), so each figure is kernel time without launch gaps;
+ * op_ms receives sparkmv_plan_size(plan) values. */
 int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms);
 
 /* ---- synthetic workloads (host memory; no reference counterpart) ----

@@ -22,6 +22,9 @@
 
 namespace sparkmv {
 
+thread_local LaunchEvents g_launch_events;
+
+
 static char g_err[512];
 
 void set_error(const char * fmt, ...) {

@@ -15,6 +15,7 @@
  */
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -64,6 +65,26 @@ int fail_hip(const char * what, hipError_t e);
 
 /* Device properties cached per device. */
 int cu_count();
+
+/* Kernel-exact timing. While `stop` is set (the plan's timing pass sets it
+ * around one op), hot-path launches carry the events in the dispatch itself
+ * (hipExtLaunchKernel): `start` is recorded as the op's first kernel begins
+ * and `stop` as its last one ends, so their difference is device time with
+ * no launch gap in it. */
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchEvents g_launch_events;
+
+template <typename F, typename... Args>
+inline void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Args... args) {
+    if (g_launch_events.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, s, g_launch_events.start, g_launch_events.stop, 0, args...);
+        g_launch_events.start = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+    }
+}
 
 constexpr int kMaxStages = 4;   /* residual stages one fused launch accepts */
 constexpr int kMaxCols = 16;    /* activation columns one batched launch accepts (the MFMA N width) */

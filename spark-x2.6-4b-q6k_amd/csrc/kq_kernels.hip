@@ -283,8 +283,8 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
     const int cap = cu_count() * 16;
     if (grid > cap) grid = cap;
     const uint8_t * bp = (const uint8_t *) blocks;
-#define KQ_LAUNCH(K, NC, XF) hipLaunchKernelGGL((K<NC, XF>), dim3(grid), dim3(threads), lds, s, bp, rows, cols, x, \
-                                                ldx, ncol, y, ldy, accumulate)
+#define KQ_LAUNCH(K, NC, XF) launch_kernel(K<NC, XF>, dim3(grid), dim3(threads), (uint32_t) lds, s, bp, rows, cols, x, \
+                                           ldx, ncol, y, ldy, accumulate)
 #define KQ_PICK(K, XF)                          \
     do {                                        \
         if (ncol == 1) KQ_LAUNCH(K, 1, XF);     \

@@ -159,15 +159,17 @@ int sparkmv_plan_launch(void * plan, void * stream) {
     return e == hipSuccess ? 0 : fail_hip("graph launch", e);
 }
 
-/* Average device time of every op over `iters` eager runs, events recorded on
- * `stream` around each launch; op_ms holds plan_size entries. */
+/* Average device time of every op over `iters` eager runs: each op's
+ * kernels carry a start and a stop event in their own dispatches, so an op's
+ * time is its kernels' duration without the launch gap between ops. op_ms
+ * holds plan_size entries. */
 int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms) {
     Plan * p = (Plan *) plan;
     if (!p || !op_ms || iters < 1) { set_error("plan timing needs a plan, an output array and iters >= 1"); return -1; }
     hipStream_t s = (hipStream_t) stream;
     const size_t n = p->ops.size();
-    std::vector<hipEvent_t> ev(n + 1);
-    for (size_t i = 0; i <= n; i++) {
+    std::vector<hipEvent_t> ev(2 * n);
+    for (size_t i = 0; i < 2 * n; i++) {
         hipError_t e = hipEventCreate(&ev[i]);
         if (e != hipSuccess) {
             for (size_t j = 0; j < i; j++) hipEventDestroy(ev[j]);
@@ -178,19 +180,21 @@ int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms)
     int rc = 0;
     for (int it = 0; it < iters && !rc; it++) {
         for (size_t i = 0; i < n && !rc; i++) {
-            hipEventRecord(ev[i], s);
+            g_launch_events.start = ev[2 * i];
+            g_launch_events.stop = ev[2 * i + 1];
             rc = run_op(p->ops[i], s);
+            g_launch_events = LaunchEvents();
         }
-        hipEventRecord(ev[n], s);
-        hipError_t e = hipEventSynchronize(ev[n]);
+        hipError_t e = n ? hipEventSynchronize(ev[2 * n - 1]) : hipSuccess;
         if (!rc && e != hipSuccess) rc = fail_hip("op timing", e);
         for (size_t i = 0; i < n && !rc; i++) {
             float t = 0;
-            hipEventElapsedTime(&t, ev[i], ev[i + 1]);
+            e = hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]);
+            if (e != hipSuccess) { rc = fail_hip("op timing", e); break; }
             op_ms[i] += t / iters;
         }
     }
-    for (size_t i = 0; i <= n; i++) hipEventDestroy(ev[i]);
+    for (size_t i = 0; i < 2 * n; i++) hipEventDestroy(ev[i]);
     return rc;
 }
 

@@ -288,7 +288,9 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         }
     };
     const int first = min(t0 + j, t1 - 1);
-    constexpr int K = 8;
+    /* staging chunks per thread: two 32 KB codebooks are 4096 chunks, which
+     * 10 loads per thread cover from seven waves up */
+    constexpr int K = 10;
     const int bd = blockDim.x, tid = threadIdx.x;
     if constexpr (MSC > 0) {
         /* One 16-byte aligned activation column of at most 16 * blockDim
@@ -624,7 +626,7 @@ static int launch_fast_t(const FastArgs & A, int grid, int threads, size_t lds, 
         if (e != hipSuccess) return fail_hip("LDS opt-in for the VQ block kernel", e);
         opted = lds;
     }
-    hipLaunchKernelGGL((vq_mfma_kernel<NST, XF32, EXT, MSC>), dim3(grid), dim3(threads), lds, s, A);
+    launch_kernel(vq_mfma_kernel<NST, XF32, EXT, MSC>, dim3(grid), dim3(threads), (uint32_t) lds, s, A);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip("VQ block kernel launch", e);
     return 0;
@@ -749,10 +751,10 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
     const int threads = sh.W * 64;
     /* the straight-line kernels stage in one branch-free pass: one 16-byte
      * aligned bf16 column of at most 16 * threads values, an even codebook of
-     * at most 8 chunks per thread */
+     * at most 10 chunks per thread */
     const int n16 = c.nc * 8 / 16;
     const int one_pass = c.ncol == 1 && !c.xf32 && !((uintptr_t) c.x & 15u) && c.nc % 2 == 0 &&
-                         nst * n16 <= 8 * threads && c.cols <= 16 * threads;
+                         nst * n16 <= 10 * threads && c.cols <= 16 * threads;
     const int MS = one_pass ? A.M / sh.S / sh.C : 0;
     if (nst == 2) {
         if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
@@ -779,10 +781,10 @@ static int launch_wave(const VqCall & c, int variant) {
             const int acc = s > 0 || c.accumulate;
             const uint8_t * p = (const uint8_t *) c.mats[m].stages[s];
             if (variant == 2)
-                hipLaunchKernelGGL(vq_wave_kernel<1>, dim3(grid), dim3(threads), lds, c.stream, p, L, c.x, c.ldx,
+                launch_kernel(vq_wave_kernel<1>, dim3(grid), dim3(threads), (uint32_t) lds, c.stream, p, L, c.x, c.ldx,
                                    c.xf32, c.ncol, c.mats[m].y, c.ldy, acc);
             else
-                hipLaunchKernelGGL(vq_wave_kernel<0>, dim3(grid), dim3(threads), 0, c.stream, p, L, c.x, c.ldx,
+                launch_kernel(vq_wave_kernel<0>, dim3(grid), dim3(threads), 0u, c.stream, p, L, c.x, c.ldx,
                                    c.xf32, c.ncol, c.mats[m].y, c.ldy, acc);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return fail_hip("VQ wave kernel launch", e);
