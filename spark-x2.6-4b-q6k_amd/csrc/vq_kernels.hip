@@ -294,22 +294,25 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     const int bd = blockDim.x, tid = threadIdx.x;
     if constexpr (MSC > 0) {
         /* One 16-byte aligned activation column of at most 16 * blockDim
-         * columns, an even codebook of at most K chunks per thread (the host
-         * checks all of it). Threads
-         * past the end load and store the last chunk or word again (one cache
-         * line per wave, the same bytes to the same place), so the prologue
-         * has no branches and the compiler counts every load exactly. */
+         * columns and an even codebook of at most KS chunks per thread and
+         * stage (the host checks both). Threads past the end load and store
+         * the last chunk again (one cache line per wave, the same bytes to the
+         * same place), so the prologue has no branches and the compiler
+         * counts every load exactly. */
         typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));   /* codebooks are 4-byte aligned */
         constexpr int KX = 2;                      /* 16-byte x chunks (8 columns) per thread */
+        constexpr int KS = 5;                      /* 16-byte codebook chunks per thread and stage */
         const int xq = A.cols >> 3;
-        uint32_t cv[K][4];
+        u4v cv[NST][KS];
         u4v xv[KX];
 #pragma unroll
-        for (int k = 0; k < K; k++) {
-            const int i = k * bd + tid;
-            cb_load(rot_chunk(min(i, ncb - 1)), cv[k]);
-            if (k < KX) xv[k] = ((const u4v *) A.x)[min(i, xq - 1)];
-        }
+        for (int s = 0; s < NST; s++)
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+                cv[s][k] = ((const u4a *) (stp[s] + 24))[min(k * bd + tid, n16 - 1)];
+#pragma unroll
+        for (int k = 0; k < KX; k++) xv[k] = ((const u4v *) A.x)[min(k * bd + tid, xq - 1)];
         /* every wave's staging requests enter the CU's memory pipeline
          * before any wave's index stream (which would otherwise hold them
          * up behind the unit's bulk): an execution barrier, no wait */
@@ -323,10 +326,14 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
          * between the loads */
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < K; k++) {
+        for (int s = 0; s < NST; s++)
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+                ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+#pragma unroll
+        for (int k = 0; k < KX; k++) {
             const int i = k * bd + tid;
-            cb_store(rot_chunk(min(i, ncb - 1)), cv[k]);
-            if (k < KX) {
+            {
                 /* eight bf16 columns -> eight f16 in the padded layout */
                 const int e = 8 * min(i, xq - 1);
                 uint8_t * dst = lx + 264 * (e >> 7) + 2 * (e & 127);
@@ -402,6 +409,37 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         /* stages combine with their row gains; entry C[4q + i][m16] of this
          * lane goes to the wave's reduction area */
         float * R = red + wave * kRedStride;
+        if constexpr (MSC > 0) {
+            /* one activation column and one wave per tile: row r of the tile
+             * is the sum of C[r*S + h][h] over parts h, read back by lane r.
+             * A wave's LDS operations complete in order, so no barrier. */
+            if (active) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int s = 0; s < NST; s++) v += f16_to_f32((uint16_t) gw[s][i]) * acc[s][i];
+                    R[(4 * q + i) * 17 + m16] = v;
+                }
+                if (lane < rpt) {
+                    float part[16];
+#pragma unroll
+                    for (int hh = 0; hh < 16; hh++) {
+                        const int hc = hh < S ? hh : S - 1;
+                        part[hh] = R[(lane * S + hc) * 17 + hc];
+                    }
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int hh = 0; hh < 16; hh++) sum += hh < S ? part[hh] : 0.0f;
+                    const int row = tile * rpt + lane;
+                    if (row < rows) {
+                        float * yp = A.mat[mi].y + row;
+                        *yp = (A.accumulate ? *yp : 0.0f) + sum;
+                    }
+                }
+            }
+            return;
+        }
         if (active) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -749,12 +787,13 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
         wg += A.mat[m].nwg;
     }
     const int threads = sh.W * 64;
-    /* the straight-line kernels stage in one branch-free pass: one 16-byte
-     * aligned bf16 column of at most 16 * threads values, an even codebook of
-     * at most 10 chunks per thread */
+    /* the straight-line kernels stage in one branch-free pass and reduce
+     * within a wave: one 16-byte aligned bf16 column of at most 16 * threads
+     * values, one wave per tile, an even codebook of at most 5 chunks per
+     * thread and stage */
     const int n16 = c.nc * 8 / 16;
-    const int one_pass = c.ncol == 1 && !c.xf32 && !((uintptr_t) c.x & 15u) && c.nc % 2 == 0 &&
-                         nst * n16 <= 10 * threads && c.cols <= 16 * threads;
+    const int one_pass = c.ncol == 1 && sh.C == 1 && !c.xf32 && !((uintptr_t) c.x & 15u) && c.nc % 2 == 0 &&
+                         n16 <= 5 * threads && c.cols <= 16 * threads;
     const int MS = one_pass ? A.M / sh.S / sh.C : 0;
     if (nst == 2) {
         if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
