@@ -70,7 +70,6 @@ struct FastMat {
 };
 
 struct FastArgs {
-    FastMat mat[kMaxMats];
     const void * x;
     int nmat, cols, nc, ncol, ldx, ldy, accumulate;
     uint32_t gain_off;   /* 24 + nc * 8: the same for every matrix of a launch */
@@ -78,7 +77,11 @@ struct FastArgs {
     int lgS, C, T;       /* log2 of the parts per MFMA, wave chunks per tile, tiles per workgroup pass */
     int M;               /* 32-index macro steps per row */
     int xstride;         /* LDS bytes per activation column: 264 per 128 columns, plus 8 */
+    int threads;         /* the launch width, so the kernel does not wait for the hidden argument */
+    FastMat mat[4];      /* a launch of more matrices is split into launches of 4 */
 };
+
+constexpr int kFastMats = 4;
 
 constexpr int kRedStride = 16 * 17;   /* floats per wave of the LDS reduction area */
 
@@ -179,12 +182,25 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     float * red = (float *) (lx + (XF32 ? 2 : 1) * A.ncol * A.xstride);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m16 = lane & 15, q = lane >> 4;
-    int mi = 0;
-    while (mi + 1 < A.nmat && (int) blockIdx.x >= A.mat[mi + 1].wg0) mi++;
-    const int rows = A.mat[mi].rows;
-    const uint32_t tiles = (uint32_t) A.mat[mi].tiles, nwg = (uint32_t) A.mat[mi].nwg;
-    const uint32_t wl = blockIdx.x - (uint32_t) A.mat[mi].wg0;
-    const int t0 = (int) (tiles * wl / nwg), t1 = (int) (tiles * (wl + 1) / nwg);
+    /* the workgroup's matrix: every record is read at once (independent
+     * scalar loads) and the one owning this workgroup selected, so no load
+     * waits for another before the staging loads can go out */
+    FastMat M;
+    M.st[0] = A.mat[0].st[0]; M.st[1] = A.mat[0].st[1]; M.y = A.mat[0].y;
+    M.rows = A.mat[0].rows; M.tiles = A.mat[0].tiles; M.wg0 = A.mat[0].wg0; M.nwg = A.mat[0].nwg;
+#pragma unroll
+    for (int k = 1; k < kFastMats; k++) {
+        const bool take = k < A.nmat && (int) blockIdx.x >= A.mat[k].wg0;
+        M.st[0] = take ? A.mat[k].st[0] : M.st[0];
+        M.st[1] = take ? A.mat[k].st[1] : M.st[1];
+        M.y = take ? A.mat[k].y : M.y;
+        M.rows = take ? A.mat[k].rows : M.rows;
+        M.tiles = take ? A.mat[k].tiles : M.tiles;
+        M.wg0 = take ? A.mat[k].wg0 : M.wg0;
+    }
+    const int rows = M.rows;
+    /* T consecutive tiles per workgroup (the host sized nwg = ceil(tiles / T)) */
+    const int t0 = ((int) blockIdx.x - M.wg0) * A.T, t1 = min(t0 + A.T, M.tiles);
     const int S = 1 << A.lgS, C = A.C, T = A.T, ncol = A.ncol;
     const int rpt = 16 >> A.lgS;                   /* rows per tile */
     const int j = wave / C, c = wave - j * C;      /* tile slot, K chunk */
@@ -205,7 +221,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     /* the matrix's stage payloads, read once (uniform) */
     const uint8_t * stp[NST];
 #pragma unroll
-    for (int s = 0; s < NST; s++) stp[s] = A.mat[mi].st[s];
+    for (int s = 0; s < NST; s++) stp[s] = M.st[s];
     const uint8_t * rp[NST];
     const uint8_t * pp[NST];
     /* index words of D macro steps; every load is issued unconditionally
@@ -291,7 +307,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     /* staging chunks per thread: two 32 KB codebooks are 4096 chunks, which
      * 10 loads per thread cover from seven waves up */
     constexpr int K = 10;
-    const int bd = blockDim.x, tid = threadIdx.x;
+    const int bd = A.threads, tid = threadIdx.x;
     if constexpr (MSC > 0) {
         /* One 16-byte aligned activation column of at most 16 * blockDim
          * columns and an even codebook of at most KS chunks per thread and
@@ -433,7 +449,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
                     for (int hh = 0; hh < 16; hh++) sum += hh < S ? part[hh] : 0.0f;
                     const int row = tile * rpt + lane;
                     if (row < rows) {
-                        float * yp = A.mat[mi].y + row;
+                        float * yp = M.y + row;
                         *yp = (A.accumulate ? *yp : 0.0f) + sum;
                     }
                 }
@@ -485,7 +501,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
                     }
                 }
                 if (row < rows) {
-                    float * yp = A.mat[mi].y + (size_t) col * A.ldy + row;
+                    float * yp = M.y + (size_t) col * A.ldy + row;
                     *yp = (A.accumulate ? *yp : 0.0f) + sum;
                 }
             }
@@ -787,6 +803,7 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
         wg += A.mat[m].nwg;
     }
     const int threads = sh.W * 64;
+    A.threads = threads;
     /* the straight-line kernels stage in one branch-free pass and reduce
      * within a wave: one 16-byte aligned bf16 column of at most 16 * threads
      * values, one wave per tile, an even codebook of at most 5 chunks per
@@ -865,9 +882,14 @@ int vq_launch(const VqCall & c) {
     if (!c.xf32 && (((uintptr_t) c.x & 3u) || (c.ncol > 1 && (c.ldx & 1)))) all_fast = 0;
     if (all_fast) {
         /* the block kernel also needs its codebooks and x resident in LDS */
-        FastShape sh;
         const int nst = c.nst < 2 ? c.nst : 2;
-        if (fast_shape(c, nst, sh) || sh.lds > (size_t) kLdsMax) all_fast = 0;
+        for (int m0 = 0; m0 < c.nmat && all_fast; m0 += kFastMats) {
+            VqCall part = c;
+            part.mats = c.mats + m0;
+            part.nmat = c.nmat - m0 < kFastMats ? c.nmat - m0 : kFastMats;
+            FastShape sh;
+            if (fast_shape(part, nst, sh) || sh.lds > (size_t) kLdsMax) all_fast = 0;
+        }
     }
     int variant = c.variant;
     if (variant == 0) variant = all_fast ? 3 : ((size_t) c.nc * c.dim * 2 <= 65536 ? 2 : 1);
@@ -876,9 +898,14 @@ int vq_launch(const VqCall & c) {
             set_error("the VQ block kernel does not take this geometry, alignment or LDS footprint");
             return -1;
         }
-        for (int st0 = 0; st0 < c.nst; st0 += 2) {
-            const int n = c.nst - st0 < 2 ? c.nst - st0 : 2;
-            if (launch_fast(c, st0, n, st0 > 0 || c.accumulate)) return -1;
+        for (int m0 = 0; m0 < c.nmat; m0 += kFastMats) {
+            VqCall part = c;
+            part.mats = c.mats + m0;
+            part.nmat = c.nmat - m0 < kFastMats ? c.nmat - m0 : kFastMats;
+            for (int st0 = 0; st0 < c.nst; st0 += 2) {
+                const int n = c.nst - st0 < 2 ? c.nst - st0 : 2;
+                if (launch_fast(part, st0, n, st0 > 0 || c.accumulate)) return -1;
+            }
         }
         return 0;
     }
