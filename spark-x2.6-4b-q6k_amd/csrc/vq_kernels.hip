@@ -78,6 +78,7 @@ struct FastArgs {
     int M;               /* 32-index macro steps per row */
     int xstride;         /* LDS bytes per activation column: 264 per 128 columns, plus 8 */
     int threads;         /* the launch width, so the kernel does not wait for the hidden argument */
+    int kofs;            /* first macro step of this launch in every row (a K-split launch) */
     FastMat mat[4];      /* a launch of more matrices is split into launches of 4 */
 };
 
@@ -164,12 +165,13 @@ __device__ __forceinline__ void mstep(const Words<NST, EXT> & W, const uint8_t *
     }
 }
 
-template <int NST, int XF32, int EXT, int MSC>
+template <int NST, int XF32, int EXT, int MSC, int MC>
 __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
     /* MSC > 0: a unit is exactly MSC macro steps, known at compile time, so
      * the whole unit runs as straight-line code and each step waits only for
      * its own index words (a loop would make the compiler wait for all of a
-     * wave's loads at its head). MSC == 0: any unit length, a ring of D steps. */
+     * wave's loads at its head). MSC == 0: any unit length, a ring of D steps.
+     * MC: the straight-line kernel for several activation columns. */
     constexpr int D = MSC > 0 ? MSC : 8;
     /* straight-line units keep at most kLook macro steps of index words in
      * flight per wave: with every step requested up front the memory system
@@ -244,8 +246,8 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
 #pragma unroll
         for (int s = 0; s < NST; s++) {
             const uint8_t * sb = stp[s] + stream_off;
-            rp[s] = sb + (size_t) row * A.mrow + 48 * msa + 12 * q;
-            pp[s] = sb + (size_t) rows * A.mrow + (size_t) row * A.prow + 4 * msa + q;
+            rp[s] = sb + (size_t) row * A.mrow + 48 * (A.kofs + msa) + 12 * q;
+            pp[s] = sb + (size_t) rows * A.mrow + (size_t) row * A.prow + 4 * (A.kofs + msa) + q;
         }
     };
     /* gains of the rows this lane's C entries belong to, per stage */
@@ -308,7 +310,59 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
      * 10 loads per thread cover from seven waves up */
     constexpr int K = 10;
     const int bd = A.threads, tid = threadIdx.x;
-    if constexpr (MSC > 0) {
+    if constexpr (MC) {
+        /* Several activation columns (speculative verify): codebooks and x
+         * are staged in batches of unconditional 16-byte loads (indices past
+         * the end re-read the last chunk), then the unit's index words are
+         * requested. The host sends 16-byte aligned x with ldx % 8 == 0 and
+         * at most 5 codebook chunks per thread and stage. */
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
+        constexpr int KS = 5, KXM = 8;
+        {
+            u4v cv[NST][KS];
+#pragma unroll
+            for (int s = 0; s < NST; s++)
+#pragma unroll
+                for (int k = 0; k < KS; k++)
+                    cv[s][k] = ((const u4a *) (stp[s] + 24))[min(k * bd + tid, n16 - 1)];
+#pragma unroll
+            for (int s = 0; s < NST; s++)
+#pragma unroll
+                for (int k = 0; k < KS; k++)
+                    ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+        }
+        const int xq = A.cols >> 3, nx = ncol * xq;
+        for (int base = 0; base < nx; base += KXM * bd) {
+            u4v xv[KXM];
+            int ci[KXM];
+#pragma unroll
+            for (int k = 0; k < KXM; k++) {
+                ci[k] = min(base + k * bd + tid, nx - 1);
+                const int n = ci[k] / xq, cc = ci[k] - n * xq;
+                xv[k] = *(const u4v *) ((const uint16_t *) A.x + (size_t) n * A.ldx + 8 * cc);
+            }
+#pragma unroll
+            for (int k = 0; k < KXM; k++) {
+                const int n = ci[k] / xq, e = 8 * (ci[k] - n * xq);
+                uint8_t * dst = lx + n * A.xstride + 264 * (e >> 7) + 2 * (e & 127);
+                h4 lo4, hi4;
+                lo4[0] = (_Float16) __uint_as_float(xv[k].x << 16);
+                lo4[1] = (_Float16) __uint_as_float(xv[k].x & 0xffff0000u);
+                lo4[2] = (_Float16) __uint_as_float(xv[k].y << 16);
+                lo4[3] = (_Float16) __uint_as_float(xv[k].y & 0xffff0000u);
+                hi4[0] = (_Float16) __uint_as_float(xv[k].z << 16);
+                hi4[1] = (_Float16) __uint_as_float(xv[k].z & 0xffff0000u);
+                hi4[2] = (_Float16) __uint_as_float(xv[k].w << 16);
+                hi4[3] = (_Float16) __uint_as_float(xv[k].w & 0xffff0000u);
+                *(h4 *) dst = lo4;
+                *(h4 *) (dst + 8) = hi4;
+            }
+        }
+        point(first);
+        ld_gains(first);
+        ld_head();
+    } else if constexpr (MSC > 0) {
         /* One 16-byte aligned activation column of at most 16 * blockDim
          * columns and an even codebook of at most KS chunks per thread and
          * stage (the host checks both). Threads past the end load and store
@@ -425,7 +479,7 @@ __global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
         /* stages combine with their row gains; entry C[4q + i][m16] of this
          * lane goes to the wave's reduction area */
         float * R = red + wave * kRedStride;
-        if constexpr (MSC > 0) {
+        if constexpr (MSC > 0 && !MC) {
             /* one activation column and one wave per tile: row r of the tile
              * is the sum of C[r*S + h][h] over parts h, read back by lane r.
              * A wave's LDS operations complete in order, so no barrier. */
@@ -671,16 +725,16 @@ int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
 
 static int aligned4(const void * p) { return ((uintptr_t) p & 3u) == 0; }
 
-template <int NST, int XF32, int EXT, int MSC>
+template <int NST, int XF32, int EXT, int MSC, int MC = 0>
 static int launch_fast_t(const FastArgs & A, int grid, int threads, size_t lds, hipStream_t s) {
     static size_t opted = 0;
-    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, MSC>;
+    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, MSC, MC>;
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the VQ block kernel", e);
         opted = lds;
     }
-    launch_kernel(vq_mfma_kernel<NST, XF32, EXT, MSC>, dim3(grid), dim3(threads), (uint32_t) lds, s, A);
+    launch_kernel(vq_mfma_kernel<NST, XF32, EXT, MSC, MC>, dim3(grid), dim3(threads), (uint32_t) lds, s, A);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip("VQ block kernel launch", e);
     return 0;
@@ -748,8 +802,18 @@ static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
  * ring kernel. Thirteen-bit indices hold plane bytes too, so their
  * straight-line units stop at 8 steps (10 would spill). */
 template <int NST, int XF32, int EXT>
-static int launch_ms(const FastArgs & A, int MS, int grid, int threads, size_t lds, hipStream_t s) {
+static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, size_t lds, hipStream_t s) {
     if constexpr (!XF32) {
+        if (mc) {
+            /* several columns: the unit lengths of the trunk's verify shapes */
+            switch (MS) {
+                case 2: return launch_fast_t<NST, 0, EXT, 2, 1>(A, grid, threads, lds, s);
+                case 5: return launch_fast_t<NST, 0, EXT, 5, 1>(A, grid, threads, lds, s);
+                case 10: if (!EXT) return launch_fast_t<NST, 0, EXT, EXT ? 0 : 10, 1>(A, grid, threads, lds, s); break;
+                default: break;
+            }
+            return launch_fast_t<NST, XF32, EXT, 0>(A, grid, threads, lds, s);
+        }
         switch (MS) {
             case 1: return launch_fast_t<NST, 0, EXT, 1>(A, grid, threads, lds, s);
             case 2: return launch_fast_t<NST, 0, EXT, 2>(A, grid, threads, lds, s);
@@ -765,20 +829,24 @@ static int launch_ms(const FastArgs & A, int MS, int grid, int threads, size_t l
     return launch_fast_t<NST, XF32, EXT, 0>(A, grid, threads, lds, s);
 }
 
-static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
+/* One launch of the block kernel over macro steps [k0, k0 + mk) of every row
+ * (the whole row unless x has to be split to fit LDS). */
+static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, int k0, int mk) {
     const Layout L0 = make_layout(c.dim, c.nc, c.mats[0].rows, c.cols, 1);
     const int ext = L0.nbit > 12;
+    VqCall part = c;
+    part.cols = 128 * mk;
     FastShape sh;
-    if (fast_shape(c, nst, sh)) return -1;
+    if (fast_shape(part, nst, sh)) return -1;
     if (sh.lds > (size_t) kLdsMax) {
-        set_error("codebooks and %d activation columns of %d need %zu bytes of LDS", c.ncol, c.cols, sh.lds);
+        set_error("codebooks and %d activation columns of %d need %zu bytes of LDS", c.ncol, part.cols, sh.lds);
         return -1;
     }
     FastArgs A;
     memset(&A, 0, sizeof A);
-    A.x = c.x;
+    A.x = (const uint8_t *) c.x + (size_t) 128 * k0 * (c.xf32 ? 4 : 2);
     A.nmat = c.nmat;
-    A.cols = c.cols;
+    A.cols = part.cols;
     A.nc = c.nc;
     A.ncol = c.ncol;
     A.ldx = c.ldx;
@@ -790,8 +858,9 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
     A.lgS = 0;
     while ((1 << A.lgS) < sh.S) A.lgS++;
     A.C = sh.C; A.T = sh.T;
-    A.M = c.cols / 4 / 32;
-    A.xstride = fast_xstride(c.cols, sh.S);
+    A.M = mk;
+    A.kofs = k0;
+    A.xstride = fast_xstride(part.cols, sh.S);
     int wg = 0;
     for (int m = 0; m < c.nmat; m++) {
         for (int s = 0; s < nst; s++) A.mat[m].st[s] = (const uint8_t *) c.mats[m].stages[st0 + s];
@@ -804,24 +873,59 @@ static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
     }
     const int threads = sh.W * 64;
     A.threads = threads;
-    /* the straight-line kernels stage in one branch-free pass and reduce
-     * within a wave: one 16-byte aligned bf16 column of at most 16 * threads
-     * values, one wave per tile, an even codebook of at most 5 chunks per
-     * thread and stage */
+    /* The straight-line kernels take bf16 x and an even codebook. One column
+     * is staged in one branch-free pass and reduced within a wave: 16-byte
+     * aligned x of at most 16 * threads values, one wave per tile, at most 5
+     * codebook chunks per thread and stage. Several columns are staged by
+     * loops before the index words are requested. */
     const int n16 = c.nc * 8 / 16;
-    const int one_pass = c.ncol == 1 && sh.C == 1 && !c.xf32 && !((uintptr_t) c.x & 15u) && c.nc % 2 == 0 &&
-                         n16 <= 5 * threads && c.cols <= 16 * threads;
-    const int MS = one_pass ? A.M / sh.S / sh.C : 0;
+    const int one_col = sh.C == 1 && !((uintptr_t) A.x & 15u) && n16 <= 5 * threads && part.cols <= 16 * threads;
+    const int multi_col = c.ncol > 1 && !((uintptr_t) A.x & 15u) && c.ldx % 8 == 0 && n16 <= 5 * threads;
+    const int straight = !c.xf32 && c.nc % 2 == 0 && (c.ncol > 1 ? multi_col : one_col);
+    const int MS = straight ? A.M / sh.S / sh.C : 0;
+    const int mc = c.ncol > 1;
     if (nst == 2) {
-        if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
-                               : launch_ms<2, 1, 0>(A, MS, wg, threads, sh.lds, c.stream);
-        return ext ? launch_ms<2, 0, 1>(A, MS, wg, threads, sh.lds, c.stream)
-                   : launch_ms<2, 0, 0>(A, MS, wg, threads, sh.lds, c.stream);
+        if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, mc, wg, threads, sh.lds, c.stream)
+                               : launch_ms<2, 1, 0>(A, MS, mc, wg, threads, sh.lds, c.stream);
+        return ext ? launch_ms<2, 0, 1>(A, MS, mc, wg, threads, sh.lds, c.stream)
+                   : launch_ms<2, 0, 0>(A, MS, mc, wg, threads, sh.lds, c.stream);
     }
-    if (c.xf32) return ext ? launch_ms<1, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
-                           : launch_ms<1, 1, 0>(A, MS, wg, threads, sh.lds, c.stream);
-    return ext ? launch_ms<1, 0, 1>(A, MS, wg, threads, sh.lds, c.stream)
-               : launch_ms<1, 0, 0>(A, MS, wg, threads, sh.lds, c.stream);
+    if (c.xf32) return ext ? launch_ms<1, 1, 1>(A, MS, mc, wg, threads, sh.lds, c.stream)
+                           : launch_ms<1, 1, 0>(A, MS, mc, wg, threads, sh.lds, c.stream);
+    return ext ? launch_ms<1, 0, 1>(A, MS, mc, wg, threads, sh.lds, c.stream)
+               : launch_ms<1, 0, 0>(A, MS, mc, wg, threads, sh.lds, c.stream);
+}
+
+/* How many consecutive K ranges the call needs so that x (all its columns)
+ * fits LDS beside the codebooks: 1 for N = 1 at the trunk's shapes, 2 for
+ * N = 8 over 10240 columns. 0 when no split fits. */
+static int fast_splits(const VqCall & c, int nst) {
+    const int M = c.cols / 128;
+    for (int n = 1; n <= M; n++) {
+        const int mk = (M + n - 1) / n;
+        if (mk * (n - 1) >= M) continue;
+        int ok = 1;
+        for (int k0 = 0; k0 < M && ok; k0 += mk) {
+            VqCall part = c;
+            part.cols = 128 * (M - k0 < mk ? M - k0 : mk);
+            FastShape sh;
+            if (fast_shape(part, nst, sh) || sh.lds > (size_t) kLdsMax) ok = 0;
+        }
+        if (ok) return n;
+    }
+    return 0;
+}
+
+static int launch_fast(const VqCall & c, int st0, int nst, int accumulate) {
+    const int n = fast_splits(c, nst);
+    if (!n) {
+        set_error("the VQ block kernel finds no split of %d columns that fits LDS", c.cols);
+        return -1;
+    }
+    const int M = c.cols / 128, mk = (M + n - 1) / n;
+    for (int k0 = 0; k0 < M; k0 += mk)
+        if (launch_fast_part(c, st0, nst, accumulate || k0 > 0, k0, M - k0 < mk ? M - k0 : mk)) return -1;
+    return 0;
 }
 
 static int launch_wave(const VqCall & c, int variant) {
@@ -887,8 +991,7 @@ int vq_launch(const VqCall & c) {
             VqCall part = c;
             part.mats = c.mats + m0;
             part.nmat = c.nmat - m0 < kFastMats ? c.nmat - m0 : kFastMats;
-            FastShape sh;
-            if (fast_shape(part, nst, sh) || sh.lds > (size_t) kLdsMax) all_fast = 0;
+            if (!fast_splits(part, nst)) all_fast = 0;
         }
     }
     int variant = c.variant;
