@@ -274,6 +274,48 @@ def bench_single(args, sm, torch, dev):
             "frac_of_peak": round(gbps / PEAK_GBPS, 4), "algorithmic_bytes_per_step": int(nbytes)}
 
 
+def bench_prefill(args, sm, torch, dev):
+    """prefill512: the prompt GEMM of one FFN pair, W 10240x2560 (up) and
+    2560x10240 (down), VQ dim 4 nc 4096 2 stages, against 512 bf16 tokens.
+    A step is both GEMMs; MFMA-bound, so the roofline is TFLOP/s."""
+    ntok = 512
+    stream = torch.cuda.Stream(device=dev)
+    mats = []
+    with torch.cuda.stream(stream):
+        for i, (r, c) in enumerate(((FFN, HIDDEN), (HIDDEN, FFN))):
+            m = sm.DeviceContainer(sm.synth_container(0x9F00 + i, r, c), dev)
+            x = torch.from_numpy(sm.synth_bf16(0x9F10 + i, ntok * c).view(np.int16).reshape(ntok, c).copy()).to(dev)
+            y = torch.zeros(ntok, r, device=dev)
+            mats.append((m, x, y, r, c))
+        torch.cuda.synchronize()
+
+        def step():
+            for m, x, y, _, _ in mats:
+                m.prefill(x, y, stream=stream)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = sum(2.0 * ntok * r * c for _, _, _, r, c in mats)
+    tflops = flops / (ms * 1e-3) / 1e12
+    nbytes = sum(m.host.data.nbytes + 2 * ntok * c + 4 * ntok * r for m, _, _, r, c in mats)
+    log(f"  prefill {ntok} tokens, up + down: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s")
+    return {"metric": "prefill GEMM us/step (N=512, FFN up + down)", "value": round(ms * 1e3, 2), "unit": "us/step",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16xf16->f32 (bf16 x)",
+            "data": "synthetic (seeded, random-init weights of the real shapes)",
+            "config": {"workload": "prefill GEMM, 512 bf16 tokens x (10240x2560 and 2560x10240 VQ)", "tokens": ntok},
+            "roofline": {"bound": "mfma", "kernel": "prefill_mfma_kernel", "achieved": round(tflops, 1),
+                         "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
+                         "traffic": None, "flops_per_step": flops, "bytes_per_step": int(nbytes)}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -281,7 +323,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--workload", default="decode-set",
-                    choices=["decode-set", "verify8", "ffn-up", "q6k-down"])
+                    choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512"])
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -308,6 +350,8 @@ def main():
             t = time.time()
             out["cpu_baseline"] = cpu_baseline_decode_set()
             log(f"cpu baseline took {time.time() - t:.1f} s")
+    elif args.workload == "prefill512":
+        out = bench_prefill(args, sm, torch, dev)
     else:
         out = bench_single(args, sm, torch, dev)
     out["device"] = name

@@ -168,7 +168,10 @@ int sparkmv_q8_0_dequant(const void * blocks, int rows, int cols, float * out, v
 
 /* Prefill GEMM over every stage, token-major: x is [ntok][ldx] (bf16 or f32),
  * y is [ntok][ldy] f32, y (+)= W x_t for each token t. Replaces the
- * transpose + vqg_prefill_launch_tile route of tools/vq/gpu/vq-model-gpu.cu:838-851, :899-900. */
+ * transpose + vqg_prefill_launch_tile route of tools/vq/gpu/vq-model-gpu.cu:838-851, :899-900.
+ * DQV3 dim-4 matrices with 16-byte aligned x rows run on the matrix cores
+ * (weights decoded to f16 tiles, f32 accumulation, like the reference's
+ * f16 tiled kernel); any other call runs the one-thread-per-output kernel. */
 int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
                        const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy,
                        int accumulate, void * stream);

@@ -368,8 +368,19 @@ int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc
     for (int i = 0; i < nstages && i < kMaxStages; i++)
         if (!stages[i]) { set_error("stage %d payload is null", i); return -1; }
     const Layout L = make_layout(dim, nc, rows, cols, v3);
-    return prefill_simple_launch(stages, nstages, L, x, x_dtype == SPARKMV_X_F32, (size_t) ldx, 1, ntok, y, ldy,
-                                 accumulate ? 1 : 0, (hipStream_t) stream);
+    const int xf32 = x_dtype == SPARKMV_X_F32;
+    if (prefill_mfma_ready(L, nstages < 2 ? nstages : 2, x, xf32, ldx)) {
+        /* the matrix cores, two stages per launch; later pairs accumulate */
+        for (int s0 = 0; s0 < nstages; s0 += 2) {
+            const int n = nstages - s0 < 2 ? nstages - s0 : 2;
+            if (prefill_mfma_launch(stages + s0, n, L, x, xf32, ldx, ntok, y, ldy, accumulate || s0 > 0,
+                                    (hipStream_t) stream))
+                return -1;
+        }
+        return 0;
+    }
+    return prefill_simple_launch(stages, nstages, L, x, xf32, (size_t) ldx, 1, ntok, y, ldy, accumulate ? 1 : 0,
+                                 (hipStream_t) stream);
 }
 
 }  // extern "C"

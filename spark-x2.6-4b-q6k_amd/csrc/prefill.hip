@@ -4,9 +4,19 @@
  * cb_s[idx_s(r, i)] . x[t][dim*i ..] — the reference's per-token GEMV summed
  * over stages (tools/vq/gpu/decode-gpu.cu:359-501 is its tiled form).
  *
+ * prefill_mfma_kernel: the DQV3 dim-4 GEMM on the matrix cores. A workgroup
+ * owns 128 rows x 128 tokens. Per 64-column chunk it decodes its weight tile
+ * into LDS as f16 (W = c0*g0 + c1*g1 formed in f32 with one rounding, as the
+ * reference decode does, then rounded to f16), converts the tokens' x to f16
+ * beside it, and four waves run v_mfma_f32_16x16x32_f16 over 64 x 64
+ * sub-tiles with f32 accumulation. Tiles are double buffered: the next
+ * chunk's index words and x are in flight while the current chunk's MFMAs
+ * run, and its decode follows them.
+ *
  * prefill_simple_kernel: one thread per (row, token), the row's indices staged
  * in LDS; any geometry and any x layout (strided), f32 arithmetic. It backs
- * variant 3 of the reference-compatible prefill entry points.
+ * variant 3 of the reference-compatible prefill entry points and every call
+ * the MFMA kernel does not take.
  */
 #include "prefill.h"
 
@@ -82,6 +92,250 @@ __global__ __launch_bounds__(256) void prefill_simple_kernel(const SimpleArgs A)
         v += pf_f16(((const uint16_t *) (A.st[s] + L.gain_off))[row]) * acc;
     }
     *yp = v;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MFMA prefill                                                              */
+/* ------------------------------------------------------------------------ */
+
+typedef _Float16 pf_h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 pf_h8 __attribute__((ext_vector_type(8)));
+typedef float pf_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pf_u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pf_u4a __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kPR = 128;   /* rows per workgroup tile */
+constexpr int kPT = 128;   /* tokens per workgroup tile */
+constexpr int kPK = 64;    /* columns per chunk */
+constexpr int kPS = 72;    /* LDS row stride of a tile in halves (64 + 8 pad: conflict-free 16-byte reads) */
+
+struct MfmaArgs {
+    const uint8_t * st[2];
+    const void * x;      /* token-major: x[t * ldx + k], bf16 bits or f32 */
+    float * y;           /* y[t * ldy + r] */
+    int rows, cols, nc, ntok, ldx, ldy, accumulate;
+    uint32_t gain_off, stream_off, mrow, prow;
+};
+
+/* field j of 8 12-bit fields packed LSB-first in three words */
+__device__ __forceinline__ uint32_t pf_field12(uint32_t w0, uint32_t w1, uint32_t w2, int j) {
+    switch (j) {
+        case 0: return w0 & 0xfffu;
+        case 1: return (w0 >> 12) & 0xfffu;
+        case 2: return __builtin_amdgcn_alignbit(w1, w0, 24) & 0xfffu;
+        case 3: return (w1 >> 4) & 0xfffu;
+        case 4: return (w1 >> 16) & 0xfffu;
+        case 5: return __builtin_amdgcn_alignbit(w2, w1, 28) & 0xfffu;
+        case 6: return (w2 >> 8) & 0xfffu;
+        default: return w2 >> 20;
+    }
+}
+
+template <int NST, int EXT, int XF32>
+__global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const uint32_t cbb = (uint32_t) P.nc * 8u;
+    _Float16 * At = (_Float16 *) (lds + NST * cbb);   /* [2][kPR][kPS] decoded weights */
+    _Float16 * Bt = At + 2 * kPR * kPS;                /* [2][kPT][kPS] tokens */
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * kPR, t0 = blockIdx.y * kPT;
+    const int nk = P.cols / kPK;
+
+    /* codebooks to LDS in batches of unconditional 16-byte loads */
+    {
+        const int n16 = (int) (cbb >> 4), ncb = NST * n16;
+        for (int base = 0; base < ncb; base += 8 * 256) {
+            pf_u4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = min(base + k * 256 + tid, ncb - 1), s = i >= n16 ? 1 : 0;
+                v[k] = ((const pf_u4a *) (P.st[NST > 1 ? s : 0] + 24))[i - s * n16];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) ((pf_u4 *) lds)[min(base + k * 256 + tid, ncb - 1)] = v[k];
+        }
+    }
+
+    /* decode role: row dr of the tile, columns 32 h .. 32 h + 31 of a chunk
+     * (8 indices); x role: token dr of the tile, the same columns */
+    const int dr = tid >> 1, h = tid & 1;
+    const int drow = min(r0 + dr, P.rows - 1), dtok = min(t0 + dr, P.ntok - 1);
+    float g[NST];
+    const uint8_t * rs[NST];
+    const uint8_t * ps[NST];
+#pragma unroll
+    for (int s = 0; s < NST; s++) {
+        g[s] = (float) *(const _Float16 *) (P.st[s] + P.gain_off + 2 * (size_t) drow);
+        rs[s] = P.st[s] + P.stream_off + (size_t) drow * P.mrow + 12 * h;
+        ps[s] = P.st[s] + P.stream_off + (size_t) P.rows * P.mrow + (size_t) drow * P.prow + h;
+    }
+    const uint8_t * xr = (const uint8_t *) P.x + (size_t) dtok * P.ldx * (XF32 ? 4 : 2) + 32 * h * (XF32 ? 4 : 2);
+
+    constexpr int NXV = XF32 ? 8 : 4;
+    uint32_t wv[NST][3], pb[NST];
+    pf_u4 xv[NXV];
+    auto fetch = [&](int kc) {
+#pragma unroll
+        for (int s = 0; s < NST; s++) {
+            const uint32_t * wp = (const uint32_t *) (rs[s] + 24 * kc);
+            wv[s][0] = wp[0]; wv[s][1] = wp[1]; wv[s][2] = wp[2];
+            pb[s] = EXT ? ps[s][2 * kc] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < NXV; k++) xv[k] = ((const pf_u4 *) (xr + kPK * kc * (XF32 ? 4 : 2)))[k];
+    };
+    auto store = [&](int b) {
+        _Float16 * ad = At + (b * kPR + dr) * kPS + 32 * h;
+#pragma unroll
+        for (int jj = 0; jj < 8; jj += 2) {
+            pf_h8 w8;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int j = jj + u;
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < NST; s++) {
+                    uint32_t idx = pf_field12(wv[s][0], wv[s][1], wv[s][2], j);
+                    if (EXT) idx |= ((pb[s] >> j) & 1u) << 12;
+                    const pf_h4 c = *(const pf_h4 *) (lds + s * cbb + 8 * idx);
+#pragma unroll
+                    for (int d = 0; d < 4; d++) acc[d] = __builtin_fmaf((float) c[d], g[s], acc[d]);
+                }
+#pragma unroll
+                for (int d = 0; d < 4; d++) w8[4 * u + d] = (_Float16) acc[d];
+            }
+            *(pf_h8 *) (ad + 4 * jj) = w8;
+        }
+        _Float16 * bd = Bt + (b * kPT + dr) * kPS + 32 * h;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            pf_h8 v8;
+            if (XF32) {
+                const pf_u4 lo = xv[2 * k], hi = xv[2 * k + 1];
+                v8[0] = (_Float16) __uint_as_float(lo.x); v8[1] = (_Float16) __uint_as_float(lo.y);
+                v8[2] = (_Float16) __uint_as_float(lo.z); v8[3] = (_Float16) __uint_as_float(lo.w);
+                v8[4] = (_Float16) __uint_as_float(hi.x); v8[5] = (_Float16) __uint_as_float(hi.y);
+                v8[6] = (_Float16) __uint_as_float(hi.z); v8[7] = (_Float16) __uint_as_float(hi.w);
+            } else {
+                const pf_u4 q = xv[k];
+                v8[0] = (_Float16) __uint_as_float(q.x << 16); v8[1] = (_Float16) __uint_as_float(q.x & 0xffff0000u);
+                v8[2] = (_Float16) __uint_as_float(q.y << 16); v8[3] = (_Float16) __uint_as_float(q.y & 0xffff0000u);
+                v8[4] = (_Float16) __uint_as_float(q.z << 16); v8[5] = (_Float16) __uint_as_float(q.z & 0xffff0000u);
+                v8[6] = (_Float16) __uint_as_float(q.w << 16); v8[7] = (_Float16) __uint_as_float(q.w & 0xffff0000u);
+            }
+            *(pf_h8 *) (bd + 8 * k) = v8;
+        }
+    };
+
+    /* MFMA role: wave (wm, wn) owns rows 64 wm .. +63 and tokens 64 wn .. +63
+     * of the tile as 4 x 4 blocks of 16 x 16. A lane's operand is 8
+     * consecutive columns of one row (A) or one token (B); A and B assign
+     * columns to lanes the same way, so each block is a plain dot over the
+     * chunk's columns. */
+    const int wm = wave & 1, wn = wave >> 1, m16 = lane & 15, kq = lane >> 4;
+    pf_f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = pf_f4{0.f, 0.f, 0.f, 0.f};
+
+    __syncthreads();   /* codebooks staged */
+    fetch(0);
+    store(0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; kc++) {
+        const int b = kc & 1;
+        if (kc + 1 < nk) fetch(kc + 1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            pf_h8 a[4], bb[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                a[i] = *(const pf_h8 *) (At + (b * kPR + 64 * wm + 16 * i + m16) * kPS + 32 * ks + 8 * kq);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                bb[j] = *(const pf_h8 *) (Bt + (b * kPT + 64 * wn + 16 * j + m16) * kPS + 32 * ks + 8 * kq);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bb[j], acc[i][j], 0, 0, 0);
+        }
+        if (kc + 1 < nk) store(b ^ 1);
+        __syncthreads();
+    }
+
+    /* block (i, j): lane holds rows 4 kq .. 4 kq + 3 of token m16 */
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tok = t0 + 64 * wn + 16 * j + m16;
+            if (tok >= P.ntok) continue;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int row = r0 + 64 * wm + 16 * i + 4 * kq + e;
+                if (row < P.rows) {
+                    float * yp = P.y + (size_t) tok * P.ldy + row;
+                    *yp = (P.accumulate ? *yp : 0.0f) + acc[i][j][e];
+                }
+            }
+        }
+}
+
+/* The MFMA kernel takes DQV3 dim-4 stages with 12- or 13-bit indices, 1 or
+ * 2 stages, an even codebook, columns a multiple of 128, dword-aligned row
+ * streams, and token-major x in 16-byte aligned rows. */
+int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int ldx) {
+    if (!L.v3 || L.dim != 4 || L.nbit < 12 || L.nbit > 13 || nst < 1 || nst > 2) return 0;
+    if (L.nc % 2 || L.cols % 128 || L.stream_off % 4 || L.mrow % 4) return 0;
+    if ((uintptr_t) x & 15u) return 0;
+    if (ldx % (xf32 ? 4 : 8)) return 0;
+    const size_t lds = (size_t) nst * L.nc * 8 + (size_t) 4 * kPR * kPS * 2;
+    return lds <= 160 * 1024;
+}
+
+template <int NST, int EXT, int XF32>
+static int prefill_mfma_t(const MfmaArgs & P, size_t lds, hipStream_t s) {
+    static size_t opted = 0;
+    const void * fn = (const void *) prefill_mfma_kernel<NST, EXT, XF32>;
+    if (lds > 65536 && lds > opted) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return fail_hip("LDS opt-in for the MFMA prefill kernel", e);
+        opted = lds;
+    }
+    const dim3 grid((unsigned) ((P.rows + kPR - 1) / kPR), (unsigned) ((P.ntok + kPT - 1) / kPT));
+    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32>, grid, dim3(256), (uint32_t) lds, s, P);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail_hip("MFMA prefill launch", e);
+}
+
+int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
+                        int ntok, float * y, int ldy, int accumulate, hipStream_t s) {
+    if (!prefill_mfma_ready(L, nst, x, xf32, ldx)) {
+        set_error("the MFMA prefill kernel does not take this geometry, stage count or x layout");
+        return -1;
+    }
+    if (ntok <= 0) { set_error("prefill needs at least one token"); return -1; }
+    MfmaArgs P;
+    memset(&P, 0, sizeof P);
+    P.st[0] = (const uint8_t *) stages[0];
+    P.st[1] = (const uint8_t *) stages[nst > 1 ? 1 : 0];
+    P.x = x;
+    P.y = y;
+    P.rows = L.rows; P.cols = L.cols; P.nc = L.nc; P.ntok = ntok;
+    P.ldx = ldx; P.ldy = ldy; P.accumulate = accumulate;
+    P.gain_off = (uint32_t) L.gain_off;
+    P.stream_off = (uint32_t) L.stream_off;
+    P.mrow = (uint32_t) L.mrow;
+    P.prow = (uint32_t) L.prow;
+    const size_t lds = (size_t) nst * L.nc * 8 + (size_t) 4 * kPR * kPS * 2;
+    const int ext = L.nbit > 12;
+    if (nst == 2) {
+        if (xf32) return ext ? prefill_mfma_t<2, 1, 1>(P, lds, s) : prefill_mfma_t<2, 0, 1>(P, lds, s);
+        return ext ? prefill_mfma_t<2, 1, 0>(P, lds, s) : prefill_mfma_t<2, 0, 0>(P, lds, s);
+    }
+    if (xf32) return ext ? prefill_mfma_t<1, 1, 1>(P, lds, s) : prefill_mfma_t<1, 0, 1>(P, lds, s);
+    return ext ? prefill_mfma_t<1, 1, 0>(P, lds, s) : prefill_mfma_t<1, 0, 0>(P, lds, s);
 }
 
 int prefill_simple_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32,

@@ -238,6 +238,34 @@ def test_prefill_token_major(sm, ref, dev, ntok):
     assert rel_l2(y.cpu().numpy(), xf.astype(np.float64) @ W.T) <= BAR
 
 
+@pytest.mark.parametrize("rows,cols,ntok,nc,f32", [(320, 2560, 200, 4096, False), (130, 1024, 512, 4096, False),
+                                                    (64, 512, 77, 8192, False), (96, 640, 130, 4096, True),
+                                                    (256, 10240, 64, 4096, False)])
+def test_prefill_mfma_against_oracle(sm, ref, dev, rows, cols, ntok, nc, f32):
+    """The matrix-core prefill: ragged row and token tiles, 13-bit indices,
+    f32 x, and the long 10240-column rows of down_proj. Weights enter the
+    MFMA as f16 (one rounding of the exact decode), so the bar is the 1e-3
+    relative L2 of the GEMM gate, not the GEMV's f32-exact 1e-5."""
+    import torch
+    data = sm.synth_container(rows * 3 + ntok, rows, cols, 4, nc, 2, 1)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    xt, xf = _x(sm, ntok + 5, ntok, cols, f32)
+    y = torch.full((ntok, rows), float("nan"), device=dev)
+    dc.prefill(xt, y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = xf.astype(np.float64) @ W.T
+    err = rel_l2(got, want)
+    print(f"prefill {rows}x{cols} ntok {ntok} nc {nc} f32 {f32}: relL2 {err:.2e}")
+    assert err <= BAR
+    # accumulate adds into y
+    y2 = torch.from_numpy(got.copy()).to(dev)
+    dc.prefill(xt, y2, accumulate=True)
+    torch.cuda.synchronize()
+    assert rel_l2(y2.cpu().numpy(), 2 * want) <= BAR
+
+
 def test_prefill_reference_layout(sm, ref, dev):
     import torch
     rows, cols, ntok = 48, 128, 20
