@@ -166,7 +166,7 @@ __device__ __forceinline__ void mstep(const Words<NST, EXT> & W, const uint8_t *
 }
 
 template <int NST, int XF32, int EXT, int MSC, int MC>
-__global__ __launch_bounds__(640) void vq_mfma_kernel(const FastArgs A) {
+__global__ __launch_bounds__(MC ? 1024 : 640) void vq_mfma_kernel(const FastArgs A) {
     /* MSC > 0: a unit is exactly MSC macro steps, known at compile time, so
      * the whole unit runs as straight-line code and each step waits only for
      * its own index words (a loop would make the compiler wait for all of a
@@ -794,6 +794,40 @@ static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
     for (int m = 0; m < c.nmat; m++) sh.nwg += (int) (((c.mats[m].rows * (long) S + 15) / 16 + T - 1) / T);
     sh.lds = fast_lds(c, nst, S, sh.W);
     (void) total_rows;
+    if (c.ncol > 1) {
+        /* Several columns: codebooks plus N columns of x leave room for one
+         * workgroup per CU, so the shape that matters is the number of rounds
+         * of workgroups over the CUs. Search parts S, K chunks C and tiles T
+         * (up to 16 waves) for the fewest rounds, then the shortest unit,
+         * preferring unit lengths with a straight-line kernel. */
+        /* 16 waves only in the multi-column kernels (bf16 x, even codebook,
+         * 16-byte aligned x rows, at least 5 codebook chunks' worth of threads) */
+        const int mc_ok = !c.xf32 && c.nc % 2 == 0 && !((uintptr_t) c.x & 15u) && c.ldx % 8 == 0;
+        const int n16 = c.nc * 8 / 16;
+        long best = -1;
+        for (int s = 1; s <= 16; s *= 2) {
+            if (s * c.ncol > 16 || M % s) continue;
+            const int MP = M / s;
+            for (int cc = 1; cc <= 16; cc++) {
+                if (MP % cc) continue;
+                const int ms = MP / cc;
+                for (int tt = 1; tt * cc <= 16; tt++) {
+                    if (tt * cc > 10 && !(mc_ok && n16 <= 5 * 64 * tt * cc)) continue;
+                    long nwg = 0;
+                    for (int m = 0; m < c.nmat; m++) nwg += ((c.mats[m].rows * (long) s + 15) / 16 + tt - 1) / tt;
+                    const size_t lds = fast_lds(c, nst, s, tt * cc);
+                    if (lds > (size_t) kLdsMax) continue;
+                    const long rounds = (nwg + G - 1) / G;
+                    const int straight = ms == 2 || ms == 4 || ms == 5 || ms == 8 || ms == 10;
+                    const long cost = rounds * (8 + ms + (straight ? 0 : ms)) * 64 + tt * cc;
+                    if (best < 0 || cost < best) {
+                        best = cost;
+                        sh.S = s; sh.C = cc; sh.T = tt; sh.W = tt * cc; sh.nwg = (int) nwg; sh.lds = lds;
+                    }
+                }
+            }
+        }
+    }
     return 0;
 }
 
@@ -808,11 +842,13 @@ static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, 
             /* several columns: the unit lengths of the trunk's verify shapes */
             switch (MS) {
                 case 2: return launch_fast_t<NST, 0, EXT, 2, 1>(A, grid, threads, lds, s);
+                case 4: return launch_fast_t<NST, 0, EXT, 4, 1>(A, grid, threads, lds, s);
                 case 5: return launch_fast_t<NST, 0, EXT, 5, 1>(A, grid, threads, lds, s);
+                case 8: return launch_fast_t<NST, 0, EXT, 8, 1>(A, grid, threads, lds, s);
                 case 10: if (!EXT) return launch_fast_t<NST, 0, EXT, EXT ? 0 : 10, 1>(A, grid, threads, lds, s); break;
                 default: break;
             }
-            return launch_fast_t<NST, XF32, EXT, 0>(A, grid, threads, lds, s);
+            return launch_fast_t<NST, 0, EXT, 0, 1>(A, grid, threads, lds, s);
         }
         switch (MS) {
             case 1: return launch_fast_t<NST, 0, EXT, 1>(A, grid, threads, lds, s);
@@ -883,7 +919,10 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     const int multi_col = c.ncol > 1 && !((uintptr_t) A.x & 15u) && c.ldx % 8 == 0 && n16 <= 5 * threads;
     const int straight = !c.xf32 && c.nc % 2 == 0 && (c.ncol > 1 ? multi_col : one_col);
     const int MS = straight ? A.M / sh.S / sh.C : 0;
-    const int mc = c.ncol > 1;
+    /* the multi-column kernels (MS without its own instantiation runs their
+     * ring form); any other several-column call runs the generic kernel,
+     * which the shape search kept within 10 waves */
+    const int mc = c.ncol > 1 && straight;
     if (nst == 2) {
         if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, mc, wg, threads, sh.lds, c.stream)
                                : launch_ms<2, 1, 0>(A, MS, mc, wg, threads, sh.lds, c.stream);
