@@ -263,6 +263,92 @@ __global__ void q6k_dequant_kernel(const uint8_t * blocks, size_t nblocks, float
 
 /* -------------------------------- host ----------------------------------- */
 
+/* Q6_K, wide form: 32 lanes per row (two rows per wave), every lane issues
+ * the loads of all its half superblocks (at most 3, so rows of up to 96
+ * half superblocks = 12288 columns) before any of them is used, which keeps
+ * a whole row's blocks in flight per wave instead of one at a time. The
+ * arithmetic per half superblock is the one of q6k_gemv_kernel. */
+template <int NC, int XF32>
+__global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * blocks, int rows, int cols, const void * x,
+                                                            int ldx, int ncol, float * y, int ldy, int accumulate) {
+    constexpr int NU = 3;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72;
+    kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
+    const int lane = threadIdx.x & 63, j = lane & 31, g = lane >> 5;
+    const int row = ((int) blockIdx.x * (int) (blockDim.x >> 6) + (int) (threadIdx.x >> 6)) * 2 + g;
+    const int rowc = min(row, rows - 1);
+    uint32_t ql[NU][16], qh[NU][8], scw[NU][2];
+    float d[NU];
+#pragma unroll
+    for (int k = 0; k < NU; k++) {
+        const int u = min(j + 32 * k, units - 1), sb = u >> 1, h = u & 1;
+        const uint8_t * blk = blocks + ((size_t) rowc * bpr + sb) * 210;
+        d[k] = kq_f16(*(const uint16_t *) (blk + 208));
+        load_stream<16>(blk + 64 * h, ql[k], true);
+        load_stream<8>(blk + 128 + 32 * h, qh[k], true);
+        load_stream<2>(blk + 192 + 8 * h, scw[k], true);
+    }
+    __syncthreads();
+    float acc[NC];
+#pragma unroll
+    for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < NU; kk++) {
+        const int u = j + 32 * kk;
+        if (u >= units) continue;
+        const int sb = u >> 1, h = u & 1;
+        const int chunk0 = (sb * 256 + 128 * h) >> 5;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const int sci = p + 2 * k;
+                const float dsc = d[kk] * (float) (int) (int8_t) (scw[kk][sci >> 2] >> (8 * (sci & 3)));
+                kq_h2 qv[8];
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const int l = 16 * p + 4 * w;
+                    const uint32_t lo = (ql[kk][(l + 32 * (k & 1)) >> 2] >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
+                    const uint32_t hi = ((qh[kk][l >> 2] >> (2 * k)) & 0x03030303u) << 4;
+                    bytes_to_h2(lo | hi, (_Float16) 1056.0f, qv[2 * w], qv[2 * w + 1]);
+                }
+#pragma unroll
+                for (int n = 0; n < NC; n++) {
+                    if (n < ncol) {
+                        const uint8_t * xp = lds + n * xst + (chunk0 + k) * 72 + 32 * p;
+                        float sacc = 0.0f;
+#pragma unroll
+                        for (int w = 0; w < 4; w++) {
+                            const kq_h4 xv = *(const kq_h4 *) (xp + 8 * w);
+                            sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xv[0], xv[1]}, sacc, false);
+                            sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xv[2], xv[3]}, sacc, false);
+                            if (XF32) {
+                                const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * w);
+                                sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xl[0], xl[1]}, sacc, false);
+                                sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xl[2], xl[3]}, sacc, false);
+                            }
+                        }
+                        acc[n] += dsc * sacc;
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NC; n++) {
+        if (n < ncol) {
+            float v = acc[n];
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (j == 0 && row < rows) {
+                float * yp = y + (size_t) n * ldy + row;
+                *yp = (accumulate ? *yp : 0.0f) + v;
+            }
+        }
+    }
+}
+
 int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void * x, int xf32, int ldx, int ncol,
                    float * y, int ldy, int accumulate, hipStream_t s) {
     const int blk = kind == 6 ? 256 : 32;
@@ -291,7 +377,12 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
         else if (ncol <= 4) KQ_LAUNCH(K, 4, XF); \
         else KQ_LAUNCH(K, 16, XF);              \
     } while (0)
-    if (kind == 6) {
+    if (kind == 6 && cols <= 12288) {
+        /* eight rows per workgroup, every row's blocks requested at once */
+        grid = (rows + 7) / 8;
+        if (xf32) KQ_PICK(q6k_gemv_wide_kernel, 1);
+        else KQ_PICK(q6k_gemv_wide_kernel, 0);
+    } else if (kind == 6) {
         if (xf32) KQ_PICK(q6k_gemv_kernel, 1);
         else KQ_PICK(q6k_gemv_kernel, 0);
     } else {
