@@ -80,8 +80,59 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t w, _Float16 bias, kq_h2 & l
  * (64 bytes of data and 8 of pad, so the 16 lanes of a row, 16 slots apart,
  * hit distinct LDS banks). f32 activations also stage the residual
  * lo = f16(x - hi) one array further on, and the dot runs over both. */
+/* x to LDS as f16 (and the f32 remainder as a second f16 array), 72-byte
+ * slots of 32 columns. With 4-byte aligned rows (x aligned, ldx even) the
+ * columns go in groups of 8 through batches of unconditional 16-byte loads
+ * (groups past the end re-read the last one), so the staging costs a few
+ * memory latencies rather than one per element; otherwise one element per
+ * thread and step. */
 template <int XF32>
 __device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
+    typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
+    const bool vec = !((uintptr_t) x & 3) && (ncol == 1 || !(ldx & 1));
+    if (vec) {
+        constexpr int KB = 4, NV = XF32 ? 2 : 1;
+        const int ng = cols >> 3, total = ncol * ng;
+        for (int base = 0; base < total; base += KB * (int) blockDim.x) {
+            u4a v[KB][NV];
+            int gi[KB];
+#pragma unroll
+            for (int k = 0; k < KB; k++) {
+                gi[k] = min(base + k * (int) blockDim.x + (int) threadIdx.x, total - 1);
+                const int n = gi[k] / ng, c8 = gi[k] - n * ng;
+                const uint8_t * src = (const uint8_t *) x + ((size_t) n * ldx + 8 * c8) * (XF32 ? 4 : 2);
+#pragma unroll
+                for (int q = 0; q < NV; q++) v[k][q] = ((const u4a *) src)[q];
+            }
+#pragma unroll
+            for (int k = 0; k < KB; k++) {
+                const int n = gi[k] / ng, e = 8 * (gi[k] - n * ng);
+                const int off = (e >> 5) * 72 + 2 * (e & 31);
+                float f[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const uint32_t w = XF32 ? v[k][q >> 2][q & 3] : v[k][0][q >> 1];
+                    f[q] = XF32 ? __uint_as_float(w) : __uint_as_float((q & 1) ? (w & 0xffff0000u) : (w << 16));
+                }
+                kq_h4 h0, h1;
+#pragma unroll
+                for (int q = 0; q < 4; q++) { h0[q] = (_Float16) f[q]; h1[q] = (_Float16) f[4 + q]; }
+                *(kq_h4 *) (lds + n * xst + off) = h0;
+                *(kq_h4 *) (lds + n * xst + off + 8) = h1;
+                if (XF32) {
+                    kq_h4 l0, l1;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        l0[q] = (_Float16) (f[q] - (float) h0[q]);
+                        l1[q] = (_Float16) (f[4 + q] - (float) h1[q]);
+                    }
+                    *(kq_h4 *) (lds + (ncol + n) * xst + off) = l0;
+                    *(kq_h4 *) (lds + (ncol + n) * xst + off + 8) = l1;
+                }
+            }
+        }
+        return;
+    }
     for (int e = threadIdx.x; e < ncol * cols; e += blockDim.x) {
         const int n = e / cols, k = e - n * cols;
         const float v = kq_x(x, XF32, (size_t) n * ldx + k);
