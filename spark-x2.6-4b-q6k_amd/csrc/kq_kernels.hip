@@ -85,13 +85,15 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t w, _Float16 bias, kq_h2 & l
  * columns go in groups of 8 through batches of unconditional 16-byte loads
  * (groups past the end re-read the last one), so the staging costs a few
  * memory latencies rather than one per element; otherwise one element per
- * thread and step. */
-template <int XF32>
+ * thread and step. PADU adds 8 bytes after every 4 slots (128 columns): the
+ * Q6_K kernels' lanes read 128-column units, and the pad puts neighbouring
+ * units on different LDS banks. */
+template <int XF32, int PADU = 0>
 __device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
     typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
     const bool vec = !((uintptr_t) x & 3) && (ncol == 1 || !(ldx & 1));
     if (vec) {
-        constexpr int KB = 4, NV = XF32 ? 2 : 1;
+        constexpr int KB = 8, NV = XF32 ? 2 : 1;
         const int ng = cols >> 3, total = ncol * ng;
         for (int base = 0; base < total; base += KB * (int) blockDim.x) {
             u4a v[KB][NV];
@@ -107,7 +109,7 @@ __device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ld
 #pragma unroll
             for (int k = 0; k < KB; k++) {
                 const int n = gi[k] / ng, e = 8 * (gi[k] - n * ng);
-                const int off = (e >> 5) * 72 + 2 * (e & 31);
+                const int off = (e >> 5) * 72 + (PADU ? (e >> 7) * 8 : 0) + 2 * (e & 31);
                 float f[8];
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
@@ -137,7 +139,7 @@ __device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ld
         const int n = e / cols, k = e - n * cols;
         const float v = kq_x(x, XF32, (size_t) n * ldx + k);
         const _Float16 hi = (_Float16) v;
-        const int off = (k >> 5) * 72 + 2 * (k & 31);
+        const int off = (k >> 5) * 72 + (PADU ? (k >> 7) * 8 : 0) + 2 * (k & 31);
         *(_Float16 *) (lds + n * xst + off) = hi;
         if (XF32) *(_Float16 *) (lds + (ncol + n) * xst + off) = (_Float16) (v - (float) hi);
     }
@@ -223,8 +225,8 @@ template <int NC, int XF32>
 __global__ __launch_bounds__(256) void q6k_gemv_kernel(const uint8_t * blocks, int rows, int cols, const void * x,
                                                        int ldx, int ncol, float * y, int ldy, int accumulate) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72;
-    kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
+    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72 + (cols / 128) * 8;
+    kq_stage_x<XF32, 1>(lds, x, ldx, ncol, cols, xst);
     __syncthreads();
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int row_step = gridDim.x * (blockDim.x >> 6) * 4;
@@ -259,7 +261,7 @@ __global__ __launch_bounds__(256) void q6k_gemv_kernel(const uint8_t * blocks, i
 #pragma unroll
                     for (int n = 0; n < NC; n++) {
                         if (n < ncol) {
-                            const uint8_t * xp = lds + n * xst + (chunk0 + k) * 72 + 32 * p;
+                            const uint8_t * xp = lds + n * xst + (chunk0 + k) * 72 + (chunk0 >> 2) * 8 + 32 * p;
                             float s = 0.0f;
 #pragma unroll
                             for (int w = 0; w < 4; w++) {
@@ -324,8 +326,7 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
                                                             int ldx, int ncol, float * y, int ldy, int accumulate) {
     constexpr int NU = 3;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72;
-    kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
+    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72 + (cols / 128) * 8;
     const int lane = threadIdx.x & 63, j = lane & 31, g = lane >> 5;
     const int row = ((int) blockIdx.x * (int) (blockDim.x >> 6) + (int) (threadIdx.x >> 6)) * 2 + g;
     const int rowc = min(row, rows - 1);
@@ -340,6 +341,8 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
         load_stream<8>(blk + 128 + 32 * h, qh[k], true);
         load_stream<2>(blk + 192 + 8 * h, scw[k], true);
     }
+    /* x after the blocks are requested: both latencies overlap */
+    kq_stage_x<XF32, 1>(lds, x, ldx, ncol, cols, xst);
     __syncthreads();
     float acc[NC];
 #pragma unroll
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
 #pragma unroll
                 for (int n = 0; n < NC; n++) {
                     if (n < ncol) {
-                        const uint8_t * xp = lds + n * xst + (chunk0 + k) * 72 + 32 * p;
+                        const uint8_t * xp = lds + n * xst + (chunk0 + k) * 72 + (chunk0 >> 2) * 8 + 32 * p;
                         float sacc = 0.0f;
 #pragma unroll
                         for (int w = 0; w < 4; w++) {
@@ -400,6 +403,148 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
     }
 }
 
+/* 4-byte reads of LDS at a 2-byte aligned address, shifted into N words */
+template <int N>
+__device__ __forceinline__ void lds_stream(const uint8_t * addr, uint32_t * out) {
+    const uintptr_t a = (uintptr_t) addr;
+    const uint32_t * p = (const uint32_t *) (a & ~(uintptr_t) 3);
+    const uint32_t sh = (uint32_t) (a & 3) * 8u;
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int k = 0; k <= N; k++) w[k] = p[k];
+#pragma unroll
+    for (int k = 0; k < N; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+}
+
+/* Q6_K, staged form: the workgroup's rows are one contiguous run of blocks,
+ * copied into LDS by 1 KB direct-to-LDS loads (a whole cache line per lane
+ * group, each line fetched once), then each row is worked by 32 lanes from
+ * LDS with the arithmetic of q6k_gemv_kernel. One row per wave (64 lanes,
+ * up to 128 half superblocks = 16384 columns); rows a multiple of 4 bytes
+ * long (even superblock count) and 4-byte aligned blocks (the host checks
+ * both). */
+template <int NC, int XF32>
+__global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * blocks, int rows, int cols,
+                                                                const void * x, int ldx, int ncol, float * y, int ldy,
+                                                                int accumulate) {
+    constexpr int NU = 2;
+    typedef __attribute__((address_space(3))) void lds_void;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72 + (cols / 128) * 8;
+    const size_t rowbytes = (size_t) bpr * 210;
+    const int nw = blockDim.x >> 6, rpw = nw;                  /* one row per wave */
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = blockIdx.x * rpw, nrow = min(rpw, rows - row0);
+    const uint32_t region = (uint32_t) (nrow * rowbytes);        /* >= 1 KB, checked by the host */
+    const uint32_t xoff = (uint32_t) ((rpw * rowbytes + 15) & ~(size_t) 15);
+    const uint8_t * src = blocks + (size_t) row0 * rowbytes;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int nblk = (int) ((region + 1023) >> 10);
+    for (int b = wv; b < nblk; b += nw) {
+        const uint32_t o = min((uint32_t) b * 1024u, region - 1024u);   /* the last block overlaps its neighbour */
+        __builtin_amdgcn_global_load_lds((const void *) (src + o + 16 * lane), (lds_void *) (lds + o), 16, 0, 0);
+    }
+    kq_stage_x<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int j = lane, rl = wave, row = row0 + rl;
+    float acc[NC];
+#pragma unroll
+    for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+    if (rl < nrow) {
+#pragma unroll
+        for (int kk = 0; kk < NU; kk++) {
+            const int u = j + 64 * kk;
+            if (u >= units) continue;
+            const int sb = u >> 1, h = u & 1;
+            const uint8_t * blk = lds + rl * rowbytes + (size_t) sb * 210;
+            uint32_t ql[16], qh[8], scw[2], dw[1];
+            lds_stream<16>(blk + 64 * h, ql);
+            lds_stream<8>(blk + 128 + 32 * h, qh);
+            lds_stream<2>(blk + 192 + 8 * h, scw);
+            lds_stream<1>(blk + 208, dw);
+            const float d = kq_f16((uint16_t) dw[0]);
+            const int chunk0 = (sb * 256 + 128 * h) >> 5;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const int sci = p + 2 * k;
+                    const float dsc = d * (float) (int) (int8_t) (scw[sci >> 2] >> (8 * (sci & 3)));
+                    kq_h2 qv[8];
+#pragma unroll
+                    for (int w = 0; w < 4; w++) {
+                        const int l = 16 * p + 4 * w;
+                        const uint32_t lo = (ql[(l + 32 * (k & 1)) >> 2] >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
+                        const uint32_t hi = ((qh[l >> 2] >> (2 * k)) & 0x03030303u) << 4;
+                        bytes_to_h2(lo | hi, (_Float16) 1056.0f, qv[2 * w], qv[2 * w + 1]);
+                    }
+#pragma unroll
+                    for (int n = 0; n < NC; n++) {
+                        if (n < ncol) {
+                            const uint8_t * xp = lds + xoff + n * xst + (chunk0 + k) * 72 + (chunk0 >> 2) * 8 + 32 * p;
+                            float sacc = 0.0f;
+#pragma unroll
+                            for (int w = 0; w < 4; w++) {
+                                const kq_h4 xv = *(const kq_h4 *) (xp + 8 * w);
+                                sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xv[0], xv[1]}, sacc, false);
+                                sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xv[2], xv[3]}, sacc, false);
+                                if (XF32) {
+                                    const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * w);
+                                    sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xl[0], xl[1]}, sacc, false);
+                                    sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xl[2], xl[3]}, sacc, false);
+                                }
+                            }
+                            acc[n] += dsc * sacc;
+                        }
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NC; n++) {
+        if (n < ncol) {
+            float v = acc[n];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (j == 0 && rl < nrow) {
+                float * yp = y + (size_t) n * ldy + row;
+                *yp = (accumulate ? *yp : 0.0f) + v;
+            }
+        }
+    }
+}
+
+static inline const uint8_t * bp_in(const void * p) { return (const uint8_t *) p; }
+
+template <int XF32>
+static int kq_q6k_staged_t(const uint8_t * bp, int rows, int cols, const void * x, int ldx, int ncol, float * y,
+                           int ldy, int accumulate, int rpw, size_t lds, hipStream_t s) {
+    static size_t opted[3] = {0, 0, 0};
+    const int slot = ncol == 1 ? 0 : (ncol <= 4 ? 1 : 2);
+    const void * fn = slot == 0 ? (const void *) q6k_gemv_staged_kernel<1, XF32>
+                    : slot == 1 ? (const void *) q6k_gemv_staged_kernel<4, XF32>
+                                : (const void *) q6k_gemv_staged_kernel<16, XF32>;
+    if (lds > 65536 && lds > opted[slot]) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return fail_hip("LDS opt-in for the staged Q6_K kernel", e);
+        opted[slot] = lds;
+    }
+    const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block((unsigned) (64 * rpw));
+    if (slot == 0) launch_kernel(q6k_gemv_staged_kernel<1, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate);
+    else if (slot == 1) launch_kernel(q6k_gemv_staged_kernel<4, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate);
+    else launch_kernel(q6k_gemv_staged_kernel<16, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail_hip("staged Q6_K launch", e);
+}
+
+static int kq_q6k_staged(const uint8_t * bp, int rows, int cols, const void * x, int xf32, int ldx, int ncol, float * y,
+                         int ldy, int accumulate, int rpw, size_t lds, hipStream_t s) {
+    return xf32 ? kq_q6k_staged_t<1>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s)
+                : kq_q6k_staged_t<0>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
+}
+
 int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void * x, int xf32, int ldx, int ncol,
                    float * y, int ldy, int accumulate, hipStream_t s) {
     const int blk = kind == 6 ? 256 : 32;
@@ -414,7 +559,8 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
     if (ncol > 1 && (ldx < cols || ldy < rows)) { set_error("ldx/ldy below the matrix extent"); return -1; }
     const int threads = 256;
     const int rows_per_block = (threads / 64) * 4;
-    const size_t lds = (size_t) (xf32 ? 2 : 1) * ncol * (cols / 32) * 72;
+    /* Q6_K slots carry 8 bytes of pad per 128 columns */
+    const size_t lds = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (kind == 6 ? (cols / 128) * 8 : 0));
     if (lds > 160 * 1024) { set_error("%d activation columns of %d do not fit LDS", ncol, cols); return -1; }
     int grid = (rows + rows_per_block - 1) / rows_per_block;
     const int cap = cu_count() * 16;
@@ -428,6 +574,21 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
         else if (ncol <= 4) KQ_LAUNCH(K, 4, XF); \
         else KQ_LAUNCH(K, 16, XF);              \
     } while (0)
+    if (kind == 6 && cols <= 16384 && (cols / 256) % 2 == 0 && !((uintptr_t) blocks & 3) && !(xf32 && ncol > 4)) {
+        /* rows per workgroup: about one workgroup per CU, two rows per wave,
+         * the rows' blocks and x within LDS */
+        const size_t rowbytes = (size_t) (cols / 256) * 210;
+        const size_t xbytes = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (cols / 128) * 8);
+        int rpw = (rows + cu_count() - 1) / cu_count();
+        rpw = rpw < 2 ? 2 : (rpw > 16 ? 16 : rpw);
+        while (rpw > 2 && ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes > 160 * 1024) rpw--;
+        const size_t slds = ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes;
+        /* every workgroup's run of blocks must hold at least one 1 KB copy */
+        const size_t last = (size_t) (rows % rpw ? rows % rpw : rpw) * rowbytes;
+        if (slds <= 160 * 1024 && last >= 1024 && rpw * rowbytes >= 1024) {
+            return kq_q6k_staged(bp_in(blocks), rows, cols, x, xf32, ldx, ncol, y, ldy, accumulate, rpw, slds, s);
+        }
+    }
     if (kind == 6 && cols <= 12288) {
         /* eight rows per workgroup, every row's blocks requested at once */
         grid = (rows + 7) / 8;
