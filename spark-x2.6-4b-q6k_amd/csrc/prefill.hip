@@ -131,7 +131,7 @@ __device__ __forceinline__ uint32_t pf_field12(uint32_t w0, uint32_t w1, uint32_
     }
 }
 
-template <int NST, int EXT, int XF32>
+template <int NST, int EXT, int XF32, int PF>
 __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) P.nc * 8u;
@@ -171,20 +171,22 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
     }
     const uint8_t * xr = (const uint8_t *) P.x + (size_t) dtok * P.ldx * (XF32 ? 4 : 2) + 32 * h * (XF32 ? 4 : 2);
 
+    /* PF chunks of index words and x in flight: a ring of register slots,
+     * slot kc % PF holding chunk kc until it is decoded */
     constexpr int NXV = XF32 ? 8 : 4;
-    uint32_t wv[NST][3], pb[NST];
-    pf_u4 xv[NXV];
-    auto fetch = [&](int kc) {
+    uint32_t wv[PF][NST][3], pb[PF][NST];
+    pf_u4 xv[PF][NXV];
+    auto fetch = [&](int kc, int sl) {
 #pragma unroll
         for (int s = 0; s < NST; s++) {
             const uint32_t * wp = (const uint32_t *) (rs[s] + 24 * kc);
-            wv[s][0] = wp[0]; wv[s][1] = wp[1]; wv[s][2] = wp[2];
-            pb[s] = EXT ? ps[s][2 * kc] : 0u;
+            wv[sl][s][0] = wp[0]; wv[sl][s][1] = wp[1]; wv[sl][s][2] = wp[2];
+            pb[sl][s] = EXT ? ps[s][2 * kc] : 0u;
         }
 #pragma unroll
-        for (int k = 0; k < NXV; k++) xv[k] = ((const pf_u4 *) (xr + kPK * kc * (XF32 ? 4 : 2)))[k];
+        for (int k = 0; k < NXV; k++) xv[sl][k] = ((const pf_u4 *) (xr + kPK * kc * (XF32 ? 4 : 2)))[k];
     };
-    auto store = [&](int b) {
+    auto store = [&](int b, int sl) {
         _Float16 * ad = At + (b * kPR + dr) * kPS + 32 * h;
 #pragma unroll
         for (int jj = 0; jj < 8; jj += 2) {
@@ -195,8 +197,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
                 float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int s = 0; s < NST; s++) {
-                    uint32_t idx = pf_field12(wv[s][0], wv[s][1], wv[s][2], j);
-                    if (EXT) idx |= ((pb[s] >> j) & 1u) << 12;
+                    uint32_t idx = pf_field12(wv[sl][s][0], wv[sl][s][1], wv[sl][s][2], j);
+                    if (EXT) idx |= ((pb[sl][s] >> j) & 1u) << 12;
                     const pf_h4 c = *(const pf_h4 *) (lds + s * cbb + 8 * idx);
 #pragma unroll
                     for (int d = 0; d < 4; d++) acc[d] = __builtin_fmaf((float) c[d], g[s], acc[d]);
@@ -211,13 +213,13 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
         for (int k = 0; k < 4; k++) {
             pf_h8 v8;
             if (XF32) {
-                const pf_u4 lo = xv[2 * k], hi = xv[2 * k + 1];
+                const pf_u4 lo = xv[sl][2 * k], hi = xv[sl][2 * k + 1];
                 v8[0] = (_Float16) __uint_as_float(lo.x); v8[1] = (_Float16) __uint_as_float(lo.y);
                 v8[2] = (_Float16) __uint_as_float(lo.z); v8[3] = (_Float16) __uint_as_float(lo.w);
                 v8[4] = (_Float16) __uint_as_float(hi.x); v8[5] = (_Float16) __uint_as_float(hi.y);
                 v8[6] = (_Float16) __uint_as_float(hi.z); v8[7] = (_Float16) __uint_as_float(hi.w);
             } else {
-                const pf_u4 q = xv[k];
+                const pf_u4 q = xv[sl][k];
                 v8[0] = (_Float16) __uint_as_float(q.x << 16); v8[1] = (_Float16) __uint_as_float(q.x & 0xffff0000u);
                 v8[2] = (_Float16) __uint_as_float(q.y << 16); v8[3] = (_Float16) __uint_as_float(q.y & 0xffff0000u);
                 v8[4] = (_Float16) __uint_as_float(q.z << 16); v8[5] = (_Float16) __uint_as_float(q.z & 0xffff0000u);
@@ -240,28 +242,40 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
         for (int j = 0; j < 4; j++) acc[i][j] = pf_f4{0.f, 0.f, 0.f, 0.f};
 
     __syncthreads();   /* codebooks staged */
-    fetch(0);
-    store(0);
+#pragma unroll
+    for (int u = 0; u < PF; u++) fetch(min(u, nk - 1), u);
+    store(0, 0);
     __syncthreads();
-    for (int kc = 0; kc < nk; kc++) {
-        const int b = kc & 1;
-        if (kc + 1 < nk) fetch(kc + 1);
+    /* nk is a multiple of PF (even), so chunk kc0 + u uses buffer u & 1 and
+     * slot u; the body has no branches (chunks past the end are clamped and
+     * their decode lands in a buffer nobody reads), so the compiler counts
+     * the ring's loads exactly across iterations */
+    for (int kc0 = 0; kc0 < nk; kc0 += PF) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            pf_h8 a[4], bb[4];
+        for (int u = 0; u < PF; u++) {
+            const int kc = kc0 + u, b = u & 1;
+            /* keep each chunk's decode in its own step: hoisted above, it
+             * would wait for loads that are meant to stay in flight */
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(min(kc + PF, nk - 1), u);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                a[i] = *(const pf_h8 *) (At + (b * kPR + 64 * wm + 16 * i + m16) * kPS + 32 * ks + 8 * kq);
+            for (int ks = 0; ks < 2; ks++) {
+                pf_h8 a[4], bb[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                bb[j] = *(const pf_h8 *) (Bt + (b * kPT + 64 * wn + 16 * j + m16) * kPS + 32 * ks + 8 * kq);
+                for (int i = 0; i < 4; i++)
+                    a[i] = *(const pf_h8 *) (At + (b * kPR + 64 * wm + 16 * i + m16) * kPS + 32 * ks + 8 * kq);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int j = 0; j < 4; j++)
+                    bb[j] = *(const pf_h8 *) (Bt + (b * kPT + 64 * wn + 16 * j + m16) * kPS + 32 * ks + 8 * kq);
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bb[j], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bb[j], acc[i][j], 0, 0, 0);
+            }
+            store(b ^ 1, (u + 1) % PF);
+            __syncthreads();
         }
-        if (kc + 1 < nk) store(b ^ 1);
-        __syncthreads();
     }
 
     /* block (i, j): lane holds rows 4 kq .. 4 kq + 3 of token m16 */
@@ -294,17 +308,17 @@ int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int 
     return lds <= 160 * 1024;
 }
 
-template <int NST, int EXT, int XF32>
+template <int NST, int EXT, int XF32, int PF>
 static int prefill_mfma_t(const MfmaArgs & P, size_t lds, hipStream_t s) {
     static size_t opted = 0;
-    const void * fn = (const void *) prefill_mfma_kernel<NST, EXT, XF32>;
+    const void * fn = (const void *) prefill_mfma_kernel<NST, EXT, XF32, PF>;
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the MFMA prefill kernel", e);
         opted = lds;
     }
     const dim3 grid((unsigned) ((P.rows + kPR - 1) / kPR), (unsigned) ((P.ntok + kPT - 1) / kPT));
-    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32>, grid, dim3(256), (uint32_t) lds, s, P);
+    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32, PF>, grid, dim3(256), (uint32_t) lds, s, P);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("MFMA prefill launch", e);
 }
@@ -330,12 +344,18 @@ int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, 
     P.prow = (uint32_t) L.prow;
     const size_t lds = (size_t) nst * L.nc * 8 + (size_t) 4 * kPR * kPS * 2;
     const int ext = L.nbit > 12;
+    /* four chunks in flight when the chunk count allows, else two */
+    const int pf4 = (L.cols / kPK) % 4 == 0;
+#define PF_PICK(N, E, X) return pf4 ? prefill_mfma_t<N, E, X, 4>(P, lds, s) : prefill_mfma_t<N, E, X, 2>(P, lds, s)
     if (nst == 2) {
-        if (xf32) return ext ? prefill_mfma_t<2, 1, 1>(P, lds, s) : prefill_mfma_t<2, 0, 1>(P, lds, s);
-        return ext ? prefill_mfma_t<2, 1, 0>(P, lds, s) : prefill_mfma_t<2, 0, 0>(P, lds, s);
+        if (xf32) { if (ext) PF_PICK(2, 1, 1); PF_PICK(2, 0, 1); }
+        if (ext) PF_PICK(2, 1, 0);
+        PF_PICK(2, 0, 0);
     }
-    if (xf32) return ext ? prefill_mfma_t<1, 1, 1>(P, lds, s) : prefill_mfma_t<1, 0, 1>(P, lds, s);
-    return ext ? prefill_mfma_t<1, 1, 0>(P, lds, s) : prefill_mfma_t<1, 0, 0>(P, lds, s);
+    if (xf32) { if (ext) PF_PICK(1, 1, 1); PF_PICK(1, 0, 1); }
+    if (ext) PF_PICK(1, 1, 0);
+    PF_PICK(1, 0, 0);
+#undef PF_PICK
 }
 
 int prefill_simple_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32,
