@@ -320,9 +320,33 @@ def bench_prefill(args, sm, torch, dev):
             step()
         e1.record(stream)
         torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+        ms = e0.elapsed_time(e1) / args.steps
+        # the same step through the reference's ABI: xT [cols][ntok] f32, one
+        # launch per stage, tiled variant 2 with the runtime's 128 x 64 tile
+        # (vq-model-gpu.cu:296-299, :838-851); the null stream, as it uses
+        L = sm.lib()
+        xts = [x.float().t().contiguous() for _, x, _, _, _ in mats]
+        torch.cuda.synchronize()
+
+        def step_ref():
+            for (m, _, y, r, c), xT in zip(mats, xts):
+                for p in m.stage_ptrs:
+                    sm.check(L.vqg_prefill_launch_tile(p, 4, 4096, r, c, 1, xT.data_ptr(), ntok, y.data_ptr(),
+                                                       128, 64, 2), "reference-layout prefill")
+        for _ in range(args.warmup):
+            step_ref()
+        torch.cuda.synchronize()
+        r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        r0.record(torch.cuda.default_stream(dev))
+        for _ in range(args.steps):
+            step_ref()
+        r1.record(torch.cuda.default_stream(dev))
+        torch.cuda.synchronize()
+        ms_ref = r0.elapsed_time(r1) / args.steps
     flops = sum(2.0 * ntok * r * c for _, _, _, r, c in mats)
     tflops = flops / (ms * 1e-3) / 1e12
+    log(f"  reference ABI (xT f32, one launch per stage): {ms_ref * 1e3:.1f} us/step, "
+        f"{flops / (ms_ref * 1e-3) / 1e12:.1f} TFLOP/s")
     nbytes = sum(m.host.data.nbytes + 2 * ntok * c + 4 * ntok * r for m, _, _, r, c in mats)
     log(f"  prefill {ntok} tokens, up + down: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s")
     return {"metric": "prefill GEMM us/step (N=512, FFN up + down)", "value": round(ms * 1e3, 2), "unit": "us/step",
@@ -332,7 +356,10 @@ def bench_prefill(args, sm, torch, dev):
             "config": {"workload": "prefill GEMM, 512 bf16 tokens x (10240x2560 and 2560x10240 VQ)", "tokens": ntok},
             "roofline": {"bound": "mfma", "kernel": "prefill_mfma_kernel", "achieved": round(tflops, 1),
                          "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
-                         "traffic": None, "flops_per_step": flops, "bytes_per_step": int(nbytes)}}
+                         "traffic": None, "flops_per_step": flops, "bytes_per_step": int(nbytes)},
+            "reference_abi": {"us_per_step": round(ms_ref * 1e3, 2),
+                              "tflops": round(flops / (ms_ref * 1e-3) / 1e12, 1),
+                              "route": "vqg_prefill_launch_tile variant 2, xT [cols][512] f32, one launch per stage"}}
 
 
 def main():

@@ -181,11 +181,27 @@ int vqg_row_dequant(const void * payload, int dim, int nc, int rows, int cols, i
     return vq_row_dequant_launch(payload, make_layout(dim, nc, rows, cols, v3), row, out, 0);
 }
 
-/* ---- prefill (reference layout: xT [cols][ntok], y [ntok][rows]) ---- */
+/* ---- prefill (reference layout: xT [cols][ntok], y [ntok][rows]) ----
+ * Variants are numbered as the reference numbers them
+ * (tools/vq/gpu/decode-gpu.cu:995-1004, :1017-1025): 1 and 2 are its tiled
+ * f16 GEMMs (codebook through L1 / in shared memory), 3 its legacy
+ * one-thread-per-output kernel, 0 picks 1 when the geometry allows it, else 3.
+ * Readiness follows the reference's rules, so its runtime chooses the same
+ * variant it would on CUDA (vq-model-gpu.cu:296-297). Here variants 1 and 2
+ * both run the MFMA GEMM when it takes the call (dim 4, columns a multiple
+ * of 128, 16-byte aligned xT with ntok a multiple of 4) and the
+ * one-thread-per-output kernel otherwise; a tile (bn, bk) of the tuner's
+ * table is accepted and leaves the gfx950 kernel's 128 x 128 x 64 tile as is. */
 
 struct PreCfg { int bn, bk; };
-static const PreCfg k_pre_cfg[] = { { 64, 64 }, { 128, 64 } };
+static const PreCfg k_pre_cfg[] = { { 64, 64 }, { 128, 64 }, { 256, 64 } };
 static const int k_pre_ncfg = (int) (sizeof k_pre_cfg / sizeof k_pre_cfg[0]);
+
+/* the tiled kernels' geometry rule, decode-gpu.cu:527-530 */
+static int pre_ok(const Layout & L, int bk) {
+    return L.v3 && (L.dim == 4 || L.dim == 8) && L.rows > 0 && L.cols > 0 && L.nbit >= 12 && bk > 0
+        && L.cols % bk == 0 && L.mrow % 4 == 0 && L.stream_off % 4 == 0;
+}
 
 int vqg_prefill_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
     if (dim <= 0 || nc <= 0 || rows <= 0 || cols <= 0 || cols % dim) return 0;
@@ -193,6 +209,7 @@ int vqg_prefill_ready(int dim, int nc, int rows, int cols, int v3, int variant) 
     const Layout L = make_layout(dim, nc, rows, cols, v3);
     switch (variant) {
         case 0: return 1;
+        case 1: case 2: return pre_ok(L, 64);
         case 3: return L.nidx_row * 2 <= 64 * 1024;
         default: return 0;
     }
@@ -208,9 +225,11 @@ int vqg_prefill_cfg(int idx, int * bn, int * bk) {
 }
 
 int vqg_prefill_cfg_ready(int dim, int nc, int rows, int cols, int v3, int bn, int bk, int variant) {
-    (void) bn; (void) bk;
+    (void) bn;
     if (variant == 3) return vqg_prefill_ready(dim, nc, rows, cols, v3, 3);
-    return 0;
+    if (variant != 1 && variant != 2) return 0;
+    if (!vqg_prefill_ready(dim, nc, rows, cols, v3, variant)) return 0;
+    return pre_ok(make_layout(dim, nc, rows, cols, v3), bk);
 }
 
 static int prefill_ref_layout(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * xT,
@@ -218,10 +237,20 @@ static int prefill_ref_layout(const void * payload, int dim, int nc, int rows, i
     if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
     if (ntok <= 0) { set_error("prefill needs at least one token"); return -1; }
     if (!payload || !xT || !y) { set_error("null pointer passed to prefill"); return -1; }
-    if (variant == 0) variant = 3;
-    if (variant != 3) { set_error("prefill variant %d does not take this geometry", variant); return -1; }
     const Layout L = make_layout(dim, nc, rows, cols, v3);
+    if (variant == 0) variant = pre_ok(L, 64) ? 1 : 3;
+    if (variant < 1 || variant > 3) { set_error("unknown prefill variant %d", variant); return -1; }
+    if (variant != 3 && !pre_ok(L, 64)) {
+        set_error("prefill variant %d does not take this geometry", variant);
+        return -1;
+    }
     const void * st[1] = { payload };
+    if (variant != 3 && prefill_mfma_ready(L, 1, xT, 1, ntok, 1, ntok))
+        return prefill_mfma_launch(st, 1, L, xT, 1, ntok, 1, ntok, y, rows, 1, 0);
+    if (variant == 3 && !vqg_prefill_ready(dim, nc, rows, cols, v3, 3)) {
+        set_error("the legacy prefill kernel stages %zu bytes of indices per row, more than it holds", L.nidx_row * 2);
+        return -1;
+    }
     return prefill_simple_launch(st, 1, L, xT, 1, 1, (size_t) ntok, ntok, y, rows, 1, 0);
 }
 
@@ -369,11 +398,11 @@ int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc
         if (!stages[i]) { set_error("stage %d payload is null", i); return -1; }
     const Layout L = make_layout(dim, nc, rows, cols, v3);
     const int xf32 = x_dtype == SPARKMV_X_F32;
-    if (prefill_mfma_ready(L, nstages < 2 ? nstages : 2, x, xf32, ldx)) {
+    if (prefill_mfma_ready(L, nstages < 2 ? nstages : 2, x, xf32, ldx, 0, ntok)) {
         /* the matrix cores, two stages per launch; later pairs accumulate */
         for (int s0 = 0; s0 < nstages; s0 += 2) {
             const int n = nstages - s0 < 2 ? nstages - s0 : 2;
-            if (prefill_mfma_launch(stages + s0, n, L, x, xf32, ldx, ntok, y, ldy, accumulate || s0 > 0,
+            if (prefill_mfma_launch(stages + s0, n, L, x, xf32, ldx, 0, ntok, y, ldy, accumulate || s0 > 0,
                                     (hipStream_t) stream))
                 return -1;
         }

@@ -10,11 +10,13 @@ namespace sparkmv {
 int prefill_simple_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32,
                           size_t xs_t, size_t xs_k, int ntok, float * y, int ldy, int accumulate, hipStream_t s);
 
-/* The MFMA GEMM: DQV3 dim 4, 12/13-bit indices, 1 or 2 stages, token-major
- * x (bf16 or f32) with 16-byte aligned rows; y[t * ldy + r] (+)= W x_t.
- * Weights are decoded to f16 tiles (one rounding of the f32 decode). */
-int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int ldx);
+/* The MFMA GEMM: DQV3 dim 4, 12/13-bit indices, 1 or 2 stages, x in
+ * 16-byte aligned rows, y[t * ldy + r] (+)= W x_t. x is token-major
+ * (x[t * ldx + k], bf16 or f32) or, with xt, K-major f32 of one stage
+ * (x[k * ldx + t], the reference's xT layout, ntok >= 4). Weights are decoded
+ * to f16 tiles (one rounding of the f32 decode). */
+int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int ldx, int xt, int ntok);
 int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
-                        int ntok, float * y, int ldy, int accumulate, hipStream_t s);
+                        int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s);
 
 }  // namespace sparkmv

@@ -111,7 +111,7 @@ constexpr int kPS = 72;    /* LDS row stride of a tile in halves (64 + 8 pad: co
 
 struct MfmaArgs {
     const uint8_t * st[2];
-    const void * x;      /* token-major: x[t * ldx + k], bf16 bits or f32 */
+    const void * x;      /* token-major: x[t * ldx + k], bf16 bits or f32; K-major (XT): f32 x[k * ldx + t] */
     float * y;           /* y[t * ldy + r] */
     int rows, cols, nc, ntok, ldx, ldy, accumulate;
     uint32_t gain_off, stream_off, mrow, prow;
@@ -131,7 +131,7 @@ __device__ __forceinline__ uint32_t pf_field12(uint32_t w0, uint32_t w1, uint32_
     }
 }
 
-template <int NST, int EXT, int XF32, int PF>
+template <int NST, int EXT, int XF32, int PF, int XT>
 __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) P.nc * 8u;
@@ -170,6 +170,11 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
         ps[s] = P.st[s] + P.stream_off + (size_t) P.rows * P.mrow + (size_t) drow * P.prow + h;
     }
     const uint8_t * xr = (const uint8_t *) P.x + (size_t) dtok * P.ldx * (XF32 ? 4 : 2) + 32 * h * (XF32 ? 4 : 2);
+    /* K-major x role (the reference's xT[cols][ntok]): tokens 4 tq .. 4 tq + 3
+     * of the tile, columns 8 cg .. 8 cg + 7 of a chunk; lanes run along the
+     * tokens, so each 16-byte load of a wave reads 512 contiguous bytes */
+    const int tq = tid & 31, cg = tid >> 5;
+    const float * xk = (const float *) P.x + (size_t) (8 * cg) * P.ldx + min(t0 + 4 * tq, P.ntok - 4);
 
     /* PF chunks of index words and x in flight: a ring of register slots,
      * slot kc % PF holding chunk kc until it is decoded */
@@ -183,8 +188,13 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
             wv[sl][s][0] = wp[0]; wv[sl][s][1] = wp[1]; wv[sl][s][2] = wp[2];
             pb[sl][s] = EXT ? ps[s][2 * kc] : 0u;
         }
+        if constexpr (XT) {
 #pragma unroll
-        for (int k = 0; k < NXV; k++) xv[sl][k] = ((const pf_u4 *) (xr + kPK * kc * (XF32 ? 4 : 2)))[k];
+            for (int k = 0; k < NXV; k++) xv[sl][k] = *(const pf_u4 *) (xk + (size_t) (kPK * kc + k) * P.ldx);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NXV; k++) xv[sl][k] = ((const pf_u4 *) (xr + kPK * kc * (XF32 ? 4 : 2)))[k];
+        }
     };
     auto store = [&](int b, int sl) {
         _Float16 * ad = At + (b * kPR + dr) * kPS + 32 * h;
@@ -207,6 +217,18 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
                 for (int d = 0; d < 4; d++) w8[4 * u + d] = (_Float16) acc[d];
             }
             *(pf_h8 *) (ad + 4 * jj) = w8;
+        }
+        if constexpr (XT) {
+            /* xv[c] holds tokens 4 tq .. +3 of column 8 cg + c: one 16-byte
+             * row of eight columns per token */
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pf_h8 v8;
+#pragma unroll
+                for (int c = 0; c < 8; c++) v8[c] = (_Float16) __uint_as_float(xv[sl][c][i]);
+                *(pf_h8 *) (Bt + (b * kPT + 4 * tq + i) * kPS + 8 * cg) = v8;
+            }
+            return;
         }
         _Float16 * bd = Bt + (b * kPT + dr) * kPS + 32 * h;
 #pragma unroll
@@ -298,34 +320,36 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
 
 /* The MFMA kernel takes DQV3 dim-4 stages with 12- or 13-bit indices, 1 or
  * 2 stages, an even codebook, columns a multiple of 128, dword-aligned row
- * streams, and token-major x in 16-byte aligned rows. */
-int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int ldx) {
+ * streams, and x in 16-byte aligned rows: token-major, or K-major f32 of one
+ * stage with at least 4 tokens (xt). */
+int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int ldx, int xt, int ntok) {
     if (!L.v3 || L.dim != 4 || L.nbit < 12 || L.nbit > 13 || nst < 1 || nst > 2) return 0;
     if (L.nc % 2 || L.cols % 128 || L.stream_off % 4 || L.mrow % 4) return 0;
     if ((uintptr_t) x & 15u) return 0;
     if (ldx % (xf32 ? 4 : 8)) return 0;
+    if (xt && (!xf32 || nst != 1 || ntok < 4 || ldx < ntok)) return 0;
     const size_t lds = (size_t) nst * L.nc * 8 + (size_t) 4 * kPR * kPS * 2;
     return lds <= 160 * 1024;
 }
 
-template <int NST, int EXT, int XF32, int PF>
+template <int NST, int EXT, int XF32, int PF, int XT = 0>
 static int prefill_mfma_t(const MfmaArgs & P, size_t lds, hipStream_t s) {
     static size_t opted = 0;
-    const void * fn = (const void *) prefill_mfma_kernel<NST, EXT, XF32, PF>;
+    const void * fn = (const void *) prefill_mfma_kernel<NST, EXT, XF32, PF, XT>;
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the MFMA prefill kernel", e);
         opted = lds;
     }
     const dim3 grid((unsigned) ((P.rows + kPR - 1) / kPR), (unsigned) ((P.ntok + kPT - 1) / kPT));
-    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32, PF>, grid, dim3(256), (uint32_t) lds, s, P);
+    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32, PF, XT>, grid, dim3(256), (uint32_t) lds, s, P);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("MFMA prefill launch", e);
 }
 
 int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
-                        int ntok, float * y, int ldy, int accumulate, hipStream_t s) {
-    if (!prefill_mfma_ready(L, nst, x, xf32, ldx)) {
+                        int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s) {
+    if (!prefill_mfma_ready(L, nst, x, xf32, ldx, xt, ntok)) {
         set_error("the MFMA prefill kernel does not take this geometry, stage count or x layout");
         return -1;
     }
@@ -347,6 +371,10 @@ int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, 
     /* four chunks in flight when the chunk count allows, else two */
     const int pf4 = (L.cols / kPK) % 4 == 0;
 #define PF_PICK(N, E, X) return pf4 ? prefill_mfma_t<N, E, X, 4>(P, lds, s) : prefill_mfma_t<N, E, X, 2>(P, lds, s)
+    if (xt) {   /* one stage, f32 (checked above) */
+        if (ext) return pf4 ? prefill_mfma_t<1, 1, 1, 4, 1>(P, lds, s) : prefill_mfma_t<1, 1, 1, 2, 1>(P, lds, s);
+        return pf4 ? prefill_mfma_t<1, 0, 1, 4, 1>(P, lds, s) : prefill_mfma_t<1, 0, 1, 2, 1>(P, lds, s);
+    }
     if (nst == 2) {
         if (xf32) { if (ext) PF_PICK(2, 1, 1); PF_PICK(2, 0, 1); }
         if (ext) PF_PICK(2, 1, 0);

@@ -56,6 +56,36 @@ def test_readiness_rules(sm):
     assert L.vqg_gemv_ready(4, 4096, 1, 10, 1, 0) == 0         # cols not a multiple of dim
 
 
+def test_prefill_readiness_rules(sm):
+    """The reference's prefill rules (decode-gpu.cu:527-558, :995-1025): its
+    tuner's three tiles, tiled variants 1 and 2 for DQV3 dim 4/8 streams of
+    at least 12 bits whose columns split into 64-column rounds, the legacy
+    variant 3 and the picker 0 for anything."""
+    L = sm.lib()
+    assert L.vqg_prefill_cfg_count() == 3
+    tiles = []
+    for i in range(3):
+        bn, bk = ctypes.c_int(), ctypes.c_int()
+        assert L.vqg_prefill_cfg(i, ctypes.byref(bn), ctypes.byref(bk)) == 0
+        tiles.append((bn.value, bk.value))
+    assert tiles == [(64, 64), (128, 64), (256, 64)]
+    assert L.vqg_prefill_cfg(3, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == -1
+    for v in (0, 1, 2, 3):
+        assert L.vqg_prefill_ready(4, 4096, 10240, 2560, 1, v) == 1
+        assert L.vqg_prefill_ready(4, 8192, 2560, 10240, 1, v) == 1
+    for v in (1, 2):
+        assert L.vqg_prefill_ready(4, 4096, 64, 2560, 0, v) == 0    # DQVQ: legacy only
+        assert L.vqg_prefill_ready(4, 1024, 64, 2560, 1, v) == 0    # 10-bit stream
+        assert L.vqg_prefill_ready(4, 4096, 64, 2592, 1, v) == 0    # 2592 columns: not whole 64-column rounds
+        assert L.vqg_prefill_ready(8, 4096, 64, 2560, 1, v) == 1    # dim 8 runs (one thread per output here)
+        assert L.vqg_prefill_cfg_ready(4, 4096, 64, 2560, 1, 128, 64, v) == 1
+        assert L.vqg_prefill_cfg_ready(4, 4096, 64, 2560, 1, 128, 48, v) == 0   # 2560 % 48 != 0
+    assert L.vqg_prefill_ready(4, 4096, 64, 2560, 0, 3) == 1
+    assert L.vqg_prefill_cfg_ready(4, 4096, 64, 2560, 0, 1, 1, 3) == 1
+    assert L.vqg_prefill_ready(4, 4096, 64, 2560, 1, 4) == 0
+    assert L.vqg_prefill_cfg_ready(4, 4096, 64, 2560, 1, 128, 64, 0) == 0
+
+
 @pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))))
 def test_container_open_agrees_with_oracle(sm, ref, path):
     with np.load(path, allow_pickle=False) as z:

@@ -282,6 +282,40 @@ def test_prefill_reference_layout(sm, ref, dev):
     assert rel_l2(y.cpu().numpy(), x.astype(np.float64) @ W.T) <= BAR
 
 
+@pytest.mark.parametrize("rows,cols,ntok,nc,variant,tile", [(320, 2560, 200, 4096, 2, (128, 64)),
+                                                          (130, 1024, 512, 8192, 1, (64, 64)),
+                                                          (64, 512, 36, 4096, 0, None),
+                                                          (48, 640, 37, 4096, 2, (256, 64)),
+                                                          (96, 256, 12, 4096, 3, None)])
+def test_prefill_reference_layout_variants(sm, ref, dev, rows, cols, ntok, nc, variant, tile):
+    """The reference's prefill ABI (xT [cols][ntok] f32, y [ntok][rows]
+    accumulating, one stage per call, as vq-model-gpu.cu:838-851 drives it).
+    Tiled variants with ntok a multiple of 4 run the matrix cores on K-major
+    x; 37 tokens and the legacy variant run one thread per output. The bar
+    is the GEMM gate's 1e-3 relative L2 (weights enter the MFMA as f16)."""
+    import torch
+    data = sm.synth_container(rows + ntok + variant, rows, cols, 4, nc, 2, 1)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    x = np.random.default_rng(ntok).standard_normal((ntok, cols)).astype(np.float32)
+    xT = torch.from_numpy(np.ascontiguousarray(x.T)).to(dev)
+    base = np.random.default_rng(rows).standard_normal((ntok, rows)).astype(np.float32)
+    y = torch.from_numpy(base.copy()).to(dev)
+    L = sm.lib()
+    for p in dc.stage_ptrs:
+        if tile is None:
+            rc = L.vqg_prefill_launch(p, 4, nc, rows, cols, 1, xT.data_ptr(), ntok, y.data_ptr(), variant)
+        else:
+            rc = L.vqg_prefill_launch_tile(p, 4, nc, rows, cols, 1, xT.data_ptr(), ntok, y.data_ptr(),
+                                           tile[0], tile[1], variant)
+        sm.check(rc, "prefill")
+    torch.cuda.synchronize()
+    want = x.astype(np.float64) @ W.T
+    err = rel_l2(y.cpu().numpy() - base, want)
+    print(f"reference-layout prefill {rows}x{cols} ntok {ntok} nc {nc} variant {variant}: relL2 {err:.2e}")
+    assert err <= BAR
+
+
 def test_full_size_ffn_up(sm, ref, dev):
     """10240 x 2560, dim 4, nc 4096, 2 stages, bf16 x: the single-GEMV workload
     at its real size, against the oracle's decode and an f64 matvec."""
