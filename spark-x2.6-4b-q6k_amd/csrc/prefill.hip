@@ -101,6 +101,7 @@ __global__ __launch_bounds__(256) void prefill_simple_kernel(const SimpleArgs A)
 typedef _Float16 pf_h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 pf_h8 __attribute__((ext_vector_type(8)));
 typedef float pf_f4 __attribute__((ext_vector_type(4)));
+typedef float pf_f16v __attribute__((ext_vector_type(16)));
 typedef uint32_t pf_u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t pf_u4a __attribute__((ext_vector_type(4), aligned(4)));
 
@@ -131,8 +132,10 @@ __device__ __forceinline__ uint32_t pf_field12(uint32_t w0, uint32_t w1, uint32_
     }
 }
 
+constexpr int kPThreads = 512;   /* 8 waves: two per SIMD, so one wave's decode hides another's latency */
+
 template <int NST, int EXT, int XF32, int PF, int XT>
-__global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
+__global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) P.nc * 8u;
     _Float16 * At = (_Float16 *) (lds + NST * cbb);   /* [2][kPR][kPS] decoded weights */
@@ -144,48 +147,52 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
     /* codebooks to LDS in batches of unconditional 16-byte loads */
     {
         const int n16 = (int) (cbb >> 4), ncb = NST * n16;
-        for (int base = 0; base < ncb; base += 8 * 256) {
-            pf_u4 v[8];
+        for (int base = 0; base < ncb; base += 4 * kPThreads) {
+            pf_u4 v[4];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int i = min(base + k * 256 + tid, ncb - 1), s = i >= n16 ? 1 : 0;
+            for (int k = 0; k < 4; k++) {
+                const int i = min(base + k * kPThreads + tid, ncb - 1), s = i >= n16 ? 1 : 0;
                 v[k] = ((const pf_u4a *) (P.st[NST > 1 ? s : 0] + 24))[i - s * n16];
             }
 #pragma unroll
-            for (int k = 0; k < 8; k++) ((pf_u4 *) lds)[min(base + k * 256 + tid, ncb - 1)] = v[k];
+            for (int k = 0; k < 4; k++) ((pf_u4 *) lds)[min(base + k * kPThreads + tid, ncb - 1)] = v[k];
         }
     }
 
-    /* decode role: row dr of the tile, columns 32 h .. 32 h + 31 of a chunk
-     * (8 indices); x role: token dr of the tile, the same columns */
-    const int dr = tid >> 1, h = tid & 1;
+    /* decode role: row dr of the tile, columns 16 h .. 16 h + 15 of a chunk
+     * (4 indices, bits 48 h .. 48 h + 47 of the chunk's 24 stream bytes:
+     * the two dwords from byte 6 h rounded down, shifted by 0 or 16 bits);
+     * x role (token-major): token dr of the tile, the same columns */
+    const int dr = tid >> 2, h = tid & 3;
     const int drow = min(r0 + dr, P.rows - 1), dtok = min(t0 + dr, P.ntok - 1);
+    const int wd = (6 * h) >> 2;
+    const uint32_t wsh = (uint32_t) ((6 * h) & 3) * 8u;
     float g[NST];
-    const uint8_t * rs[NST];
+    const uint32_t * rs[NST];
     const uint8_t * ps[NST];
 #pragma unroll
     for (int s = 0; s < NST; s++) {
         g[s] = (float) *(const _Float16 *) (P.st[s] + P.gain_off + 2 * (size_t) drow);
-        rs[s] = P.st[s] + P.stream_off + (size_t) drow * P.mrow + 12 * h;
-        ps[s] = P.st[s] + P.stream_off + (size_t) P.rows * P.mrow + (size_t) drow * P.prow + h;
+        rs[s] = (const uint32_t *) (P.st[s] + P.stream_off + (size_t) drow * P.mrow) + wd;
+        ps[s] = P.st[s] + P.stream_off + (size_t) P.rows * P.mrow + (size_t) drow * P.prow + (h >> 1);
     }
-    const uint8_t * xr = (const uint8_t *) P.x + (size_t) dtok * P.ldx * (XF32 ? 4 : 2) + 32 * h * (XF32 ? 4 : 2);
+    const uint8_t * xr = (const uint8_t *) P.x + ((size_t) dtok * P.ldx + 16 * h) * (XF32 ? 4 : 2);
     /* K-major x role (the reference's xT[cols][ntok]): tokens 4 tq .. 4 tq + 3
-     * of the tile, columns 8 cg .. 8 cg + 7 of a chunk; lanes run along the
+     * of the tile, columns 4 cg .. 4 cg + 3 of a chunk; lanes run along the
      * tokens, so each 16-byte load of a wave reads 512 contiguous bytes */
     const int tq = tid & 31, cg = tid >> 5;
-    const float * xk = (const float *) P.x + (size_t) (8 * cg) * P.ldx + min(t0 + 4 * tq, P.ntok - 4);
+    const float * xk = (const float *) P.x + (size_t) (4 * cg) * P.ldx + min(t0 + 4 * tq, P.ntok - 4);
 
     /* PF chunks of index words and x in flight: a ring of register slots,
      * slot kc % PF holding chunk kc until it is decoded */
-    constexpr int NXV = XF32 ? 8 : 4;
-    uint32_t wv[PF][NST][3], pb[PF][NST];
+    constexpr int NXV = XT ? 4 : (XF32 ? 4 : 2);
+    uint32_t wv[PF][NST][2], pb[PF][NST];
     pf_u4 xv[PF][NXV];
     auto fetch = [&](int kc, int sl) {
 #pragma unroll
         for (int s = 0; s < NST; s++) {
-            const uint32_t * wp = (const uint32_t *) (rs[s] + 24 * kc);
-            wv[sl][s][0] = wp[0]; wv[sl][s][1] = wp[1]; wv[sl][s][2] = wp[2];
+            wv[sl][s][0] = rs[s][6 * kc];
+            wv[sl][s][1] = rs[s][6 * kc + 1];
             pb[sl][s] = EXT ? ps[s][2 * kc] : 0u;
         }
         if constexpr (XT) {
@@ -197,42 +204,42 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
         }
     };
     auto store = [&](int b, int sl) {
-        _Float16 * ad = At + (b * kPR + dr) * kPS + 32 * h;
+        pf_h8 w8[2];
 #pragma unroll
-        for (int jj = 0; jj < 8; jj += 2) {
-            pf_h8 w8;
+        for (int j = 0; j < 4; j++) {
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int j = jj + u;
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < NST; s++) {
+                const uint32_t lo = __builtin_amdgcn_alignbit(wv[sl][s][1], wv[sl][s][0], wsh);
+                const uint32_t hi = wv[sl][s][1] >> wsh;
+                uint32_t idx = j == 0 ? lo : j == 1 ? lo >> 12 : j == 2 ? __builtin_amdgcn_alignbit(hi, lo, 24) : hi >> 4;
+                idx &= 0xfffu;
+                if (EXT) idx |= ((pb[sl][s] >> (4 * (h & 1) + j)) & 1u) << 12;
+                const pf_h4 c = *(const pf_h4 *) (lds + s * cbb + 8 * idx);
 #pragma unroll
-                for (int s = 0; s < NST; s++) {
-                    uint32_t idx = pf_field12(wv[sl][s][0], wv[sl][s][1], wv[sl][s][2], j);
-                    if (EXT) idx |= ((pb[sl][s] >> j) & 1u) << 12;
-                    const pf_h4 c = *(const pf_h4 *) (lds + s * cbb + 8 * idx);
-#pragma unroll
-                    for (int d = 0; d < 4; d++) acc[d] = __builtin_fmaf((float) c[d], g[s], acc[d]);
-                }
-#pragma unroll
-                for (int d = 0; d < 4; d++) w8[4 * u + d] = (_Float16) acc[d];
+                for (int d = 0; d < 4; d++) acc[d] = __builtin_fmaf((float) c[d], g[s], acc[d]);
             }
-            *(pf_h8 *) (ad + 4 * jj) = w8;
+#pragma unroll
+            for (int d = 0; d < 4; d++) w8[j >> 1][4 * (j & 1) + d] = (_Float16) acc[d];
         }
+        _Float16 * ad = At + (b * kPR + dr) * kPS + 16 * h;
+        *(pf_h8 *) ad = w8[0];
+        *(pf_h8 *) (ad + 8) = w8[1];
         if constexpr (XT) {
-            /* xv[c] holds tokens 4 tq .. +3 of column 8 cg + c: one 16-byte
-             * row of eight columns per token */
+            /* xv[c] holds tokens 4 tq .. +3 of column 4 cg + c: four
+             * columns (8 bytes) per token */
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                pf_h8 v8;
+                pf_h4 v4;
 #pragma unroll
-                for (int c = 0; c < 8; c++) v8[c] = (_Float16) __uint_as_float(xv[sl][c][i]);
-                *(pf_h8 *) (Bt + (b * kPT + 4 * tq + i) * kPS + 8 * cg) = v8;
+                for (int c = 0; c < 4; c++) v4[c] = (_Float16) __uint_as_float(xv[sl][c][i]);
+                *(pf_h4 *) (Bt + (b * kPT + 4 * tq + i) * kPS + 4 * cg) = v4;
             }
             return;
         }
-        _Float16 * bd = Bt + (b * kPT + dr) * kPS + 32 * h;
+        _Float16 * bd = Bt + (b * kPT + dr) * kPS + 16 * h;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < 2; k++) {
             pf_h8 v8;
             if (XF32) {
                 const pf_u4 lo = xv[sl][2 * k], hi = xv[sl][2 * k + 1];
@@ -251,17 +258,18 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
         }
     };
 
-    /* MFMA role: wave (wm, wn) owns rows 64 wm .. +63 and tokens 64 wn .. +63
-     * of the tile as 4 x 4 blocks of 16 x 16. A lane's operand is 8
-     * consecutive columns of one row (A) or one token (B); A and B assign
-     * columns to lanes the same way, so each block is a plain dot over the
-     * chunk's columns. */
-    const int wm = wave & 1, wn = wave >> 1, m16 = lane & 15, kq = lane >> 4;
-    pf_f4 acc[4][4];
+    /* MFMA role: wave (wm, wn) owns rows 64 wm .. +63 and tokens 32 wn .. +31
+     * of the tile as 2 blocks of 32 x 32 (v_mfma_f32_32x32x16_f16: each
+     * operand element serves 32 outputs, half the LDS reads of 16 x 16
+     * blocks). A lane's operand is 8 consecutive columns of one row (A) or
+     * one token (B); A and B assign columns to lanes the same way, so each
+     * block is a plain dot over the chunk's columns. */
+    const int wm = wave & 1, wn = wave >> 1, m32 = lane & 31, kh = lane >> 5;
+    pf_f16v acc[2];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = pf_f4{0.f, 0.f, 0.f, 0.f};
+        for (int e = 0; e < 16; e++) acc[i][e] = 0.0f;
 
     __syncthreads();   /* codebooks staged */
 #pragma unroll
@@ -281,41 +289,35 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const MfmaArgs P) {
             __builtin_amdgcn_sched_barrier(0);
             fetch(min(kc + PF, nk - 1), u);
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                pf_h8 a[4], bb[4];
+            for (int ks = 0; ks < 4; ks++) {
+                pf_h8 a[2];
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    a[i] = *(const pf_h8 *) (At + (b * kPR + 64 * wm + 16 * i + m16) * kPS + 32 * ks + 8 * kq);
+                for (int i = 0; i < 2; i++)
+                    a[i] = *(const pf_h8 *) (At + (b * kPR + 64 * wm + 32 * i + m32) * kPS + 16 * ks + 8 * kh);
+                const pf_h8 bb = *(const pf_h8 *) (Bt + (b * kPT + 32 * wn + m32) * kPS + 16 * ks + 8 * kh);
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    bb[j] = *(const pf_h8 *) (Bt + (b * kPT + 64 * wn + 16 * j + m16) * kPS + 32 * ks + 8 * kq);
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bb[j], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bb, acc[i], 0, 0, 0);
             }
             store(b ^ 1, (u + 1) % PF);
             __syncthreads();
         }
     }
 
-    /* block (i, j): lane holds rows 4 kq .. 4 kq + 3 of token m16 */
+    /* block i: entry e of a lane is row 8 (e / 4) + 4 kh + e % 4 of the
+     * block, token m32 */
+    const int tok = t0 + 32 * wn + m32;
+    if (tok < P.ntok) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int tok = t0 + 64 * wn + 16 * j + m16;
-            if (tok >= P.ntok) continue;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int row = r0 + 64 * wm + 16 * i + 4 * kq + e;
+            for (int e = 0; e < 16; e++) {
+                const int row = r0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
                 if (row < P.rows) {
                     float * yp = P.y + (size_t) tok * P.ldy + row;
-                    *yp = (P.accumulate ? *yp : 0.0f) + acc[i][j][e];
+                    *yp = (P.accumulate ? *yp : 0.0f) + acc[i][e];
                 }
             }
-        }
+    }
 }
 
 /* The MFMA kernel takes DQV3 dim-4 stages with 12- or 13-bit indices, 1 or
@@ -342,7 +344,7 @@ static int prefill_mfma_t(const MfmaArgs & P, size_t lds, hipStream_t s) {
         opted = lds;
     }
     const dim3 grid((unsigned) ((P.rows + kPR - 1) / kPR), (unsigned) ((P.ntok + kPT - 1) / kPT));
-    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32, PF, XT>, grid, dim3(256), (uint32_t) lds, s, P);
+    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32, PF, XT>, grid, dim3(kPThreads), (uint32_t) lds, s, P);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("MFMA prefill launch", e);
 }
