@@ -123,11 +123,12 @@ def time_steps(plan, torch, stream, steps, warmup, mode):
     return start.elapsed_time(end) / steps
 
 
-def cpu_baseline_decode_set(sample_layers=4, head_rows=16384, reps=9):
+def cpu_baseline_decode_set(sample_layers=LAYERS, head_rows=VOCAB, reps=9):
     """The oracle's runtime path (model.rs:209-234): containers decoded to f32
-    once, then a row-parallel 8-lane dot per matvec, all host threads. Timed
-    on a bounded sample (a few layers and a slice of the head) and scaled to
-    one token of the full set."""
+    once, then a row-parallel 8-lane dot per matvec, all host threads. By
+    default the whole token is timed (every layer and the full head, one
+    layer decoded at a time, the median of `reps` runs of each); a smaller
+    sample is scaled to one token."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import sparkmv as sm
     import sparkref as ref
@@ -154,9 +155,11 @@ def cpu_baseline_decode_set(sample_layers=4, head_rows=16384, reps=9):
         ref.matvec(Wh, xh, nth)
         th.append(time.perf_counter() - t)
     us = (np.mean(per_layer) * LAYERS + np.median(th) * VOCAB / head_rows) * 1e6
+    whole = sample_layers == LAYERS and head_rows == VOCAB
     return {"value": round(float(us), 1), "unit": "us/token", "cores": int(nth), "kind": "port",
-            "sample": f"oracle decode-to-f32 + row-parallel 8-lane dot (model.rs:209-234) on {sample_layers} of 36 "
-                      f"layers and {head_rows} of {VOCAB} head rows, median of {reps}, scaled to one token"}
+            "sample": f"oracle decode-to-f32 + row-parallel 8-lane dot (model.rs:209-234) on {sample_layers} of "
+                      f"{LAYERS} layers and {head_rows} of {VOCAB} head rows, median of {reps} per layer and for the "
+                      f"head" + (", summed: one whole token" if whole else ", scaled to one token")}
 
 
 def bench_decode_set(args, sm, torch, dev):
