@@ -105,7 +105,7 @@ typedef float pf_f16v __attribute__((ext_vector_type(16)));
 typedef uint32_t pf_u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t pf_u4a __attribute__((ext_vector_type(4), aligned(4)));
 
-constexpr int kPR = 128;   /* rows per workgroup tile */
+constexpr int kPR = 128;   /* rows per workgroup tile (the larger of the two tile heights) */
 constexpr int kPT = 128;   /* tokens per workgroup tile */
 constexpr int kPK = 64;    /* columns per chunk */
 constexpr int kPS = 72;    /* LDS row stride of a tile in halves (64 + 8 pad: conflict-free 16-byte reads) */
@@ -134,14 +134,14 @@ __device__ __forceinline__ uint32_t pf_field12(uint32_t w0, uint32_t w1, uint32_
 
 constexpr int kPThreads = 512;   /* 8 waves: two per SIMD, so one wave's decode hides another's latency */
 
-template <int NST, int EXT, int XF32, int PF, int XT>
+template <int NST, int EXT, int XF32, int PF, int XT, int RT>
 __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) P.nc * 8u;
-    _Float16 * At = (_Float16 *) (lds + NST * cbb);   /* [2][kPR][kPS] decoded weights */
-    _Float16 * Bt = At + 2 * kPR * kPS;                /* [2][kPT][kPS] tokens */
+    _Float16 * At = (_Float16 *) (lds + NST * cbb);   /* [2][RT][kPS] decoded weights */
+    _Float16 * Bt = At + 2 * RT * kPS;                 /* [2][kPT][kPS] tokens */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r0 = blockIdx.x * kPR, t0 = blockIdx.y * kPT;
+    const int r0 = blockIdx.x * RT, t0 = blockIdx.y * kPT;
     const int nk = P.cols / kPK;
 
     /* codebooks to LDS in batches of unconditional 16-byte loads */
@@ -159,14 +159,19 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
         }
     }
 
-    /* decode role: row dr of the tile, columns 16 h .. 16 h + 15 of a chunk
-     * (4 indices, bits 48 h .. 48 h + 47 of the chunk's 24 stream bytes:
-     * the two dwords from byte 6 h rounded down, shifted by 0 or 16 bits);
-     * x role (token-major): token dr of the tile, the same columns */
-    const int dr = tid >> 2, h = tid & 3;
-    const int drow = min(r0 + dr, P.rows - 1), dtok = min(t0 + dr, P.ntok - 1);
-    const int wd = (6 * h) >> 2;
-    const uint32_t wsh = (uint32_t) ((6 * h) & 3) * 8u;
+    /* decode role: row dr of the tile, IPT indices (4 IPT columns) of a chunk
+     * per thread, TPR threads per row: bits 12 IPT h .. of the chunk's 24
+     * stream bytes, from the dword holding the first of them (and the next
+     * one within the chunk), shifted into place */
+    constexpr int TPR = kPThreads / RT, IPT = 16 / TPR;
+    const int dr = tid / TPR, h = tid % TPR;
+    const int drow = min(r0 + dr, P.rows - 1);
+    const int wo = (3 * IPT * h) >> 1;                 /* byte of the first index */
+    const int wd = wo >> 2, wd1 = min(wd + 1, 5);
+    const uint32_t wsh = (uint32_t) (wo & 3) * 8u;
+    /* x role (token-major): token xt of the tile, columns 16 xh .. 16 xh + 15 */
+    const int xtk = tid >> 2, xh = tid & 3;
+    const int dtok = min(t0 + xtk, P.ntok - 1);
     float g[NST];
     const uint32_t * rs[NST];
     const uint8_t * ps[NST];
@@ -174,9 +179,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
     for (int s = 0; s < NST; s++) {
         g[s] = (float) *(const _Float16 *) (P.st[s] + P.gain_off + 2 * (size_t) drow);
         rs[s] = (const uint32_t *) (P.st[s] + P.stream_off + (size_t) drow * P.mrow) + wd;
-        ps[s] = P.st[s] + P.stream_off + (size_t) P.rows * P.mrow + (size_t) drow * P.prow + (h >> 1);
+        ps[s] = P.st[s] + P.stream_off + (size_t) P.rows * P.mrow + (size_t) drow * P.prow + ((IPT * h) >> 3);
     }
-    const uint8_t * xr = (const uint8_t *) P.x + ((size_t) dtok * P.ldx + 16 * h) * (XF32 ? 4 : 2);
+    const uint8_t * xr = (const uint8_t *) P.x + ((size_t) dtok * P.ldx + 16 * xh) * (XF32 ? 4 : 2);
     /* K-major x role (the reference's xT[cols][ntok]): tokens 4 tq .. 4 tq + 3
      * of the tile, columns 4 cg .. 4 cg + 3 of a chunk; lanes run along the
      * tokens, so each 16-byte load of a wave reads 512 contiguous bytes */
@@ -192,7 +197,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
 #pragma unroll
         for (int s = 0; s < NST; s++) {
             wv[sl][s][0] = rs[s][6 * kc];
-            wv[sl][s][1] = rs[s][6 * kc + 1];
+            wv[sl][s][1] = rs[s][6 * kc + wd1 - wd];
             pb[sl][s] = EXT ? ps[s][2 * kc] : 0u;
         }
         if constexpr (XT) {
@@ -204,9 +209,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
         }
     };
     auto store = [&](int b, int sl) {
-        pf_h8 w8[2];
+        pf_h8 w8[IPT / 2];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < IPT; j++) {
             float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NST; s++) {
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
                 const uint32_t hi = wv[sl][s][1] >> wsh;
                 uint32_t idx = j == 0 ? lo : j == 1 ? lo >> 12 : j == 2 ? __builtin_amdgcn_alignbit(hi, lo, 24) : hi >> 4;
                 idx &= 0xfffu;
-                if (EXT) idx |= ((pb[sl][s] >> (4 * (h & 1) + j)) & 1u) << 12;
+                if (EXT) idx |= ((pb[sl][s] >> ((IPT * h) % 8 + j)) & 1u) << 12;
                 const pf_h4 c = *(const pf_h4 *) (lds + s * cbb + 8 * idx);
 #pragma unroll
                 for (int d = 0; d < 4; d++) acc[d] = __builtin_fmaf((float) c[d], g[s], acc[d]);
@@ -222,9 +227,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
 #pragma unroll
             for (int d = 0; d < 4; d++) w8[j >> 1][4 * (j & 1) + d] = (_Float16) acc[d];
         }
-        _Float16 * ad = At + (b * kPR + dr) * kPS + 16 * h;
-        *(pf_h8 *) ad = w8[0];
-        *(pf_h8 *) (ad + 8) = w8[1];
+        _Float16 * ad = At + (b * RT + dr) * kPS + 4 * IPT * h;
+#pragma unroll
+        for (int k = 0; k < IPT / 2; k++) *(pf_h8 *) (ad + 8 * k) = w8[k];
         if constexpr (XT) {
             /* xv[c] holds tokens 4 tq .. +3 of column 4 cg + c: four
              * columns (8 bytes) per token */
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
             }
             return;
         }
-        _Float16 * bd = Bt + (b * kPT + dr) * kPS + 16 * h;
+        _Float16 * bd = Bt + (b * kPT + xtk) * kPS + 16 * xh;
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             pf_h8 v8;
@@ -258,16 +263,17 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
         }
     };
 
-    /* MFMA role: wave (wm, wn) owns rows 64 wm .. +63 and tokens 32 wn .. +31
-     * of the tile as 2 blocks of 32 x 32 (v_mfma_f32_32x32x16_f16: each
+    /* MFMA role: wave (wm, wn) owns rows RT/2 wm .. + RT/2 - 1 and tokens
+     * 32 wn .. +31 of the tile as NB blocks of 32 x 32 (v_mfma_f32_32x32x16_f16: each
      * operand element serves 32 outputs, half the LDS reads of 16 x 16
      * blocks). A lane's operand is 8 consecutive columns of one row (A) or
      * one token (B); A and B assign columns to lanes the same way, so each
      * block is a plain dot over the chunk's columns. */
+    constexpr int NB = RT / 64;
     const int wm = wave & 1, wn = wave >> 1, m32 = lane & 31, kh = lane >> 5;
-    pf_f16v acc[2];
+    pf_f16v acc[NB];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < NB; i++)
 #pragma unroll
         for (int e = 0; e < 16; e++) acc[i][e] = 0.0f;
 
@@ -290,13 +296,13 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
             fetch(min(kc + PF, nk - 1), u);
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                pf_h8 a[2];
+                pf_h8 a[NB];
 #pragma unroll
-                for (int i = 0; i < 2; i++)
-                    a[i] = *(const pf_h8 *) (At + (b * kPR + 64 * wm + 32 * i + m32) * kPS + 16 * ks + 8 * kh);
+                for (int i = 0; i < NB; i++)
+                    a[i] = *(const pf_h8 *) (At + (b * RT + (RT / 2) * wm + 32 * i + m32) * kPS + 16 * ks + 8 * kh);
                 const pf_h8 bb = *(const pf_h8 *) (Bt + (b * kPT + 32 * wn + m32) * kPS + 16 * ks + 8 * kh);
 #pragma unroll
-                for (int i = 0; i < 2; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bb, acc[i], 0, 0, 0);
+                for (int i = 0; i < NB; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bb, acc[i], 0, 0, 0);
             }
             store(b ^ 1, (u + 1) % PF);
             __syncthreads();
@@ -308,10 +314,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
     const int tok = t0 + 32 * wn + m32;
     if (tok < P.ntok) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < NB; i++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int row = r0 + 64 * wm + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
+                const int row = r0 + (RT / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * kh + (e & 3);
                 if (row < P.rows) {
                     float * yp = P.y + (size_t) tok * P.ldy + row;
                     *yp = (P.accumulate ? *yp : 0.0f) + acc[i][e];
@@ -334,19 +340,43 @@ int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int 
     return lds <= 160 * 1024;
 }
 
-template <int NST, int EXT, int XF32, int PF, int XT = 0>
-static int prefill_mfma_t(const MfmaArgs & P, size_t lds, hipStream_t s) {
+/* LDS of a workgroup: codebooks, two weight tiles of rt rows, two token tiles */
+static size_t prefill_lds(int nst, int nc, int rt) {
+    return (size_t) nst * nc * 8 + (size_t) (2 * rt + 2 * kPT) * kPS * 2;
+}
+
+/* Tile height. A workgroup fills a CU (its LDS leaves no room for a second),
+ * so the time is rounds of workgroups over the CUs times a workgroup's time.
+ * 128-row tiles decode each weight for 128 tokens; 64-row tiles halve the
+ * decode and the MFMAs of a workgroup (not its token conversion), measured at
+ * about 0.65 of a 128-row workgroup's time, and double the workgroups. */
+static int prefill_rt(int rows, int ntok) {
+    const long ttiles = (ntok + kPT - 1) / kPT, G = cu_count();
+    const long r128 = ((rows + 127) / 128 * ttiles + G - 1) / G;
+    const long r64 = ((rows + 63) / 64 * ttiles + G - 1) / G;
+    return r64 * 65 < r128 * 100 ? 64 : 128;
+}
+
+template <int NST, int EXT, int XF32, int PF, int XT, int RT>
+static int prefill_mfma_rt(const MfmaArgs & P, size_t lds, hipStream_t s) {
     static size_t opted = 0;
-    const void * fn = (const void *) prefill_mfma_kernel<NST, EXT, XF32, PF, XT>;
+    const void * fn = (const void *) prefill_mfma_kernel<NST, EXT, XF32, PF, XT, RT>;
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the MFMA prefill kernel", e);
         opted = lds;
     }
-    const dim3 grid((unsigned) ((P.rows + kPR - 1) / kPR), (unsigned) ((P.ntok + kPT - 1) / kPT));
-    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32, PF, XT>, grid, dim3(kPThreads), (uint32_t) lds, s, P);
+    const dim3 grid((unsigned) ((P.rows + RT - 1) / RT), (unsigned) ((P.ntok + kPT - 1) / kPT));
+    launch_kernel(prefill_mfma_kernel<NST, EXT, XF32, PF, XT, RT>, grid, dim3(kPThreads), (uint32_t) lds, s, P);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("MFMA prefill launch", e);
+}
+
+template <int NST, int EXT, int XF32, int PF, int XT = 0>
+static int prefill_mfma_t(const MfmaArgs & P, int nc, hipStream_t s) {
+    if (prefill_rt(P.rows, P.ntok) == 64)
+        return prefill_mfma_rt<NST, EXT, XF32, PF, XT, 64>(P, prefill_lds(NST, nc, 64), s);
+    return prefill_mfma_rt<NST, EXT, XF32, PF, XT, 128>(P, prefill_lds(NST, nc, 128), s);
 }
 
 int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
@@ -368,14 +398,13 @@ int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, 
     P.stream_off = (uint32_t) L.stream_off;
     P.mrow = (uint32_t) L.mrow;
     P.prow = (uint32_t) L.prow;
-    const size_t lds = (size_t) nst * L.nc * 8 + (size_t) 4 * kPR * kPS * 2;
-    const int ext = L.nbit > 12;
+    const int nc = L.nc, ext = L.nbit > 12;
     /* four chunks in flight when the chunk count allows, else two */
     const int pf4 = (L.cols / kPK) % 4 == 0;
-#define PF_PICK(N, E, X) return pf4 ? prefill_mfma_t<N, E, X, 4>(P, lds, s) : prefill_mfma_t<N, E, X, 2>(P, lds, s)
+#define PF_PICK(N, E, X) return pf4 ? prefill_mfma_t<N, E, X, 4>(P, nc, s) : prefill_mfma_t<N, E, X, 2>(P, nc, s)
     if (xt) {   /* one stage, f32 (checked above) */
-        if (ext) return pf4 ? prefill_mfma_t<1, 1, 1, 4, 1>(P, lds, s) : prefill_mfma_t<1, 1, 1, 2, 1>(P, lds, s);
-        return pf4 ? prefill_mfma_t<1, 0, 1, 4, 1>(P, lds, s) : prefill_mfma_t<1, 0, 1, 2, 1>(P, lds, s);
+        if (ext) return pf4 ? prefill_mfma_t<1, 1, 1, 4, 1>(P, nc, s) : prefill_mfma_t<1, 1, 1, 2, 1>(P, nc, s);
+        return pf4 ? prefill_mfma_t<1, 0, 1, 4, 1>(P, nc, s) : prefill_mfma_t<1, 0, 1, 2, 1>(P, nc, s);
     }
     if (nst == 2) {
         if (xf32) { if (ext) PF_PICK(2, 1, 1); PF_PICK(2, 0, 1); }

@@ -240,12 +240,16 @@ def test_prefill_token_major(sm, ref, dev, ntok):
 
 @pytest.mark.parametrize("rows,cols,ntok,nc,f32", [(320, 2560, 200, 4096, False), (130, 1024, 512, 4096, False),
                                                     (64, 512, 77, 8192, False), (96, 640, 130, 4096, True),
-                                                    (256, 10240, 64, 4096, False)])
+                                                    (256, 10240, 64, 4096, False), (10240, 256, 1024, 4096, False),
+                                                    (10200, 256, 1000, 8192, True)])
 def test_prefill_mfma_against_oracle(sm, ref, dev, rows, cols, ntok, nc, f32):
     """The matrix-core prefill: ragged row and token tiles, 13-bit indices,
-    f32 x, and the long 10240-column rows of down_proj. Weights enter the
-    MFMA as f16 (one rounding of the exact decode), so the bar is the 1e-3
-    relative L2 of the GEMM gate, not the GEMV's f32-exact 1e-5."""
+    f32 x, and the long 10240-column rows of down_proj. Small grids run
+    64-row tiles; 10240 rows x 1024 tokens (three rounds of 128-row
+    workgroups over 256 CUs against five of 64-row ones) run 128-row tiles.
+    Weights enter the MFMA as f16 (one rounding of the exact decode), so the
+    bar is the 1e-3 relative L2 of the GEMM gate, not the GEMV's f32-exact
+    1e-5."""
     import torch
     data = sm.synth_container(rows * 3 + ntok, rows, cols, 4, nc, 2, 1)
     W = ref.decode(data).astype(np.float64)
@@ -284,6 +288,7 @@ def test_prefill_reference_layout(sm, ref, dev):
 
 @pytest.mark.parametrize("rows,cols,ntok,nc,variant,tile", [(320, 2560, 200, 4096, 2, (128, 64)),
                                                           (130, 1024, 512, 8192, 1, (64, 64)),
+                                                          (10240, 256, 1024, 8192, 2, (128, 64)),
                                                           (64, 512, 36, 4096, 0, None),
                                                           (48, 640, 37, 4096, 2, (256, 64)),
                                                           (96, 256, 12, 4096, 3, None)])
