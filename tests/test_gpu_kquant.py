@@ -77,6 +77,26 @@ def test_kquant_matches_runtime_dot(sm, ref, dev):
     assert rel_l2(y.cpu().numpy(), yr) <= TIGHT
 
 
+@pytest.mark.parametrize("kind", ["q8_0", "q6_k"])
+def test_kquant_columns_equal_single_launches(sm, dev, kind):
+    """A speculative verify's head columns must be exactly the logits a
+    one-column launch gives: the reference found that any other arithmetic
+    for the 8-row verify head changes accepted tokens
+    (Spark-X2.6-4B-Base-handoff.md:299-302). Bit-exact, per column."""
+    import torch
+    rows, cols, ncol = 1000, 2560, 8
+    blocks = torch.from_numpy(_blocks(sm, kind, 31, rows, cols)).to(dev)
+    xb = sm.synth_bf16(32, ncol * cols).reshape(ncol, cols)
+    xt = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+    y8 = torch.full((ncol, rows), float("nan"), device=dev)
+    sm.kquant_gemv(kind, blocks, rows, cols, xt, y8, ncols=ncol)
+    for n in range(ncol):
+        y1 = torch.full((1, rows), float("nan"), device=dev)
+        sm.kquant_gemv(kind, blocks, rows, cols, xt[n:n + 1].contiguous(), y1)
+        torch.cuda.synchronize()
+        assert np.array_equal(y8[n].cpu().numpy().view(np.uint32), y1[0].cpu().numpy().view(np.uint32)), n
+
+
 def test_kquant_errors(sm, dev):
     import torch
     L = sm.lib()
