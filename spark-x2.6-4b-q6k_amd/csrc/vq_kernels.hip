@@ -83,6 +83,8 @@ struct FastArgs {
 };
 
 constexpr int kFastMats = 4;
+/* several-column launches read x from global memory when a shape allows */
+constexpr int kFastXg = 1;
 
 constexpr int kRedStride = 16 * 17;   /* floats per wave of the LDS reduction area */
 
@@ -102,17 +104,20 @@ __device__ __forceinline__ uint32_t cw_addr(uint32_t w0, uint32_t w1, uint32_t w
     }
 }
 
-template <int NST, int EXT>
+template <int NST, int EXT, int XG = 0>
 struct Words {
     uint32_t w[NST][3];
     uint32_t pb[NST];
+    uint32_t xg[XG ? 16 : 1];   /* XG: the lane's 32 bf16 activations of the step */
 };
 
 /* Index words of one macro step: 12 bytes (8 indices) per lane quarter of
- * each stage's row stream, and for 13-bit indices the plane byte. */
-template <int NST, int EXT>
-__device__ __forceinline__ void load_words(Words<NST, EXT> & W, const uint8_t * const * rp,
-                                           const uint8_t * const * pp, int ms) {
+ * each stage's row stream, and for 13-bit indices the plane byte. With XG
+ * also the lane's 64 bytes of bf16 x for the step (128 columns per step,
+ * 32 per lane quarter), read straight from global memory. */
+template <int NST, int EXT, int XG = 0>
+__device__ __forceinline__ void load_words(Words<NST, EXT, XG> & W, const uint8_t * const * rp,
+                                           const uint8_t * const * pp, const uint8_t * xp, int ms) {
 #pragma unroll
     for (int s = 0; s < NST; s++) {
         const uint32_t * p = (const uint32_t *) (rp[s] + 48 * ms);
@@ -121,6 +126,15 @@ __device__ __forceinline__ void load_words(Words<NST, EXT> & W, const uint8_t * 
         W.w[s][2] = p[2];
         if (EXT) W.pb[s] = pp[s][4 * ms];
     }
+    if constexpr (XG != 0) {
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        const u4v * q = (const u4v *) (xp + 256 * ms);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const u4v v = q[k];
+            W.xg[4 * k] = v.x; W.xg[4 * k + 1] = v.y; W.xg[4 * k + 2] = v.z; W.xg[4 * k + 3] = v.w;
+        }
+    }
 }
 
 /* One macro step: 8 MFMA steps per stage. k-slot (quarter q, step t) is
@@ -128,32 +142,41 @@ __device__ __forceinline__ void load_words(Words<NST, EXT> & W, const uint8_t * 
  * codeword) and B (the activations) use the same assignment. Every LDS read
  * of the step (8 B reads, 8 * NST codeword gathers) is issued before the
  * first MFMA, so the gathers' latency overlaps. */
-template <int T, int NST, int EXT>
-__device__ __forceinline__ uint32_t step_addr(const Words<NST, EXT> & W, int s, uint32_t cbb) {
+template <int T, int NST, int EXT, int XG>
+__device__ __forceinline__ uint32_t step_addr(const Words<NST, EXT, XG> & W, int s, uint32_t cbb) {
     uint32_t a = cw_addr<T>(W.w[s][0], W.w[s][1], W.w[s][2]);
     if (EXT) a |= (W.pb[s] << (15 - T)) & 0x8000u;
     return (uint32_t) s * cbb + a;
 }
 
-template <int NST, int XF32, int EXT>
-__device__ __forceinline__ void mstep(const Words<NST, EXT> & W, const uint8_t * lds, uint32_t cbb,
+template <int NST, int XF32, int EXT, int XG = 0>
+__device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8_t * lds, uint32_t cbb,
                                       const uint8_t * xb, const uint8_t * xbl, f4 * acc) {
     h4 cw[8][NST], b[8], bl[8];
 #pragma unroll
     for (int s = 0; s < NST; s++) {
-        cw[0][s] = *(const h4 *) (lds + step_addr<0, NST, EXT>(W, s, cbb));
-        cw[1][s] = *(const h4 *) (lds + step_addr<1, NST, EXT>(W, s, cbb));
-        cw[2][s] = *(const h4 *) (lds + step_addr<2, NST, EXT>(W, s, cbb));
-        cw[3][s] = *(const h4 *) (lds + step_addr<3, NST, EXT>(W, s, cbb));
-        cw[4][s] = *(const h4 *) (lds + step_addr<4, NST, EXT>(W, s, cbb));
-        cw[5][s] = *(const h4 *) (lds + step_addr<5, NST, EXT>(W, s, cbb));
-        cw[6][s] = *(const h4 *) (lds + step_addr<6, NST, EXT>(W, s, cbb));
-        cw[7][s] = *(const h4 *) (lds + step_addr<7, NST, EXT>(W, s, cbb));
+        cw[0][s] = *(const h4 *) (lds + step_addr<0, NST, EXT, XG>(W, s, cbb));
+        cw[1][s] = *(const h4 *) (lds + step_addr<1, NST, EXT, XG>(W, s, cbb));
+        cw[2][s] = *(const h4 *) (lds + step_addr<2, NST, EXT, XG>(W, s, cbb));
+        cw[3][s] = *(const h4 *) (lds + step_addr<3, NST, EXT, XG>(W, s, cbb));
+        cw[4][s] = *(const h4 *) (lds + step_addr<4, NST, EXT, XG>(W, s, cbb));
+        cw[5][s] = *(const h4 *) (lds + step_addr<5, NST, EXT, XG>(W, s, cbb));
+        cw[6][s] = *(const h4 *) (lds + step_addr<6, NST, EXT, XG>(W, s, cbb));
+        cw[7][s] = *(const h4 *) (lds + step_addr<7, NST, EXT, XG>(W, s, cbb));
     }
 #pragma unroll
     for (int t = 0; t < 8; t++) {
-        b[t] = *(const h4 *) (xb + 8 * t);
-        if (XF32) bl[t] = *(const h4 *) (xbl + 8 * t);
+        if constexpr (XG != 0) {
+            /* bf16 pairs to f16 (exact for the activations' range) */
+            const uint32_t u0 = W.xg[2 * t], u1 = W.xg[2 * t + 1];
+            b[t][0] = (_Float16) __uint_as_float(u0 << 16);
+            b[t][1] = (_Float16) __uint_as_float(u0 & 0xffff0000u);
+            b[t][2] = (_Float16) __uint_as_float(u1 << 16);
+            b[t][3] = (_Float16) __uint_as_float(u1 & 0xffff0000u);
+        } else {
+            b[t] = *(const h4 *) (xb + 8 * t);
+            if (XF32) bl[t] = *(const h4 *) (xbl + 8 * t);
+        }
     }
 #pragma unroll
     for (int t = 0; t < 8; t++) {
@@ -166,12 +189,15 @@ __device__ __forceinline__ void mstep(const Words<NST, EXT> & W, const uint8_t *
 }
 
 template <int NST, int XF32, int EXT, int MSC, int MC>
-__global__ __launch_bounds__(MC ? 1024 : 640) void vq_mfma_kernel(const FastArgs A) {
+__global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const FastArgs A) {
     /* MSC > 0: a unit is exactly MSC macro steps, known at compile time, so
      * the whole unit runs as straight-line code and each step waits only for
      * its own index words (a loop would make the compiler wait for all of a
      * wave's loads at its head). MSC == 0: any unit length, a ring of D steps.
-     * MC: the straight-line kernel for several activation columns. */
+     * MC: the kernel for several activation columns, with x staged in LDS
+     * (1) or, XG (2), read from global memory (the L2) with each step's index
+     * words, so no x is staged and any column count fits LDS. */
+    constexpr int XG = MC == 2 ? 1 : 0;
     constexpr int D = MSC > 0 ? MSC : 8;
     /* straight-line units keep at most kLook macro steps of index words in
      * flight per wave: with every step requested up front the memory system
@@ -229,8 +255,13 @@ __global__ __launch_bounds__(MC ? 1024 : 640) void vq_mfma_kernel(const FastArgs
     /* index words of D macro steps; every load is issued unconditionally
      * (steps past the unit re-read its last step), so the number of loads in
      * flight is static and each use waits only for its own words */
-    Words<NST, EXT> w[D];
-    auto ld = [&](Words<NST, EXT> & W, int ms) { load_words<NST, EXT>(W, rp, pp, ms < MS ? ms : MS - 1); };
+    Words<NST, EXT, XG> w[D];
+    /* XG: the lane's x run for its B column (part hp, activation column cn;
+     * lanes past the parts read part 0 of column 0 and feed no output) */
+    const uint8_t * xgp = (const uint8_t *) A.x + ((size_t) (bval ? cn : 0) * A.ldx + 128 * msb + 32 * q) * 2;
+    auto ld = [&](Words<NST, EXT, XG> & W, int ms) {
+        load_words<NST, EXT, XG>(W, rp, pp, xgp, ms < MS ? ms : MS - 1);
+    };
     auto ld_all = [&]() {
 #pragma unroll
         for (int u = 0; u < D; u++) ld(w[u], u);
@@ -332,7 +363,7 @@ __global__ __launch_bounds__(MC ? 1024 : 640) void vq_mfma_kernel(const FastArgs
                 for (int k = 0; k < KS; k++)
                     ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
         }
-        const int xq = A.cols >> 3, nx = ncol * xq;
+        const int xq = A.cols >> 3, nx = XG ? 0 : ncol * xq;
         for (int base = 0; base < nx; base += KXM * bd) {
             u4v xv[KXM];
             int ci[KXM];
@@ -462,7 +493,7 @@ __global__ __launch_bounds__(MC ? 1024 : 640) void vq_mfma_kernel(const FastArgs
             if (MSC > 0) {
 #pragma unroll
                 for (int u = 0; u < D; u++) {
-                    mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc);
+                    mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc);
                     if (u + kLook < D) ld(w[u + kLook], u + kLook);
                 }
             } else {
@@ -470,7 +501,7 @@ __global__ __launch_bounds__(MC ? 1024 : 640) void vq_mfma_kernel(const FastArgs
 #pragma unroll
                     for (int u = 0; u < D; u++) {
                         if (ms0 + u < MS)
-                            mstep<NST, XF32, EXT>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc);
+                            mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc);
                         if (MS > D) ld(w[u], ms0 + u + D);
                     }
                 }
@@ -746,18 +777,59 @@ static int launch_fast_t(const FastArgs & A, int grid, int threads, size_t lds, 
 struct FastShape {
     int S, C, T, W, nwg;
     size_t lds;
+    int xg;   /* several columns with x read from global memory (no x in LDS) */
 };
 
 /* LDS bytes per activation column: 264 bytes per 128 columns (256 of f16
  * values and 8 of pad) and 8 more between columns. */
 static int fast_xstride(int cols, int S) { (void) S; return 264 * (cols / 128) + 8; }
 
-static size_t fast_lds(const VqCall & c, int nst, int S, int W) {
-    return (size_t) nst * c.nc * 8 + (size_t) (c.xf32 ? 2 : 1) * c.ncol * fast_xstride(c.cols, S) +
+static size_t fast_lds(const VqCall & c, int nst, int S, int W, int xg = 0) {
+    return (size_t) nst * c.nc * 8 + (xg ? 0 : (size_t) (c.xf32 ? 2 : 1) * c.ncol * fast_xstride(c.cols, S)) +
            (size_t) W * kRedStride * 4;
 }
 
+/* Several bf16 columns with x read from global memory: each lane loads its
+ * 32 activations of a step (64 bytes, 16-byte aligned rows) with the step's
+ * index words, so nothing but codebooks sits in LDS and no column count
+ * splits K. Taken when x is at least 48 KB (N = 8 at 4096 and 10240
+ * columns: staging it cost more than its loads, measured); smaller x is
+ * staged in LDS. Straight-line units only (a ring would hold 8 steps of x
+ * per lane), at most 10 waves (the registers of 4 steps in flight), and
+ * enough threads to stage the codebooks in 5 chunks each. Shape: fewest
+ * rounds of workgroups over the CUs, then the shortest unit. */
+static int fast_shape_xg(const VqCall & c, int nst, FastShape & sh) {
+    if (c.ncol < 2 || c.xf32 || c.nc % 2 || ((uintptr_t) c.x & 15u) || c.ldx % 8) return -1;
+    if ((long) c.ncol * c.cols < 24576) return -1;
+    const int M = c.cols / 128, G = cu_count(), n16 = c.nc * 8 / 16;
+    long best = -1;
+    for (int s = 1; s <= 16; s *= 2) {
+        if (s * c.ncol > 16 || M % s) continue;
+        const int MP = M / s;
+        for (int cc = 1; cc <= 10; cc++) {
+            if (MP % cc) continue;
+            const int ms = MP / cc;
+            if (ms != 2 && ms != 4 && ms != 5 && ms != 8 && (ms != 10 || c.nc > 4096)) continue;
+            for (int tt = 1; tt * cc <= 10; tt++) {
+                if (5 * 64 * tt * cc < n16) continue;
+                long nwg = 0;
+                for (int m = 0; m < c.nmat; m++) nwg += ((c.mats[m].rows * (long) s + 15) / 16 + tt - 1) / tt;
+                const size_t lds = fast_lds(c, nst, s, tt * cc, 1);
+                if (lds > (size_t) kLdsMax) continue;
+                const long cost = (nwg + G - 1) / G * (8 + ms) * 64 + tt * cc;
+                if (best < 0 || cost < best) {
+                    best = cost;
+                    sh.S = s; sh.C = cc; sh.T = tt; sh.W = tt * cc; sh.nwg = (int) nwg; sh.lds = lds; sh.xg = 1;
+                }
+            }
+        }
+    }
+    return best < 0 ? -1 : 0;
+}
+
 static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
+    if (kFastXg && fast_shape_xg(c, nst, sh) == 0) return 0;
+    sh.xg = 0;
     const int M = c.cols / 4 / 32;
     const int G = cu_count();
     const int want = G * 8;
@@ -838,6 +910,21 @@ static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
 template <int NST, int XF32, int EXT>
 static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, size_t lds, hipStream_t s) {
     if constexpr (!XF32) {
+        if (mc == 2) {
+            /* x from global memory: the shape search kept to these unit lengths */
+            switch (MS) {
+                case 2: return launch_fast_t<NST, 0, EXT, 2, 2>(A, grid, threads, lds, s);
+                case 4: return launch_fast_t<NST, 0, EXT, 4, 2>(A, grid, threads, lds, s);
+                case 5: return launch_fast_t<NST, 0, EXT, 5, 2>(A, grid, threads, lds, s);
+                case 8: return launch_fast_t<NST, 0, EXT, 8, 2>(A, grid, threads, lds, s);
+                case 10:
+                    if constexpr (!EXT) return launch_fast_t<NST, 0, EXT, 10, 2>(A, grid, threads, lds, s);
+                    break;
+                default: break;
+            }
+            set_error("no x-from-global kernel for units of %d macro steps", MS);
+            return -1;
+        }
         if (mc) {
             /* several columns: the unit lengths of the trunk's verify shapes */
             switch (MS) {
@@ -896,7 +983,7 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     A.C = sh.C; A.T = sh.T;
     A.M = mk;
     A.kofs = k0;
-    A.xstride = fast_xstride(part.cols, sh.S);
+    A.xstride = sh.xg ? 0 : fast_xstride(part.cols, sh.S);
     int wg = 0;
     for (int m = 0; m < c.nmat; m++) {
         for (int s = 0; s < nst; s++) A.mat[m].st[s] = (const uint8_t *) c.mats[m].stages[st0 + s];
@@ -918,11 +1005,12 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     const int one_col = sh.C == 1 && !((uintptr_t) A.x & 15u) && n16 <= 5 * threads && part.cols <= 16 * threads;
     const int multi_col = c.ncol > 1 && !((uintptr_t) A.x & 15u) && c.ldx % 8 == 0 && n16 <= 5 * threads;
     const int straight = !c.xf32 && c.nc % 2 == 0 && (c.ncol > 1 ? multi_col : one_col);
-    const int MS = straight ? A.M / sh.S / sh.C : 0;
-    /* the multi-column kernels (MS without its own instantiation runs their
-     * ring form); any other several-column call runs the generic kernel,
-     * which the shape search kept within 10 waves */
-    const int mc = c.ncol > 1 && straight;
+    const int MS = sh.xg ? A.M / sh.S / sh.C : straight ? A.M / sh.S / sh.C : 0;
+    /* the multi-column kernels: x from global memory (2) or staged in LDS (1;
+     * MS without its own instantiation runs their ring form); any other
+     * several-column call runs the generic kernel, which the shape search
+     * kept within 10 waves */
+    const int mc = sh.xg ? 2 : c.ncol > 1 && straight;
     if (nst == 2) {
         if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, mc, wg, threads, sh.lds, c.stream)
                                : launch_ms<2, 1, 0>(A, MS, mc, wg, threads, sh.lds, c.stream);

@@ -97,14 +97,17 @@ def test_batched_columns_equal_single_columns(sm, dev):
         assert rel_l2(a, b) <= 1e-6, n
 
 
-@pytest.mark.parametrize("rows,cols,ncol", [(96, 10240, 8), (40, 10240, 16), (33, 2560, 8), (64, 4096, 8)])
-def test_verify_columns_against_oracle(sm, ref, dev, rows, cols, ncol):
-    """Speculative-verify shapes: N columns decoded once. At 10240 columns
-    the N activation columns do not fit LDS beside the codebooks, so the call
-    runs as consecutive K ranges accumulating into y; every column must still
-    match the oracle and the N=1 result."""
+@pytest.mark.parametrize("rows,cols,ncol,nc", [(96, 10240, 8, 4096), (40, 10240, 16, 4096), (33, 2560, 8, 4096),
+                                               (64, 4096, 8, 4096), (48, 4096, 8, 8192), (24, 8192, 3, 4096)])
+def test_verify_columns_against_oracle(sm, ref, dev, rows, cols, ncol, nc):
+    """Speculative-verify shapes: N columns decoded once. When x holds 48 KB
+    or more (N = 8 at 4096 and 10240 columns, 3 columns of 8192) each lane
+    reads its activations from global memory with its index words; smaller x
+    (N = 8 at 2560 columns) is staged in LDS. 13-bit indices and an odd
+    column count included; every column must match the oracle and the N=1
+    result."""
     import torch
-    data = sm.synth_container(rows + ncol, rows, cols)
+    data = sm.synth_container(rows + ncol, rows, cols, 4, nc, 2, 1)
     W = ref.decode(data).astype(np.float64)
     dc = sm.DeviceContainer(data)
     xt, xf = _x(sm, cols + ncol, ncol, cols, False)
@@ -121,6 +124,28 @@ def test_verify_columns_against_oracle(sm, ref, dev, rows, cols, ncol):
         dc.gemv(xt[n:n + 1], y1, ncols=1)
         torch.cuda.synchronize()
         assert rel_l2(got[n], y1[0].cpu().numpy()) <= 1e-6, n
+
+
+def test_verify_multi_matrix_x_from_global(sm, ref, dev):
+    """Several matrices sharing x in one launch with 8 columns of 4096 (x read
+    from global memory), ragged row counts, then accumulating into y."""
+    import torch
+    cols, ncol = 4096, 8
+    shapes = [160, 40, 40, 16]
+    datas = [sm.synth_container(300 + i, r, cols) for i, r in enumerate(shapes)]
+    mats = [sm.DeviceContainer(d) for d in datas]
+    Ws = [ref.decode(d).astype(np.float64) for d in datas]
+    xt, xf = _x(sm, 9, ncol, cols, False)
+    ys = [torch.full((ncol, max(shapes)), float("nan"), device=dev) for _ in shapes]
+    sm.gemv_multi(mats, xt, ys, ncols=ncol)
+    torch.cuda.synchronize()
+    got = [y[:, :r].cpu().numpy().copy() for y, r in zip(ys, shapes)]
+    for W, g in zip(Ws, got):
+        assert rel_l2(g, xf.astype(np.float64) @ W.T) <= TIGHT
+    sm.gemv_multi(mats, xt, ys, ncols=ncol, accumulate=True)
+    torch.cuda.synchronize()
+    for W, y, r in zip(Ws, ys, shapes):
+        assert rel_l2(y[:, :r].cpu().numpy(), 2 * (xf.astype(np.float64) @ W.T)) <= TIGHT
 
 
 def test_reference_abi_per_stage(sm, ref, dev):
