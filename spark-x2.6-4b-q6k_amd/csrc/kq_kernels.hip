@@ -572,6 +572,7 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
     do {                                        \
         if (ncol == 1) KQ_LAUNCH(K, 1, XF);     \
         else if (ncol <= 4) KQ_LAUNCH(K, 4, XF); \
+        else if (ncol <= 8) KQ_LAUNCH(K, 8, XF); \
         else KQ_LAUNCH(K, 16, XF);              \
     } while (0)
     if (kind == 6 && cols <= 16384 && (cols / 256) % 2 == 0 && !((uintptr_t) blocks & 3) && !(xf32 && ncol > 4)) {

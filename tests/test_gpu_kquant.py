@@ -97,6 +97,26 @@ def test_kquant_columns_equal_single_launches(sm, dev, kind):
         assert np.array_equal(y8[n].cpu().numpy().view(np.uint32), y1[0].cpu().numpy().view(np.uint32)), n
 
 
+def test_q8_0_sixteen_columns(sm, ref, dev):
+    """16 columns of 4096 (147 KB of x in LDS), against the oracle and
+    bit-equal to a one-column launch."""
+    import torch
+    rows, cols, ncol = 64, 4096, 16
+    blocks = sm.synth_q8_0(41, rows, cols)
+    W = ref.q8_0_dequant(blocks, rows, cols).astype(np.float64)
+    db = torch.from_numpy(blocks).to(dev)
+    xb = sm.synth_bf16(42, ncol * cols).reshape(ncol, cols)
+    xf = sm.bf16_to_f32(xb).reshape(ncol, cols)
+    xt = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+    y = torch.full((ncol, rows), float("nan"), device=dev)
+    sm.kquant_gemv("q8_0", db, rows, cols, xt, y, ncols=ncol)
+    y1 = torch.full((1, rows), float("nan"), device=dev)
+    sm.kquant_gemv("q8_0", db, rows, cols, xt[5:6].contiguous(), y1)
+    torch.cuda.synchronize()
+    assert rel_l2(y.cpu().numpy(), xf.astype(np.float64) @ W.T) <= TIGHT
+    assert np.array_equal(y[5].cpu().numpy().view(np.uint32), y1[0].cpu().numpy().view(np.uint32))
+
+
 def test_kquant_errors(sm, dev):
     import torch
     L = sm.lib()
