@@ -89,18 +89,19 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t w, _Float16 bias, kq_h2 & l
  * Q6_K kernels' lanes read 128-column units, and the pad puts neighbouring
  * units on different LDS banks. */
 template <int XF32, int PADU = 0>
-__device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
+__device__ __forceinline__ void kq_stage_x_by(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst,
+                                              int tid, int nthr) {
     typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
     const bool vec = !((uintptr_t) x & 3) && (ncol == 1 || !(ldx & 1));
     if (vec) {
         constexpr int KB = 8, NV = XF32 ? 2 : 1;
         const int ng = cols >> 3, total = ncol * ng;
-        for (int base = 0; base < total; base += KB * (int) blockDim.x) {
+        for (int base = 0; base < total; base += KB * nthr) {
             u4a v[KB][NV];
             int gi[KB];
 #pragma unroll
             for (int k = 0; k < KB; k++) {
-                gi[k] = min(base + k * (int) blockDim.x + (int) threadIdx.x, total - 1);
+                gi[k] = min(base + k * nthr + tid, total - 1);
                 const int n = gi[k] / ng, c8 = gi[k] - n * ng;
                 const uint8_t * src = (const uint8_t *) x + ((size_t) n * ldx + 8 * c8) * (XF32 ? 4 : 2);
 #pragma unroll
@@ -135,7 +136,7 @@ __device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ld
         }
         return;
     }
-    for (int e = threadIdx.x; e < ncol * cols; e += blockDim.x) {
+    for (int e = tid; e < ncol * cols; e += nthr) {
         const int n = e / cols, k = e - n * cols;
         const float v = kq_x(x, XF32, (size_t) n * ldx + k);
         const _Float16 hi = (_Float16) v;
@@ -143,6 +144,12 @@ __device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ld
         *(_Float16 *) (lds + n * xst + off) = hi;
         if (XF32) *(_Float16 *) (lds + (ncol + n) * xst + off) = (_Float16) (v - (float) hi);
     }
+}
+
+/* The whole workgroup stages x. */
+template <int XF32, int PADU = 0>
+__device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
+    kq_stage_x_by<XF32, PADU>(lds, x, ldx, ncol, cols, xst, (int) threadIdx.x, (int) blockDim.x);
 }
 
 /* ---------------------------------- Q8_0 --------------------------------- */
@@ -403,12 +410,13 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
     }
 }
 
-/* 4-byte reads of LDS at a 2-byte aligned address, shifted into N words */
+/* N dwords of LDS bytes from byte `off` of the shared array (2-byte
+ * aligned): the covering aligned dwords, funnel-shifted. Offsets from the
+ * array itself keep the reads in the LDS address space. */
 template <int N>
-__device__ __forceinline__ void lds_stream(const uint8_t * addr, uint32_t * out) {
-    const uintptr_t a = (uintptr_t) addr;
-    const uint32_t * p = (const uint32_t *) (a & ~(uintptr_t) 3);
-    const uint32_t sh = (uint32_t) (a & 3) * 8u;
+__device__ __forceinline__ void lds_stream(const uint8_t * lds_base, uint32_t off, uint32_t * out) {
+    const uint32_t * p = (const uint32_t *) (lds_base + (off & ~3u));
+    const uint32_t sh = (off & 3u) * 8u;
     uint32_t w[N + 1];
 #pragma unroll
     for (int k = 0; k <= N; k++) w[k] = p[k];
@@ -416,88 +424,94 @@ __device__ __forceinline__ void lds_stream(const uint8_t * addr, uint32_t * out)
     for (int k = 0; k < N; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
 }
 
-/* Q6_K, staged form: the workgroup's rows are one contiguous run of blocks,
- * copied into LDS by 1 KB direct-to-LDS loads (a whole cache line per lane
- * group, each line fetched once), then each row is worked by 32 lanes from
- * LDS with the arithmetic of q6k_gemv_kernel. One row per wave (64 lanes,
- * up to 128 half superblocks = 16384 columns); rows a multiple of 4 bytes
- * long (even superblock count) and 4-byte aligned blocks (the host checks
- * both). */
+/* Q6_K, staged form. Compute waves each own one row: a wave copies its row
+ * into its own LDS region by 1 KB direct-to-LDS loads and then works it,
+ * waiting only for its own copy, so rows that land early are decoded while
+ * the others still stream in. Further waves stage x, one batch of loads per
+ * lane (a wave that had issued direct-to-LDS loads would wait for them before
+ * its own LDS stores). The
+ * row is split into units of 32 weights, an 8-wide l range of one half
+ * superblock in ggml's layout (l0 .. l0 + 7 of y[l], y[l + 32], y[l + 64],
+ * y[l + 96]): 8 units per superblock, five per lane at 10240 columns. Rows
+ * are a multiple of 4 bytes and at least 1 KB long, blocks 4-byte aligned
+ * (the host checks). Every column gets the same arithmetic whatever the
+ * column count. */
 template <int NC, int XF32>
 __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * blocks, int rows, int cols,
                                                                 const void * x, int ldx, int ncol, float * y, int ldy,
-                                                                int accumulate) {
-    constexpr int NU = 2;
+                                                                int accumulate, int rpw) {
     typedef __attribute__((address_space(3))) void lds_void;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72 + (cols / 128) * 8;
-    const size_t rowbytes = (size_t) bpr * 210;
-    const int nw = blockDim.x >> 6, rpw = nw;                  /* one row per wave */
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int bpr = cols / 256, units = 8 * bpr, xst = (cols / 32) * 72 + (cols / 128) * 8;
+    const uint32_t rowbytes = (uint32_t) bpr * 210;
+    const int xw = (blockDim.x >> 6) - rpw;                    /* waves rpw .. stage x */
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = blockIdx.x * rpw, nrow = min(rpw, rows - row0);
-    const uint32_t region = (uint32_t) (nrow * rowbytes);        /* >= 1 KB, checked by the host */
-    const uint32_t xoff = (uint32_t) ((rpw * rowbytes + 15) & ~(size_t) 15);
-    const uint8_t * src = blocks + (size_t) row0 * rowbytes;
-    const int wv = __builtin_amdgcn_readfirstlane(wave);
-    const int nblk = (int) ((region + 1023) >> 10);
-    for (int b = wv; b < nblk; b += nw) {
-        const uint32_t o = min((uint32_t) b * 1024u, region - 1024u);   /* the last block overlaps its neighbour */
-        __builtin_amdgcn_global_load_lds((const void *) (src + o + 16 * lane), (lds_void *) (lds + o), 16, 0, 0);
+    const uint32_t xoff = (uint32_t) ((rpw * rowbytes + 15) & ~15u);
+    const uint32_t reg = (uint32_t) wv * rowbytes;            /* this wave's row, a byte offset in LDS */
+    if (wv >= rpw) {
+        /* x: the x waves' loads and LDS stores, complete before the barrier */
+        kq_stage_x_by<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst, threadIdx.x - 64 * rpw, 64 * xw);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    } else if (wv < nrow) {
+        const uint8_t * src = blocks + (size_t) (row0 + wv) * rowbytes;
+        const int nchunk = (int) ((rowbytes + 1023) >> 10);
+        for (int b = 0; b < nchunk; b++) {
+            const uint32_t o = min((uint32_t) b * 1024u, rowbytes - 1024u);   /* the last chunk overlaps its neighbour */
+            __builtin_amdgcn_global_load_lds((const void *) (src + o + 16 * lane), (lds_void *) (lds + reg + o), 16, 0, 0);
+        }
     }
-    kq_stage_x<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    const int j = lane, rl = wave, row = row0 + rl;
+    /* x is in LDS after this barrier. An execution barrier only (the asm
+     * keeps the compiler from moving LDS reads above it): no wave waits for
+     * its row copy here. */
+    asm volatile("s_barrier" ::: "memory");
+    if (wv >= nrow) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* this wave's row */
     float acc[NC];
 #pragma unroll
     for (int n = 0; n < NC; n++) acc[n] = 0.0f;
-    if (rl < nrow) {
+    for (int u = lane; u < units; u += 64) {
+        const int sb = u >> 3, h = (u >> 2) & 1, l0 = 8 * (u & 3);
+        const uint32_t blk = reg + (uint32_t) sb * 210u;
+        uint32_t qa[2], qb[2], qc[2], scw[2], dw[1];
+        lds_stream<2>(lds, blk + 64 * h + l0, qa);
+        lds_stream<2>(lds, blk + 64 * h + 32 + l0, qb);
+        lds_stream<2>(lds, blk + 128 + 32 * h + l0, qc);
+        lds_stream<2>(lds, blk + 192 + 8 * h, scw);
+        lds_stream<1>(lds, blk + 208, dw);
+        const float d = kq_f16((uint16_t) dw[0]);
+        const int e0 = 256 * sb + 128 * h + l0;
 #pragma unroll
-        for (int kk = 0; kk < NU; kk++) {
-            const int u = j + 64 * kk;
-            if (u >= units) continue;
-            const int sb = u >> 1, h = u & 1;
-            const uint8_t * blk = lds + rl * rowbytes + (size_t) sb * 210;
-            uint32_t ql[16], qh[8], scw[2], dw[1];
-            lds_stream<16>(blk + 64 * h, ql);
-            lds_stream<8>(blk + 128 + 32 * h, qh);
-            lds_stream<2>(blk + 192 + 8 * h, scw);
-            lds_stream<1>(blk + 208, dw);
-            const float d = kq_f16((uint16_t) dw[0]);
-            const int chunk0 = (sb * 256 + 128 * h) >> 5;
+        for (int g = 0; g < 4; g++) {
+            const int sci = (l0 >> 4) + 2 * g;
+            const float dsc = d * (float) (int) (int8_t) (scw[sci >> 2] >> (8 * (sci & 3)));
+            kq_h2 qv[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
+            for (int w = 0; w < 2; w++) {
+                const uint32_t lo = ((g & 1 ? qb[w] : qa[w]) >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
+                const uint32_t hi = ((qc[w] >> (2 * g)) & 0x03030303u) << 4;
+                bytes_to_h2(lo | hi, (_Float16) 1056.0f, qv[2 * w], qv[2 * w + 1]);
+            }
+            const int e = e0 + 32 * g;
+            const int xo = (e >> 5) * 72 + (e >> 7) * 8 + 2 * (e & 31);
 #pragma unroll
-                for (int p = 0; p < 2; p++) {
-                    const int sci = p + 2 * k;
-                    const float dsc = d * (float) (int) (int8_t) (scw[sci >> 2] >> (8 * (sci & 3)));
-                    kq_h2 qv[8];
+            for (int n = 0; n < NC; n++) {
+                if (n < ncol) {
+                    const uint8_t * xp = lds + xoff + n * xst + xo;
+                    float sacc = 0.0f;
 #pragma unroll
-                    for (int w = 0; w < 4; w++) {
-                        const int l = 16 * p + 4 * w;
-                        const uint32_t lo = (ql[(l + 32 * (k & 1)) >> 2] >> (4 * (k >> 1))) & 0x0F0F0F0Fu;
-                        const uint32_t hi = ((qh[l >> 2] >> (2 * k)) & 0x03030303u) << 4;
-                        bytes_to_h2(lo | hi, (_Float16) 1056.0f, qv[2 * w], qv[2 * w + 1]);
-                    }
-#pragma unroll
-                    for (int n = 0; n < NC; n++) {
-                        if (n < ncol) {
-                            const uint8_t * xp = lds + xoff + n * xst + (chunk0 + k) * 72 + (chunk0 >> 2) * 8 + 32 * p;
-                            float sacc = 0.0f;
-#pragma unroll
-                            for (int w = 0; w < 4; w++) {
-                                const kq_h4 xv = *(const kq_h4 *) (xp + 8 * w);
-                                sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xv[0], xv[1]}, sacc, false);
-                                sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xv[2], xv[3]}, sacc, false);
-                                if (XF32) {
-                                    const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * w);
-                                    sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xl[0], xl[1]}, sacc, false);
-                                    sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xl[2], xl[3]}, sacc, false);
-                                }
-                            }
-                            acc[n] += dsc * sacc;
+                    for (int w = 0; w < 2; w++) {
+                        const kq_h4 xv = *(const kq_h4 *) (xp + 8 * w);
+                        sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xv[0], xv[1]}, sacc, false);
+                        sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xv[2], xv[3]}, sacc, false);
+                        if (XF32) {
+                            const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * w);
+                            sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xl[0], xl[1]}, sacc, false);
+                            sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xl[2], xl[3]}, sacc, false);
                         }
                     }
+                    acc[n] += dsc * sacc;
                 }
             }
         }
@@ -508,8 +522,8 @@ __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * b
             float v = acc[n];
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-            if (j == 0 && rl < nrow) {
-                float * yp = y + (size_t) n * ldy + row;
+            if (lane == 0) {
+                float * yp = y + (size_t) n * ldy + row0 + wv;
                 *yp = (accumulate ? *yp : 0.0f) + v;
             }
         }
@@ -531,10 +545,13 @@ static int kq_q6k_staged_t(const uint8_t * bp, int rows, int cols, const void * 
         if (e != hipSuccess) return fail_hip("LDS opt-in for the staged Q6_K kernel", e);
         opted[slot] = lds;
     }
-    const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block((unsigned) (64 * rpw));
-    if (slot == 0) launch_kernel(q6k_gemv_staged_kernel<1, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate);
-    else if (slot == 1) launch_kernel(q6k_gemv_staged_kernel<4, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate);
-    else launch_kernel(q6k_gemv_staged_kernel<16, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate);
+    /* x waves: enough for one batch of eight 16-byte groups per lane, within 16 waves */
+    int xw = (ncol * cols + 4095) / 4096;
+    xw = xw < 1 ? 1 : (xw > 16 - rpw ? 16 - rpw : xw);
+    const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block((unsigned) (64 * (rpw + xw)));
+    if (slot == 0) launch_kernel(q6k_gemv_staged_kernel<1, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw);
+    else if (slot == 1) launch_kernel(q6k_gemv_staged_kernel<4, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw);
+    else launch_kernel(q6k_gemv_staged_kernel<16, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("staged Q6_K launch", e);
 }
@@ -575,18 +592,18 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
         else if (ncol <= 8) KQ_LAUNCH(K, 8, XF); \
         else KQ_LAUNCH(K, 16, XF);              \
     } while (0)
-    if (kind == 6 && cols <= 16384 && (cols / 256) % 2 == 0 && !((uintptr_t) blocks & 3) && !(xf32 && ncol > 4)) {
-        /* rows per workgroup: about one workgroup per CU, two rows per wave,
-         * the rows' blocks and x within LDS */
+    if (kind == 6 && cols >= 1280 && cols <= 16384 && (cols / 256) % 2 == 0 && !((uintptr_t) blocks & 3) &&
+        !(xf32 && ncol > 4)) {
+        /* rows per workgroup: about one workgroup per CU, one row per wave
+         * (rows of at least 1 KB, the size of one copy) plus the wave that
+         * stages x, the rows' blocks and x within LDS */
         const size_t rowbytes = (size_t) (cols / 256) * 210;
         const size_t xbytes = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (cols / 128) * 8);
         int rpw = (rows + cu_count() - 1) / cu_count();
-        rpw = rpw < 2 ? 2 : (rpw > 16 ? 16 : rpw);
+        rpw = rpw < 2 ? 2 : (rpw > 12 ? 12 : rpw);
         while (rpw > 2 && ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes > 160 * 1024) rpw--;
         const size_t slds = ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes;
-        /* every workgroup's run of blocks must hold at least one 1 KB copy */
-        const size_t last = (size_t) (rows % rpw ? rows % rpw : rpw) * rowbytes;
-        if (slds <= 160 * 1024 && last >= 1024 && rpw * rowbytes >= 1024) {
+        if (slds <= 160 * 1024) {
             return kq_q6k_staged(bp_in(blocks), rows, cols, x, xf32, ldx, ncol, y, ldy, accumulate, rpw, slds, s);
         }
     }
