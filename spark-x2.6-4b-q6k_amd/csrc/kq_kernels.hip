@@ -39,14 +39,18 @@ __device__ __forceinline__ float kq_x(const void * x, int xf32, size_t k) {
  * extra trailing dword (the stream's end is the buffer's end). */
 template <int N>
 __device__ __forceinline__ void load_stream(const uint8_t * addr, uint32_t * out, bool last_ok) {
+    /* global address space (a pointer rebuilt from an integer would be a
+     * flat one: flat loads wait on both counters) */
+    typedef const __attribute__((address_space(1))) uint32_t gu32;
+    typedef const __attribute__((address_space(1))) uint16_t gu16;
     const uintptr_t a = (uintptr_t) addr;
-    const uint32_t * p = (const uint32_t *) (a & ~(uintptr_t) 3);
+    gu32 * p = (gu32 *) (a & ~(uintptr_t) 3);
     const uint32_t sh = (uint32_t) (a & 3) * 8u;
     uint32_t w[N + 1];
 #pragma unroll
     for (int k = 0; k < N; k++) w[k] = p[k];
     if (sh && last_ok) w[N] = p[N];
-    else if (sh) w[N] = (uint32_t) *(const uint16_t *) (p + N);
+    else if (sh) w[N] = (uint32_t) *(gu16 *) (p + N);
     else w[N] = 0;
 #pragma unroll
     for (int k = 0; k < N; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
