@@ -190,22 +190,27 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, 
             for (int u = 0; u < 4; u++) {
                 const int c = cb + 16 * u;
                 if (c < bpr) {
+                    /* the block's quants as f16 pairs, once for every column */
+                    kq_h2 qa[8], qb[8];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) bytes_to_h2(qw[u][k] ^ 0x80808080u, (_Float16) 1152.0f, qa[k], qb[k]);
+                    /* every column slot, branch-free (slots past ncol re-read
+                     * the last column and are not stored), so the compiler
+                     * can read the next column's x while this one computes */
 #pragma unroll
                     for (int n = 0; n < NC; n++) {
-                        if (n < ncol) {
-                            const uint8_t * xp = lds + n * xst + c * 72;
+                        {
+                            const uint8_t * xp = lds + min(n, ncol - 1) * xst + c * 72;
                             float s = 0.0f;
 #pragma unroll
                             for (int k = 0; k < 8; k++) {
-                                kq_h2 qa, qb;
-                                bytes_to_h2(qw[u][k] ^ 0x80808080u, (_Float16) 1152.0f, qa, qb);
                                 const kq_h4 xv = *(const kq_h4 *) (xp + 8 * k);
-                                s = __builtin_amdgcn_fdot2(qa, kq_h2{xv[0], xv[1]}, s, false);
-                                s = __builtin_amdgcn_fdot2(qb, kq_h2{xv[2], xv[3]}, s, false);
+                                s = __builtin_amdgcn_fdot2(qa[k], kq_h2{xv[0], xv[1]}, s, false);
+                                s = __builtin_amdgcn_fdot2(qb[k], kq_h2{xv[2], xv[3]}, s, false);
                                 if (XF32) {
                                     const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * k);
-                                    s = __builtin_amdgcn_fdot2(qa, kq_h2{xl[0], xl[1]}, s, false);
-                                    s = __builtin_amdgcn_fdot2(qb, kq_h2{xl[2], xl[3]}, s, false);
+                                    s = __builtin_amdgcn_fdot2(qa[k], kq_h2{xl[0], xl[1]}, s, false);
+                                    s = __builtin_amdgcn_fdot2(qb[k], kq_h2{xl[2], xl[3]}, s, false);
                                 }
                             }
                             acc[n] += d[u] * s;
