@@ -359,7 +359,7 @@ def bench_prefill(args, sm, torch, dev):
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16xf16->f32 (bf16 x)",
             "data": "synthetic (seeded, random-init weights of the real shapes)",
             "config": {"workload": "prefill GEMM, 512 bf16 tokens x (10240x2560 and 2560x10240 VQ)", "tokens": ntok},
-            "roofline": {"bound": "mfma", "kernel": "prefill_mfma_kernel", "achieved": round(tflops, 1),
+            "roofline": {"bound": "mfma", "kernel": "prefill_cw_kernel", "achieved": round(tflops, 1),
                          "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
                          "traffic": None, "flops_per_step": flops, "bytes_per_step": int(nbytes)},
             "reference_abi": {"us_per_step": round(ms_ref * 1e3, 2),

@@ -13,8 +13,11 @@ int prefill_simple_launch(const void * const * stages, int nst, const Layout & L
 /* The MFMA GEMM: DQV3 dim 4, 12/13-bit indices, 1 or 2 stages, x in
  * 16-byte aligned rows, y[t * ldy + r] (+)= W x_t. x is token-major
  * (x[t * ldx + k], bf16 or f32) or, with xt, K-major f32 of one stage
- * (x[k * ldx + t], the reference's xT layout, ntok >= 4). Weights are decoded
- * to f16 tiles (one rounding of the f32 decode). */
+ * (x[k * ldx + t], the reference's xT layout, ntok >= 4). Two stages enter
+ * the MFMA as one f16 weight (one rounding of the f32 decode); one stage as
+ * its exact codewords, scaled by the row gain in f32. x enters as f16. Short
+ * matrices split K through a stream-ordered workspace and a fixed-order
+ * reduction. */
 int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int ldx, int xt, int ntok);
 int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
                         int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s);

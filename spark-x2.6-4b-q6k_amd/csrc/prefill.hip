@@ -4,14 +4,15 @@
  * cb_s[idx_s(r, i)] . x[t][dim*i ..] — the reference's per-token GEMV summed
  * over stages (tools/vq/gpu/decode-gpu.cu:359-501 is its tiled form).
  *
- * prefill_mfma_kernel: the DQV3 dim-4 GEMM on the matrix cores. A workgroup
- * owns 128 rows x 128 tokens. Per 64-column chunk it decodes its weight tile
- * into LDS as f16 (W = c0*g0 + c1*g1 formed in f32 with one rounding, as the
- * reference decode does, then rounded to f16), converts the tokens' x to f16
- * beside it, and four waves run v_mfma_f32_16x16x32_f16 over 64 x 64
- * sub-tiles with f32 accumulation. Tiles are double buffered: the next
- * chunk's index words and x are in flight while the current chunk's MFMAs
- * run, and its decode follows them.
+ * prefill_cw_kernel: the DQV3 dim-4 GEMM on the matrix cores with the
+ * codewords gathered straight into the MFMA operands (no weight tile in LDS),
+ * 256 rows x 128 tokens per workgroup, split K for short matrices. It takes
+ * every MFMA-shaped call whose LDS fits.
+ *
+ * prefill_mfma_kernel: the same GEMM through a decoded f16 weight tile in
+ * LDS (64 or 128 rows x 128 tokens); it takes what the codeword kernel's LDS
+ * does not fit (two stages of an 8192-entry codebook) and y rows that are not
+ * 16-byte aligned.
  *
  * prefill_simple_kernel: one thread per (row, token), the row's indices staged
  * in LDS; any geometry and any x layout (strided), f32 arithmetic. It backs
@@ -326,6 +327,317 @@ __global__ __launch_bounds__(kPThreads) void prefill_mfma_kernel(const MfmaArgs 
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* Codeword-operand MFMA prefill                                             */
+/* ------------------------------------------------------------------------ */
+
+/* prefill_cw_kernel: the same GEMM with no decoded weight tile. Since a row's
+ * gain is constant along the row, sum_k (g0 c0_k + g1 c1_k) x_k =
+ * g0 (c0 . x) + g1 (c1 . x): each stage's f16 codewords go straight from the
+ * LDS codebook into the A operand of v_mfma_f32_32x32x16_f16 (a lane's 8
+ * columns are two dim-4 codewords), each stage accumulates in its own f32
+ * registers, and the gains are applied once in the epilogue (the decode
+ * GEMV's form, exact codewords, no rounding of W). Two stages instead fold
+ * in the lane that gathered them: W = g0 c0 + g1 c1 in f32 (one rounding,
+ * the reference decode's rule) rounded to f16, one MFMA per block. Either
+ * way a weight costs one LDS gather per stage and no trip through an LDS
+ * weight tile.
+ *
+ * A workgroup owns 256 rows x 128 tokens: wave w owns rows 32 w .. 32 w + 31
+ * against all 128 tokens (four 32 x 32 blocks), so every codeword is gathered
+ * once per workgroup, and the token tile (f16, staged by all threads, three
+ * buffers) is shared by the eight waves. The columns a lane
+ * reads are permuted so that its index words are contiguous: for MFMA step
+ * ks, lane half kh takes codewords 8 kh + 2 ks and 8 kh + 2 ks + 1 of the
+ * 16-codeword chunk, i.e. columns 32 kh + 8 ks .. + 7, on the A and the B side
+ * alike. Lane half kh therefore needs the three dwords at byte 12 kh of the
+ * row's 24-byte chunk (and bits 8 kh .. 8 kh + 7 of its 13th-bit plane).
+ *
+ * Split K (grid z): when the row and token tiles alone leave the CUs idle
+ * (the 2560-row matrix), each split covers nkc consecutive chunks and writes
+ * its partial sums to its own slice of a workspace; prefill_cw_reduce then
+ * adds the slices in split order, so the result does not depend on timing. */
+constexpr int kCT = 128;            /* tokens per workgroup tile */
+constexpr int kCR = 256;            /* rows per workgroup tile: 8 waves x 32 */
+constexpr int kCThreads = 512;
+
+struct CwArgs {
+    const uint8_t * st[2];
+    const void * x;      /* token-major: x[t * ldx + k], bf16 bits or f32; K-major (XT): f32 x[k * ldx + t] */
+    float * y;           /* y[t * ldy + r]; split z writes y + z * ysplit */
+    size_t ysplit;
+    int rows, cols, nc, ntok, ldx, ldy, accumulate, nkc;
+    uint32_t gain_off, stream_off, mrow, prow;
+};
+
+template <int NST, int EXT, int XF32, int XT, int FOLD>
+__global__ __launch_bounds__(kCThreads) void prefill_cw_kernel(const CwArgs P) {
+    /* FOLD (two stages): W = g0 c0 + g1 c1 formed in f32 (one rounding) and
+     * rounded to f16 in the lane that feeds it to the MFMA, one accumulator
+     * set; else each stage's exact codewords accumulate apart and the gains
+     * apply in the epilogue */
+    constexpr int NA = FOLD ? 1 : NST;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const uint32_t cbb = (uint32_t) P.nc * 8u;
+    _Float16 * Bt = (_Float16 *) (lds + NST * cbb);   /* [3][kCT][kPS] tokens */
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m32 = lane & 31, kh = lane >> 5;
+    const int r0 = blockIdx.x * kCR, t0 = blockIdx.y * kCT;
+    const int kcb = blockIdx.z * P.nkc;               /* this split's first chunk */
+    const int nkc = P.nkc;
+
+    /* codebooks to LDS in batches of unconditional 16-byte loads */
+    {
+        const int n16 = (int) (cbb >> 4), ncb = NST * n16;
+        for (int base = 0; base < ncb; base += 4 * kCThreads) {
+            pf_u4 v[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int i = min(base + k * kCThreads + tid, ncb - 1), s = i >= n16 ? 1 : 0;
+                v[k] = ((const pf_u4a *) (P.st[NST > 1 ? s : 0] + 24))[i - s * n16];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) ((pf_u4 *) lds)[min(base + k * kCThreads + tid, ncb - 1)] = v[k];
+        }
+    }
+
+    /* A role: row arow of the tile; per chunk, three index dwords per stage */
+    const int arow = min(r0 + 32 * wave + m32, P.rows - 1);
+    const uint32_t * rs[NST];
+    const uint8_t * ps[NST];
+#pragma unroll
+    for (int s = 0; s < NST; s++) {
+        rs[s] = (const uint32_t *) (P.st[s] + P.stream_off + (size_t) arow * P.mrow) + 6 * kcb + 3 * kh;
+        ps[s] = P.st[s] + P.stream_off + (size_t) P.rows * P.mrow + (size_t) arow * P.prow + 2 * kcb + kh;
+    }
+    /* x role (token-major): token xtk of the tile, columns 16 xh .. 16 xh + 15 */
+    const int xtk = tid >> 2, xh = tid & 3;
+    const int dtok = min(t0 + xtk, P.ntok - 1);
+    const uint8_t * xr = (const uint8_t *) P.x + ((size_t) dtok * P.ldx + (size_t) kPK * kcb + 16 * xh) * (XF32 ? 4 : 2);
+    /* x role (K-major f32, ntok >= 4): tokens 4 tq .. 4 tq + 3, columns 4 cg .. 4 cg + 3 of a chunk */
+    const int tq = tid & 31, cg = tid >> 5;
+    const float * xk = (const float *) P.x + (size_t) (kPK * kcb + 4 * cg) * P.ldx + min(t0 + 4 * tq, P.ntok - 4);
+
+    /* register rings of two slots: index words of chunk c in slot c & 1
+     * (loaded two chunks ahead), x of chunk c in slot c & 1 (loaded three
+     * chunks ahead, staged two ahead) */
+    constexpr int NXV = XT ? 4 : (XF32 ? 4 : 2);
+    uint32_t iw[2][NST][3], pb[2][NST];
+    pf_u4 xv[2][NXV];
+    auto fetch_idx = [&](int kc, int sl) {
+#pragma unroll
+        for (int s = 0; s < NST; s++) {
+            iw[sl][s][0] = rs[s][6 * kc];
+            iw[sl][s][1] = rs[s][6 * kc + 1];
+            iw[sl][s][2] = rs[s][6 * kc + 2];
+            pb[sl][s] = EXT ? (uint32_t) ps[s][2 * kc] : 0u;
+        }
+    };
+    auto fetch_x = [&](int kc, int sl) {
+        if constexpr (XT) {
+#pragma unroll
+            for (int k = 0; k < NXV; k++) xv[sl][k] = *(const pf_u4 *) (xk + (size_t) (kPK * kc + k) * P.ldx);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NXV; k++) xv[sl][k] = ((const pf_u4 *) (xr + kPK * kc * (XF32 ? 4 : 2)))[k];
+        }
+    };
+    /* the token tile of the chunk in x slot sl, as f16, into buffer b */
+    auto stage_x = [&](int b, int sl) {
+        if constexpr (XT) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pf_h4 v4;
+#pragma unroll
+                for (int c = 0; c < 4; c++) v4[c] = (_Float16) __uint_as_float(xv[sl][c][i]);
+                *(pf_h4 *) (Bt + (b * kCT + 4 * tq + i) * kPS + 4 * cg) = v4;
+            }
+            return;
+        }
+        _Float16 * bd = Bt + (b * kCT + xtk) * kPS + 16 * xh;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            pf_h8 v8;
+            if (XF32) {
+                const pf_u4 lo = xv[sl][2 * k], hi = xv[sl][2 * k + 1];
+                v8[0] = (_Float16) __uint_as_float(lo.x); v8[1] = (_Float16) __uint_as_float(lo.y);
+                v8[2] = (_Float16) __uint_as_float(lo.z); v8[3] = (_Float16) __uint_as_float(lo.w);
+                v8[4] = (_Float16) __uint_as_float(hi.x); v8[5] = (_Float16) __uint_as_float(hi.y);
+                v8[6] = (_Float16) __uint_as_float(hi.z); v8[7] = (_Float16) __uint_as_float(hi.w);
+            } else {
+                const pf_u4 q = xv[sl][k];
+                v8[0] = (_Float16) __uint_as_float(q.x << 16); v8[1] = (_Float16) __uint_as_float(q.x & 0xffff0000u);
+                v8[2] = (_Float16) __uint_as_float(q.y << 16); v8[3] = (_Float16) __uint_as_float(q.y & 0xffff0000u);
+                v8[4] = (_Float16) __uint_as_float(q.z << 16); v8[5] = (_Float16) __uint_as_float(q.z & 0xffff0000u);
+                v8[6] = (_Float16) __uint_as_float(q.w << 16); v8[7] = (_Float16) __uint_as_float(q.w & 0xffff0000u);
+            }
+            *(pf_h8 *) (bd + 8 * k) = v8;
+        }
+    };
+    /* step ks's A operand of each stage (codewords 2 ks and 2 ks + 1 of the
+     * lane's eight), from index slot sl */
+    auto gather_a = [&](int sl, int ks, pf_h8 * a) {
+#pragma unroll
+        for (int s = 0; s < NST; s++) {
+            uint32_t i0 = pf_field12(iw[sl][s][0], iw[sl][s][1], iw[sl][s][2], 2 * ks);
+            uint32_t i1 = pf_field12(iw[sl][s][0], iw[sl][s][1], iw[sl][s][2], 2 * ks + 1);
+            if (EXT) {
+                i0 |= ((pb[sl][s] >> (2 * ks)) & 1u) << 12;
+                i1 |= ((pb[sl][s] >> (2 * ks + 1)) & 1u) << 12;
+            }
+            const pf_h4 lo = *(const pf_h4 *) (lds + s * cbb + 8u * i0);
+            const pf_h4 hi = *(const pf_h4 *) (lds + s * cbb + 8u * i1);
+            a[s] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+    /* step ks's B operands (four token blocks) from token buffer b */
+    auto read_b = [&](int b, int ks, pf_h8 * bb) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) bb[j] = *(const pf_h8 *) (Bt + (b * kCT + 32 * j + m32) * kPS + 32 * kh + 8 * ks);
+    };
+
+    pf_f16v acc[NA][4];
+#pragma unroll
+    for (int s = 0; s < NA; s++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[s][j][e] = 0.0f;
+    /* FOLD: the gains of the lane's row */
+    float ga[NST];
+#pragma unroll
+    for (int s = 0; s < NST; s++) ga[s] = FOLD ? (float) *(const _Float16 *) (P.st[s] + P.gain_off + 2 * (size_t) arow) : 0.0f;
+
+    /* Three token buffers: chunk c sits in buffer c % 3. While chunk kc's
+     * MFMAs run, chunk kc + 2 is staged, and the first operands of chunk
+     * kc + 1 (staged a chunk earlier) are read before the barrier; each
+     * step's operands are read one step ahead of its MFMAs. */
+    __syncthreads();   /* codebooks staged */
+    fetch_idx(0, 0);
+    fetch_idx(min(1, nkc - 1), 1);
+    fetch_x(0, 0);
+    fetch_x(min(1, nkc - 1), 1);
+    stage_x(0, 0);
+    stage_x(1, 1);
+    fetch_x(min(2, nkc - 1), 0);
+    __syncthreads();
+    pf_h8 aa[2][NST], bq[2][4];
+    gather_a(0, 0, aa[0]);
+    read_b(0, 0, bq[0]);
+    int b0 = 0;
+    /* nkc is even: chunk kc0 + u uses index slot u and x slot u */
+    for (int kc0 = 0; kc0 < nkc; kc0 += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int kc = kc0 + u;
+            const int b1 = b0 == 2 ? 0 : b0 + 1, b2 = b1 == 2 ? 0 : b1 + 1;
+            /* the scheduler keeps each group in place: reads stay a step
+             * ahead of the MFMAs that use them, loads at their slot */
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_x(min(kc + 3, nkc - 1), u ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                if (ks < 3) {
+                    gather_a(u, ks + 1, aa[(ks + 1) & 1]);
+                    read_b(b0, ks + 1, bq[(ks + 1) & 1]);
+                } else {
+                    /* slot u is done: it takes chunk kc + 2's index words */
+                    fetch_idx(min(kc + 2, nkc - 1), u);
+                    gather_a(u ^ 1, 0, aa[0]);
+                    read_b(b1, 0, bq[0]);
+                }
+                if constexpr (FOLD) {
+                    const pf_h8 c0 = aa[ks & 1][0], c1 = aa[ks & 1][1];
+                    pf_h8 w;
+#pragma unroll
+                    for (int d = 0; d < 8; d++) w[d] = (_Float16) __builtin_fmaf((float) c1[d], ga[1], (float) c0[d] * ga[0]);
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w, bq[ks & 1][j], acc[0][j], 0, 0, 0);
+                    /* two operand reads between consecutive MFMAs */
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int s = 0; s < NST; s++)
+                            acc[s][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aa[ks & 1][s], bq[ks & 1][j], acc[s][j], 0, 0, 0);
+                    /* the next step's operand reads spread between the MFMAs,
+                     * one read between consecutive MFMAs, so the LDS queue
+                     * is fed evenly rather than in bursts */
+#pragma unroll
+                    for (int q = 0; q < 4 * NST; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            stage_x(b2, u);
+            __syncthreads();
+            b0 = b1;
+        }
+    }
+
+    /* block j: entry e of a lane is row 8 (e / 4) + 4 kh + e % 4 of the
+     * wave's 32 rows, token 32 j + m32; four consecutive rows per store */
+    float g[NST][4][4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = min(r0 + 32 * wave + 8 * q + 4 * kh + i, P.rows - 1);
+#pragma unroll
+            for (int s = 0; s < NST; s++) g[s][q][i] = (float) *(const _Float16 *) (P.st[s] + P.gain_off + 2 * (size_t) row);
+        }
+    float * yb = P.y + blockIdx.z * P.ysplit;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int tok = t0 + 32 * j + m32;
+        if (tok >= P.ntok) continue;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int row = r0 + 32 * wave + 8 * q + 4 * kh;
+            if (row >= P.rows) continue;
+            pf_f4 v;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float t = 0.0f;
+                if (FOLD) t = acc[0][j][4 * q + i];
+                else
+#pragma unroll
+                    for (int s = 0; s < NST; s++) t = __builtin_fmaf(g[s][q][i], acc[s][j][4 * q + i], t);
+                v[i] = t;
+            }
+            float * yp = yb + (size_t) tok * P.ldy + row;
+            if (row + 4 <= P.rows) {
+                if (P.accumulate) v += *(const pf_f4 *) yp;
+                *(pf_f4 *) yp = v;
+            } else {
+                for (int i = 0; i < 4 && row + i < P.rows; i++) yp[i] = (P.accumulate ? yp[i] : 0.0f) + v[i];
+            }
+        }
+    }
+}
+
+/* y[t][r] (+)= the sum of the splits' partial sums, in split order */
+__global__ __launch_bounds__(256) void prefill_cw_reduce(const float * ws, int nsplit, int rows, int ntok, float * y,
+                                                          int ldy, int accumulate) {
+    const size_t n4 = (size_t) ntok * (rows >> 2);
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const int t = (int) (i / (size_t) (rows >> 2)), r = 4 * (int) (i % (size_t) (rows >> 2));
+    const size_t slice = (size_t) ntok * rows;
+    float * yp = y + (size_t) t * ldy + r;
+    pf_f4 v = accumulate ? *(const pf_f4 *) yp : pf_f4{0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < nsplit; z++) v += *(const pf_f4 *) (ws + z * slice + (size_t) t * rows + r);
+    *(pf_f4 *) yp = v;
+}
+
 /* The MFMA kernel takes DQV3 dim-4 stages with 12- or 13-bit indices, 1 or
  * 2 stages, an even codebook, columns a multiple of 128, dword-aligned row
  * streams, and x in 16-byte aligned rows: token-major, or K-major f32 of one
@@ -379,6 +691,134 @@ static int prefill_mfma_t(const MfmaArgs & P, int nc, hipStream_t s) {
     return prefill_mfma_rt<NST, EXT, XF32, PF, XT, 128>(P, prefill_lds(NST, nc, 128), s);
 }
 
+/* LDS of a codeword-operand workgroup: codebooks and three token tiles */
+static size_t prefill_cw_lds(int nst, int nc) { return (size_t) nst * nc * 8 + (size_t) 3 * kCT * kPS * 2; }
+
+/* The codeword-operand kernel takes what the tile kernel takes, with y in
+ * 16-byte aligned rows (four rows per store), K-major x of whole token
+ * quads, and its LDS within the CU's 160 KB. */
+static int prefill_cw_ready(const Layout & L, int nst, const void * x, int xf32, int ldx, int xt, int ntok,
+                            const float * y, int ldy) {
+    if (!prefill_mfma_ready(L, nst, x, xf32, ldx, xt, ntok)) return 0;
+    if (xt && ntok % 4) return 0;
+    if (((uintptr_t) y & 15u) || ldy % 4) return 0;
+    return prefill_cw_lds(nst, L.nc) <= 160 * 1024;
+}
+
+/* K splits: a split costs its chunks times the rounds of workgroups over the
+ * CUs, plus, past one split, the reduction's traffic (the slices written and
+ * read back, and y) at about 8 bytes per ns, in chunk times of about 0.9 us. */
+static int prefill_cw_splits(int rows, int ntok, int nk) {
+    const long tiles = (long) ((rows + kCR - 1) / kCR) * ((ntok + kCT - 1) / kCT), G = cu_count();
+    int best = 1;
+    double best_cost = (double) ((tiles + G - 1) / G) * nk;
+    if (rows % 4) return 1;
+    for (int S = 2; S <= 16; S++) {
+        if (nk % S || (nk / S) % 2) continue;
+        const double red_us = (double) (2 * S + 2) * ntok * rows * 4 / 8e3 / 1e3;
+        const double cost = (double) ((tiles * S + G - 1) / G) * (nk / S) + red_us / 0.9;
+        if (cost < best_cost) { best_cost = cost; best = S; }
+    }
+    return best;
+}
+
+/* the split slices come from a pool owned by the library (stream ordered,
+ * kept between calls), one per device */
+static int cw_workspace(size_t bytes, hipStream_t s, void ** out) {
+    static hipMemPool_t pools[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail_hip("get device", e);
+    if (dev < 0 || dev >= 64) { set_error("device %d is outside the pool table", dev); return -1; }
+    if (!pools[dev]) {
+        hipMemPoolProps props;
+        memset(&props, 0, sizeof props);
+        props.allocType = hipMemAllocationTypePinned;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t p = nullptr;
+        e = hipMemPoolCreate(&p, &props);
+        if (e != hipSuccess) return fail_hip("memory pool create", e);
+        uint64_t keep = ~0ull;
+        e = hipMemPoolSetAttribute(p, hipMemPoolAttrReleaseThreshold, &keep);
+        if (e != hipSuccess) return fail_hip("memory pool attribute", e);
+        pools[dev] = p;
+    }
+    e = hipMallocFromPoolAsync(out, bytes, pools[dev], s);
+    return e == hipSuccess ? 0 : fail_hip("split workspace", e);
+}
+
+template <int NST, int EXT, int XF32, int XT>
+static int prefill_cw_t(const CwArgs & P, int nsplit, hipStream_t s) {
+    /* two stages fold into one f16 weight (one MFMA per block, measured
+     * about 10 % faster on the FFN pair than accumulating the stages apart);
+     * one stage keeps its exact codewords */
+    constexpr int FOLD = NST == 2 ? 1 : 0;
+    static size_t opted = 0;
+    const size_t lds = prefill_cw_lds(NST, P.nc);
+    const void * fn = (const void *) prefill_cw_kernel<NST, EXT, XF32, XT, FOLD>;
+    if (lds > 65536 && lds > opted) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return fail_hip("LDS opt-in for the codeword prefill kernel", e);
+        opted = lds;
+    }
+    const dim3 grid((unsigned) ((P.rows + kCR - 1) / kCR), (unsigned) ((P.ntok + kCT - 1) / kCT), (unsigned) nsplit);
+    launch_kernel(prefill_cw_kernel<NST, EXT, XF32, XT, FOLD>, grid, dim3(kCThreads), (uint32_t) lds, s, P);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail_hip("codeword prefill launch", e);
+}
+
+static int prefill_cw_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32,
+                             int ldx, int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s) {
+    CwArgs P;
+    memset(&P, 0, sizeof P);
+    P.st[0] = (const uint8_t *) stages[0];
+    P.st[1] = (const uint8_t *) stages[nst > 1 ? 1 : 0];
+    P.x = x;
+    P.rows = L.rows; P.cols = L.cols; P.nc = L.nc; P.ntok = ntok;
+    P.ldx = ldx;
+    P.gain_off = (uint32_t) L.gain_off;
+    P.stream_off = (uint32_t) L.stream_off;
+    P.mrow = (uint32_t) L.mrow;
+    P.prow = (uint32_t) L.prow;
+    const int nk = L.cols / kPK, nsplit = prefill_cw_splits(L.rows, ntok, nk);
+    P.nkc = nk / nsplit;
+    void * ws = nullptr;
+    if (nsplit > 1) {
+        P.ysplit = (size_t) ntok * L.rows;
+        if (cw_workspace(P.ysplit * nsplit * sizeof(float), s, &ws)) return -1;
+        P.y = (float *) ws;
+        P.ldy = L.rows;
+        P.accumulate = 0;
+    } else {
+        P.y = y;
+        P.ldy = ldy;
+        P.accumulate = accumulate;
+    }
+    const int ext = L.nbit > 12;
+    int rc;
+    if (xt) rc = ext ? prefill_cw_t<1, 1, 1, 1>(P, nsplit, s) : prefill_cw_t<1, 0, 1, 1>(P, nsplit, s);
+    else if (nst == 2) {
+        if (xf32) rc = ext ? prefill_cw_t<2, 1, 1, 0>(P, nsplit, s) : prefill_cw_t<2, 0, 1, 0>(P, nsplit, s);
+        else rc = ext ? prefill_cw_t<2, 1, 0, 0>(P, nsplit, s) : prefill_cw_t<2, 0, 0, 0>(P, nsplit, s);
+    } else {
+        if (xf32) rc = ext ? prefill_cw_t<1, 1, 1, 0>(P, nsplit, s) : prefill_cw_t<1, 0, 1, 0>(P, nsplit, s);
+        else rc = ext ? prefill_cw_t<1, 1, 0, 0>(P, nsplit, s) : prefill_cw_t<1, 0, 0, 0>(P, nsplit, s);
+    }
+    if (nsplit > 1) {
+        if (!rc) {
+            const size_t n4 = (size_t) ntok * (L.rows / 4);
+            launch_kernel(prefill_cw_reduce, dim3((unsigned) ((n4 + 255) / 256)), dim3(256), 0u, s, (const float *) ws,
+                          nsplit, L.rows, ntok, y, ldy, accumulate);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) rc = fail_hip("split reduction launch", e);
+        }
+        hipError_t e = hipFreeAsync(ws, s);
+        if (!rc && e != hipSuccess) rc = fail_hip("split workspace release", e);
+    }
+    return rc;
+}
+
 int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
                         int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s) {
     if (!prefill_mfma_ready(L, nst, x, xf32, ldx, xt, ntok)) {
@@ -386,6 +826,8 @@ int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, 
         return -1;
     }
     if (ntok <= 0) { set_error("prefill needs at least one token"); return -1; }
+    if (prefill_cw_ready(L, nst, x, xf32, ldx, xt, ntok, y, ldy))
+        return prefill_cw_launch(stages, nst, L, x, xf32, ldx, xt, ntok, y, ldy, accumulate, s);
     MfmaArgs P;
     memset(&P, 0, sizeof P);
     P.st[0] = (const uint8_t *) stages[0];

@@ -268,13 +268,13 @@ def test_prefill_token_major(sm, ref, dev, ntok):
                                                     (256, 10240, 64, 4096, False), (10240, 256, 1024, 4096, False),
                                                     (10200, 256, 1000, 8192, True)])
 def test_prefill_mfma_against_oracle(sm, ref, dev, rows, cols, ntok, nc, f32):
-    """The matrix-core prefill: ragged row and token tiles, 13-bit indices,
-    f32 x, and the long 10240-column rows of down_proj. Small grids run
-    64-row tiles; 10240 rows x 1024 tokens (three rounds of 128-row
-    workgroups over 256 CUs against five of 64-row ones) run 128-row tiles.
-    Weights enter the MFMA as f16 (one rounding of the exact decode), so the
-    bar is the 1e-3 relative L2 of the GEMM gate, not the GEMV's f32-exact
-    1e-5."""
+    """The matrix-core prefill: ragged row and token tiles (130 rows end
+    inside a four-row store), f32 x, the long 10240-column rows of down_proj
+    (256 x 10240 x 64 tokens splits K sixteen ways: one row tile, one token
+    tile), and an 8192-entry two-stage codebook, whose LDS only the weight-
+    tile kernel holds (64 x 512 and 10200 x 256). Two stages enter the MFMA
+    as one f16 weight (one rounding of the exact decode), so the bar is the
+    1e-3 relative L2 of the GEMM gate, not the GEMV's f32-exact 1e-5."""
     import torch
     data = sm.synth_container(rows * 3 + ntok, rows, cols, 4, nc, 2, 1)
     W = ref.decode(data).astype(np.float64)
