@@ -520,10 +520,62 @@ __global__ __launch_bounds__(kCThreads) void prefill_cw_kernel(const CwArgs P) {
     stage_x(1, 1);
     fetch_x(min(2, nkc - 1), 0);
     __syncthreads();
+    int b0 = 0;
+    if constexpr (FOLD) {
+        /* Steps t = 4 kc + ks run a three-deep pipeline in each wave: at step
+         * t the wave gathers the codewords of step t + 2, reads the token
+         * operands of step t + 1, folds step t + 1's weights and runs step
+         * t's MFMAs, the folding VALU interleaved between the MFMAs so the
+         * matrix pipe runs while the same wave decodes. */
+        auto fold = [&](const pf_h8 * c) {
+            pf_h8 w;
+#pragma unroll
+            for (int d = 0; d < 8; d++)   /* c0 g0 is exact in f32: both products map to v_fma_mix_f32 */
+                w[d] = (_Float16) __builtin_fmaf((float) c[1][d], ga[1], __builtin_fmaf((float) c[0][d], ga[0], 0.0f));
+            return w;
+        };
+        pf_h8 raw[2][NST], wv[2], bq[2][4];
+        gather_a(0, 0, raw[0]);
+        gather_a(0, 1, raw[1]);
+        read_b(0, 0, bq[0]);
+        wv[0] = fold(raw[0]);
+        for (int kc0 = 0; kc0 < nkc; kc0 += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int kc = kc0 + u;
+                const int b1 = b0 == 2 ? 0 : b0 + 1, b2 = b1 == 2 ? 0 : b1 + 1;
+                __builtin_amdgcn_sched_barrier(0);
+                fetch_x(min(kc + 3, nkc - 1), u ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    /* step t + 2's codewords into the slot step t's have left */
+                    if (ks < 2) gather_a(u, ks + 2, raw[ks & 1]);
+                    else gather_a(u ^ 1, ks - 2, raw[ks & 1]);
+                    if (ks == 2) fetch_idx(min(kc + 2, nkc - 1), u);   /* slot u is done */
+                    if (ks < 3) read_b(b0, ks + 1, bq[(ks + 1) & 1]);
+                    else read_b(b1, 0, bq[0]);
+                    wv[(ks + 1) & 1] = fold(raw[(ks + 1) & 1]);
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wv[ks & 1], bq[ks & 1][j], acc[0][j], 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                stage_x(b2, u);
+                __syncthreads();
+                b0 = b1;
+            }
+        }
+    } else {
     pf_h8 aa[2][NST], bq[2][4];
     gather_a(0, 0, aa[0]);
     read_b(0, 0, bq[0]);
-    int b0 = 0;
     /* nkc is even: chunk kc0 + u uses index slot u and x slot u */
     for (int kc0 = 0; kc0 < nkc; kc0 += 2) {
 #pragma unroll
@@ -546,34 +598,18 @@ __global__ __launch_bounds__(kCThreads) void prefill_cw_kernel(const CwArgs P) {
                     gather_a(u ^ 1, 0, aa[0]);
                     read_b(b1, 0, bq[0]);
                 }
-                if constexpr (FOLD) {
-                    const pf_h8 c0 = aa[ks & 1][0], c1 = aa[ks & 1][1];
-                    pf_h8 w;
 #pragma unroll
-                    for (int d = 0; d < 8; d++) w[d] = (_Float16) __builtin_fmaf((float) c1[d], ga[1], (float) c0[d] * ga[0]);
+                for (int j = 0; j < 4; j++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w, bq[ks & 1][j], acc[0][j], 0, 0, 0);
-                    /* two operand reads between consecutive MFMAs */
+                    for (int s = 0; s < NST; s++)
+                        acc[s][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aa[ks & 1][s], bq[ks & 1][j], acc[s][j], 0, 0, 0);
+                /* the next step's operand reads spread between the MFMAs,
+                 * one read between consecutive MFMAs, so the LDS queue is fed
+                 * evenly rather than in bursts */
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-#pragma unroll
-                        for (int s = 0; s < NST; s++)
-                            acc[s][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aa[ks & 1][s], bq[ks & 1][j], acc[s][j], 0, 0, 0);
-                    /* the next step's operand reads spread between the MFMAs,
-                     * one read between consecutive MFMAs, so the LDS queue
-                     * is fed evenly rather than in bursts */
-#pragma unroll
-                    for (int q = 0; q < 4 * NST; q++) {
-                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    }
+                for (int q = 0; q < 4 * NST; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -581,6 +617,7 @@ __global__ __launch_bounds__(kCThreads) void prefill_cw_kernel(const CwArgs P) {
             __syncthreads();
             b0 = b1;
         }
+    }
     }
 
     /* block j: entry e of a lane is row 8 (e / 4) + 4 kh + e % 4 of the
