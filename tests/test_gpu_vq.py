@@ -295,6 +295,30 @@ def test_prefill_mfma_against_oracle(sm, ref, dev, rows, cols, ntok, nc, f32):
     assert rel_l2(y2.cpu().numpy(), 2 * want) <= BAR
 
 
+def test_prefill_full_size_down_split_k(sm, ref, dev):
+    """down_proj at its real size, 2560 x 10240 against 512 bf16 tokens: the
+    2560 rows give 10 x 4 row and token tiles, so K splits five ways and a
+    reduction adds the slices in split order. Two runs are bit-identical (the
+    split order fixes the sums), and the result meets the GEMM gate against
+    the oracle's decode and an f64 product."""
+    import torch
+    rows, cols, ntok = 2560, 10240, 512
+    data = sm.synth_container(0x9F01, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    xt, xf = _x(sm, 0x9F11, ntok, cols, False)
+    ys = []
+    for _ in range(2):
+        y = torch.full((ntok, rows), float("nan"), device=dev)
+        dc.prefill(xt, y)
+        torch.cuda.synchronize()
+        ys.append(y.cpu().numpy())
+    assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32))
+    err = rel_l2(ys[0], xf.astype(np.float64) @ W.T)
+    print(f"prefill {rows}x{cols} ntok {ntok}: relL2 {err:.2e}")
+    assert err <= BAR
+
+
 def test_prefill_reference_layout(sm, ref, dev):
     import torch
     rows, cols, ntok = 48, 128, 20
