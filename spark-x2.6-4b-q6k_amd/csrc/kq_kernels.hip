@@ -158,63 +158,84 @@ __device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ld
 
 /* ---------------------------------- Q8_0 --------------------------------- */
 
-template <int NC, int XF32>
+/* Lane (j, g) of a wave sums blocks j, j + 16, j + 32, ... of RPL rows, the
+ * rows of a wave being 4 RPL consecutive ones, and 16 lanes reduce each row
+ * (sum16). Per row and column the arithmetic is the same for every RPL and
+ * NC: 16 fdot2 per block in column order, acc += d * s in block order, the
+ * same reduction tree, so each column of a several-column launch equals a
+ * one-column launch bit for bit. With RPL = 4 a lane reads each activation
+ * of a block once for four rows (several columns read x from LDS once per
+ * four rows instead of once per row); one column keeps RPL = 1 and four
+ * blocks of one row in flight. */
+template <int NC, int XF32, int RPL = 1>
 __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, int rows, int cols, const void * x,
                                                         int ldx, int ncol, float * y, int ldy, int accumulate) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int UB = 4 / RPL;   /* blocks of each row per pass: four loads in flight per lane */
     const int bpr = cols / 32, xst = bpr * 72;
     kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
     __syncthreads();
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const size_t total = (size_t) rows * bpr;
-    const int row_step = gridDim.x * (blockDim.x >> 6) * 4;
-    for (int r0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 4; r0 < rows; r0 += row_step) {
-        const int row = r0 + g, rowc = min(row, rows - 1);
-        float acc[NC];
+    const int row_step = gridDim.x * (blockDim.x >> 6) * 4 * RPL;
+    for (int r0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 4 * RPL; r0 < rows; r0 += row_step) {
+        float acc[RPL][NC];
 #pragma unroll
-        for (int n = 0; n < NC; n++) acc[n] = 0.0f;
-        for (int cb = j; cb < bpr; cb += 64) {
-            uint32_t qw[4][8];
-            float d[4];
+        for (int i = 0; i < RPL; i++)
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int n = 0; n < NC; n++) acc[i][n] = 0.0f;
+        for (int cb = j; cb < bpr; cb += 16 * UB) {
+            uint32_t qw[UB][RPL][8];
+            float d[UB][RPL];
+#pragma unroll
+            for (int u = 0; u < UB; u++) {
                 const int c = cb + 16 * u;
                 if (c < bpr) {
-                    const size_t b = (size_t) rowc * bpr + c;
-                    const uint8_t * blk = blocks + b * 34;
-                    d[u] = kq_f16(*(const uint16_t *) blk);
-                    load_stream<8>(blk + 2, qw[u], b + 1 < total);
+#pragma unroll
+                    for (int i = 0; i < RPL; i++) {
+                        const size_t b = (size_t) min(r0 + RPL * g + i, rows - 1) * bpr + c;
+                        const uint8_t * blk = blocks + b * 34;
+                        d[u][i] = kq_f16(*(const uint16_t *) blk);
+                        load_stream<8>(blk + 2, qw[u][i], b + 1 < total);
+                    }
                 }
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < UB; u++) {
                 const int c = cb + 16 * u;
                 if (c < bpr) {
                     /* the block's quants as f16 pairs, once for every column */
-                    kq_h2 qa[8], qb[8];
+                    kq_h2 qa[RPL][8], qb[RPL][8];
 #pragma unroll
-                    for (int k = 0; k < 8; k++) bytes_to_h2(qw[u][k] ^ 0x80808080u, (_Float16) 1152.0f, qa[k], qb[k]);
+                    for (int i = 0; i < RPL; i++)
+#pragma unroll
+                        for (int k = 0; k < 8; k++) bytes_to_h2(qw[u][i][k] ^ 0x80808080u, (_Float16) 1152.0f, qa[i][k], qb[i][k]);
                     /* every column slot, branch-free (slots past ncol re-read
                      * the last column and are not stored), so the compiler
                      * can read the next column's x while this one computes */
 #pragma unroll
                     for (int n = 0; n < NC; n++) {
-                        {
-                            const uint8_t * xp = lds + min(n, ncol - 1) * xst + c * 72;
-                            float s = 0.0f;
+                        const uint8_t * xp = lds + min(n, ncol - 1) * xst + c * 72;
+                        float s[RPL];
 #pragma unroll
-                            for (int k = 0; k < 8; k++) {
-                                const kq_h4 xv = *(const kq_h4 *) (xp + 8 * k);
-                                s = __builtin_amdgcn_fdot2(qa[k], kq_h2{xv[0], xv[1]}, s, false);
-                                s = __builtin_amdgcn_fdot2(qb[k], kq_h2{xv[2], xv[3]}, s, false);
+                        for (int i = 0; i < RPL; i++) s[i] = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < 8; k++) {
+                            const kq_h4 xv = *(const kq_h4 *) (xp + 8 * k);
+                            kq_h4 xl;
+                            if (XF32) xl = *(const kq_h4 *) (xp + ncol * xst + 8 * k);
+#pragma unroll
+                            for (int i = 0; i < RPL; i++) {
+                                s[i] = __builtin_amdgcn_fdot2(qa[i][k], kq_h2{xv[0], xv[1]}, s[i], false);
+                                s[i] = __builtin_amdgcn_fdot2(qb[i][k], kq_h2{xv[2], xv[3]}, s[i], false);
                                 if (XF32) {
-                                    const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * k);
-                                    s = __builtin_amdgcn_fdot2(qa[k], kq_h2{xl[0], xl[1]}, s, false);
-                                    s = __builtin_amdgcn_fdot2(qb[k], kq_h2{xl[2], xl[3]}, s, false);
+                                    s[i] = __builtin_amdgcn_fdot2(qa[i][k], kq_h2{xl[0], xl[1]}, s[i], false);
+                                    s[i] = __builtin_amdgcn_fdot2(qb[i][k], kq_h2{xl[2], xl[3]}, s[i], false);
                                 }
                             }
-                            acc[n] += d[u] * s;
                         }
+#pragma unroll
+                        for (int i = 0; i < RPL; i++) acc[i][n] += d[u][i] * s[i];
                     }
                 }
             }
@@ -222,10 +243,14 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, 
 #pragma unroll
         for (int n = 0; n < NC; n++) {
             if (n < ncol) {
-                const float v = sum16(acc[n]);
-                if (j == 0 && row < rows) {
-                    float * yp = y + (size_t) n * ldy + row;
-                    *yp = (accumulate ? *yp : 0.0f) + v;
+#pragma unroll
+                for (int i = 0; i < RPL; i++) {
+                    const float v = sum16(acc[i][n]);
+                    const int row = r0 + RPL * g + i;
+                    if (j == 0 && row < rows) {
+                        float * yp = y + (size_t) n * ldy + row;
+                        *yp = (accumulate ? *yp : 0.0f) + v;
+                    }
                 }
             }
         }
@@ -624,9 +649,25 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
     } else if (kind == 6) {
         if (xf32) KQ_PICK(q6k_gemv_kernel, 1);
         else KQ_PICK(q6k_gemv_kernel, 0);
+    } else if (ncol == 1) {
+        if (xf32) KQ_LAUNCH(q8_0_gemv_kernel, 1, 1);
+        else KQ_LAUNCH(q8_0_gemv_kernel, 1, 0);
     } else {
-        if (xf32) KQ_PICK(q8_0_gemv_kernel, 1);
-        else KQ_PICK(q8_0_gemv_kernel, 0);
+        /* four rows per lane: 64 rows per workgroup */
+        grid = (rows + 63) / 64;
+        if (grid > cap) grid = cap;
+#define KQ_LAUNCH4(NC, XF) launch_kernel(q8_0_gemv_kernel<NC, XF, 4>, dim3(grid), dim3(threads), (uint32_t) lds, s, bp, \
+                                         rows, cols, x, ldx, ncol, y, ldy, accumulate)
+        if (xf32) {
+            if (ncol <= 4) KQ_LAUNCH4(4, 1);
+            else if (ncol <= 8) KQ_LAUNCH4(8, 1);
+            else KQ_LAUNCH4(16, 1);
+        } else {
+            if (ncol <= 4) KQ_LAUNCH4(4, 0);
+            else if (ncol <= 8) KQ_LAUNCH4(8, 0);
+            else KQ_LAUNCH4(16, 0);
+        }
+#undef KQ_LAUNCH4
     }
 #undef KQ_PICK
 #undef KQ_LAUNCH
