@@ -650,6 +650,9 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
         if (xf32) KQ_PICK(q6k_gemv_kernel, 1);
         else KQ_PICK(q6k_gemv_kernel, 0);
     } else if (ncol == 1) {
+        /* one pass of 16 rows per workgroup, no cap: measured 75.8 against
+         * 78.3 us for the 151936-row head with 16 workgroups per CU looping */
+        grid = (rows + rows_per_block - 1) / rows_per_block;
         if (xf32) KQ_LAUNCH(q8_0_gemv_kernel, 1, 1);
         else KQ_LAUNCH(q8_0_gemv_kernel, 1, 0);
     } else {
