@@ -204,6 +204,49 @@ int sparkmv_plan_launch(void * plan, void * stream);
  * op_ms receives sparkmv_plan_size(plan) values. */
 int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms);
 
+/* ---- weight artifacts (host memory) ----
+ * GGUF v2/v3 (ggml's layout), the reader of tools/dspark/src/gguf.rs:95-190
+ * (Gguf::open, tensor_bytes, get_u64/get_f32/get_str/get_arr), extended to
+ * Q6_K: tensor bytes are handed out for F32 (type 0), F16 (1), BF16 (30),
+ * Q8_0 (8, 34 B per 32) and Q6_K (14, 210 B per 256); any other type is listed
+ * with nbytes 0 and refused by number. ggml dims run fastest first: a 2-D
+ * weight has dims {cols, rows}, its blocks row-major, the layout the k-quant
+ * GEMVs take. The file is memory-mapped; data pointers live until close. */
+typedef struct {
+    char name[256];
+    int ndims;
+    uint64_t dims[4];
+    uint32_t dtype;
+    uint64_t offset;   /* from the start of the data section */
+    uint64_t nbytes;   /* 0 for a type this reader does not hand out */
+} sparkmv_gguf_tensor;
+
+void * sparkmv_gguf_open(const char * path);   /* NULL on refusal */
+void sparkmv_gguf_close(void * gguf);
+int sparkmv_gguf_version(const void * gguf);
+int64_t sparkmv_gguf_tensor_count(const void * gguf);
+int64_t sparkmv_gguf_find(const void * gguf, const char * name);   /* -1 if absent */
+int sparkmv_gguf_tensor_info(const void * gguf, int64_t i, sparkmv_gguf_tensor * out);
+const void * sparkmv_gguf_tensor_data(const void * gguf, int64_t i, uint64_t * nbytes);   /* NULL on refusal */
+int64_t sparkmv_gguf_kv_count(const void * gguf);
+int sparkmv_gguf_kv_key(const void * gguf, int64_t i, char * key, int cap, uint32_t * type);
+int sparkmv_gguf_get_u64(const void * gguf, const char * key, uint64_t * out);
+int sparkmv_gguf_get_f64(const void * gguf, const char * key, double * out);
+int sparkmv_gguf_get_str(const void * gguf, const char * key, char * out, int cap);
+int64_t sparkmv_gguf_get_arr_len(const void * gguf, const char * key, uint32_t * elem);   /* -1 if absent */
+
+/* The VQ artifact directory (manifest.txt + one <name>.bin per tensor),
+ * VqDir of tools/vq-runtime/src/vq_source.rs:30-104. A read validates the
+ * file against its manifest line: stages 0 is an RQVF f32 sidecar
+ * (RawF32::open, tools/vq-format/src/lib.rs:325-350; kind 0, data = the
+ * rows x cols f32), stages >= 1 an RQVQ container (Container::open; kind 1,
+ * data = the whole file). data lives until the next read or close. */
+void * sparkmv_manifest_open(const char * dir);   /* NULL on refusal */
+void sparkmv_manifest_close(void * manifest);
+int sparkmv_manifest_count(const void * manifest);
+int sparkmv_manifest_entry(const void * manifest, int i, char * name, int cap, int * rows, int * cols, int * stages);
+int sparkmv_manifest_read(void * manifest, const char * name, const void ** data, size_t * nbytes, int * kind);
+
 /* ---- synthetic workloads (host memory; no reference counterpart) ----
  * A named, seeded generator so every test and benchmark can rebuild the same
  * inputs: xoshiro256** seeded through splitmix64; normals by Box-Muller in

@@ -9,6 +9,10 @@ Interface mirror (the reference's Rust surface this stands beside):
   DeviceContainer.gemv     tools/vq-runtime/src/model.rs:228-234 (matvec), fused
                            over stages as tools/vq/gpu/vq-model-gpu.cu:651-660 does
   DeviceContainer.dequant  lib.rs:309-315 (Container::decode) on the device
+  VqDir                    tools/vq-runtime/src/vq_source.rs:30-104 (VqDir: manifest
+                           directory of RQVQ containers and RQVF sidecars)
+  Gguf                     tools/dspark/src/gguf.rs:95-190 (Gguf::open,
+                           tensor_bytes, get_*), with Q6_K tensors handed out
 """
 import ctypes
 import os
@@ -38,6 +42,15 @@ class ContainerInfo(ctypes.Structure):
 
 class VqMatrix(ctypes.Structure):
     _fields_ = [("stages", ctypes.c_void_p * 4), ("y", ctypes.c_void_p), ("rows", ctypes.c_int)]
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("ndims", ctypes.c_int), ("dims", ctypes.c_uint64 * 4),
+                ("dtype", ctypes.c_uint32), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
+# ggml tensor types the GGUF reader hands out
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q6_K, GGML_BF16 = 0, 1, 8, 14, 30
 
 
 _I, _P, _D, _S, _U64 = ctypes.c_int, ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), ctypes.c_size_t, ctypes.c_uint64
@@ -82,6 +95,25 @@ SIGNATURES = {
     "sparkmv_plan_capture": (_I, [_P, _P]),
     "sparkmv_plan_launch": (_I, [_P, _P]),
     "sparkmv_plan_time_ops": (_I, [_P, _P, _I, _D]),
+    "sparkmv_gguf_open": (_P, [ctypes.c_char_p]),
+    "sparkmv_gguf_close": (None, [_P]),
+    "sparkmv_gguf_version": (_I, [_P]),
+    "sparkmv_gguf_tensor_count": (ctypes.c_int64, [_P]),
+    "sparkmv_gguf_find": (ctypes.c_int64, [_P, ctypes.c_char_p]),
+    "sparkmv_gguf_tensor_info": (_I, [_P, ctypes.c_int64, ctypes.POINTER(GgufTensor)]),
+    "sparkmv_gguf_tensor_data": (_P, [_P, ctypes.c_int64, ctypes.POINTER(_U64)]),
+    "sparkmv_gguf_kv_count": (ctypes.c_int64, [_P]),
+    "sparkmv_gguf_kv_key": (_I, [_P, ctypes.c_int64, ctypes.c_char_p, _I, ctypes.POINTER(ctypes.c_uint32)]),
+    "sparkmv_gguf_get_u64": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U64)]),
+    "sparkmv_gguf_get_f64": (_I, [_P, ctypes.c_char_p, _D]),
+    "sparkmv_gguf_get_str": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, _I]),
+    "sparkmv_gguf_get_arr_len": (ctypes.c_int64, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)]),
+    "sparkmv_manifest_open": (_P, [ctypes.c_char_p]),
+    "sparkmv_manifest_close": (None, [_P]),
+    "sparkmv_manifest_count": (_I, [_P]),
+    "sparkmv_manifest_entry": (_I, [_P, _I, ctypes.c_char_p, _I, ctypes.POINTER(_I), ctypes.POINTER(_I),
+                                    ctypes.POINTER(_I)]),
+    "sparkmv_manifest_read": (_I, [_P, ctypes.c_char_p, _PP, ctypes.POINTER(_S), ctypes.POINTER(_I)]),
     "sparkmv_synth_container_bytes": (_S, [_I] * 6),
     "sparkmv_synth_vq_container": (_I, [_U64, _I, _I, _I, _I, _I, _I, _P, _S]),
     "sparkmv_synth_q6k": (_I, [_U64, _I, _I, _P]),
@@ -144,6 +176,146 @@ class Container:
     @classmethod
     def open(cls, data):
         return cls(data)
+
+
+def _copy_out(ptr, n):
+    """n bytes at a library-owned address, as a writable numpy array of our own"""
+    out = np.empty(n, dtype=np.uint8)
+    if n:
+        ctypes.memmove(out.ctypes.data, ptr, n)
+    return out
+
+
+class Gguf:
+    """A GGUF v2/v3 file, memory-mapped by the library (the layout
+    tools/dspark/src/gguf.rs:95-190 reads; that reader refuses Q6_K). Tensor
+    bytes come back as copies, so they outlive the handle."""
+
+    def __init__(self, path):
+        self.h = lib().sparkmv_gguf_open(os.fsencode(path))
+        if not self.h:
+            raise SparkmvError(f"gguf open: {last_error()}")
+        self.version = lib().sparkmv_gguf_version(self.h)
+
+    def close(self):
+        if self.h:
+            lib().sparkmv_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()
+
+    def tensors(self):
+        """[{name, dims (fastest first), dtype, offset, nbytes}] in file order;
+        nbytes is 0 for a type the reader does not hand out."""
+        out = []
+        for i in range(lib().sparkmv_gguf_tensor_count(self.h)):
+            t = GgufTensor()
+            check(lib().sparkmv_gguf_tensor_info(self.h, i, ctypes.byref(t)), "gguf tensor info")
+            out.append({"name": t.name.decode(), "dims": [int(t.dims[d]) for d in range(t.ndims)],
+                        "dtype": int(t.dtype), "offset": int(t.offset), "nbytes": int(t.nbytes)})
+        return out
+
+    def _index(self, name):
+        i = lib().sparkmv_gguf_find(self.h, name.encode())
+        if i < 0:
+            raise SparkmvError(f"gguf: no tensor {name}")
+        return i
+
+    def tensor_bytes(self, name):
+        n = _U64(0)
+        p = lib().sparkmv_gguf_tensor_data(self.h, self._index(name), ctypes.byref(n))
+        if not p:
+            raise SparkmvError(f"gguf tensor {name}: {last_error()}")
+        return _copy_out(p, n.value)
+
+    def kquant(self, name):
+        """A 2-D Q8_0 or Q6_K weight as (kind 8 or 6, rows, cols, blocks): ggml
+        dims are {cols, rows}, the blocks row-major, as the GEMVs take them."""
+        t = self.tensors()[self._index(name)]
+        kind = {GGML_Q8_0: 8, GGML_Q6_K: 6}.get(t["dtype"])
+        if kind is None or len(t["dims"]) != 2:
+            raise SparkmvError(f"gguf tensor {name}: type {t['dtype']} with {len(t['dims'])} dims is not a "
+                               "2-D Q8_0 or Q6_K weight")
+        cols, rows = t["dims"]
+        return kind, rows, cols, self.tensor_bytes(name)
+
+    def keys(self):
+        out = []
+        buf = ctypes.create_string_buffer(4096)
+        ty = ctypes.c_uint32(0)
+        for i in range(lib().sparkmv_gguf_kv_count(self.h)):
+            check(lib().sparkmv_gguf_kv_key(self.h, i, buf, len(buf), ctypes.byref(ty)), "gguf key")
+            out.append((buf.value.decode(), ty.value))
+        return out
+
+    def get_u64(self, key):
+        v = _U64(0)
+        check(lib().sparkmv_gguf_get_u64(self.h, key.encode(), ctypes.byref(v)), "gguf get")
+        return v.value
+
+    def get_f64(self, key):
+        v = ctypes.c_double(0.0)
+        check(lib().sparkmv_gguf_get_f64(self.h, key.encode(), ctypes.byref(v)), "gguf get")
+        return v.value
+
+    def get_str(self, key, cap=1 << 16):
+        buf = ctypes.create_string_buffer(cap)
+        check(lib().sparkmv_gguf_get_str(self.h, key.encode(), buf, cap), "gguf get")
+        return buf.value.decode()
+
+    def get_arr_len(self, key):
+        elem = ctypes.c_uint32(0)
+        n = lib().sparkmv_gguf_get_arr_len(self.h, key.encode(), ctypes.byref(elem))
+        if n < 0:
+            raise SparkmvError(f"gguf get: {last_error()}")
+        return n, elem.value
+
+
+class VqDir:
+    """A VQ artifact directory: manifest.txt and one <name>.bin per tensor
+    (tools/vq-runtime/src/vq_source.rs:30-104). read() validates the file
+    against its manifest line and returns an RQVQ container's bytes, or a
+    norm sidecar as an f32 array [rows, cols]."""
+
+    def __init__(self, path):
+        self.h = lib().sparkmv_manifest_open(os.fsencode(path))
+        if not self.h:
+            raise SparkmvError(f"manifest open: {last_error()}")
+
+    def close(self):
+        if self.h:
+            lib().sparkmv_manifest_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def entries(self):
+        out = []
+        buf = ctypes.create_string_buffer(4096)
+        r, c, s = _I(0), _I(0), _I(0)
+        for i in range(lib().sparkmv_manifest_count(self.h)):
+            check(lib().sparkmv_manifest_entry(self.h, i, buf, len(buf), ctypes.byref(r), ctypes.byref(c),
+                                               ctypes.byref(s)), "manifest entry")
+            out.append((buf.value.decode(), r.value, c.value, s.value))
+        return out
+
+    def read(self, name):
+        p, n, kind = ctypes.c_void_p(), _S(0), _I(0)
+        check(lib().sparkmv_manifest_read(self.h, name.encode(), ctypes.byref(p), ctypes.byref(n),
+                                          ctypes.byref(kind)), "manifest read")
+        raw = _copy_out(p.value, n.value)
+        if kind.value == 1:
+            return raw
+        e = [e for e in self.entries() if e[0] == name][0]
+        return raw.view(np.float32).reshape(e[1], e[2])
 
 
 def synth_container(seed, rows, cols, dim=4, nc=4096, nstages=2, v3=1):
