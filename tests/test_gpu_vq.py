@@ -319,6 +319,28 @@ def test_prefill_full_size_down_split_k(sm, ref, dev):
     assert err <= BAR
 
 
+def test_prefill_refusals(sm, dev):
+    """Calls the prefill refuses before any launch, with real device buffers
+    so that a check that wrongly passed could not touch bad memory."""
+    import torch
+    rows, cols, ntok = 64, 256, 8
+    dc = sm.DeviceContainer(sm.synth_container(57, rows, cols))
+    x = torch.zeros(ntok, cols, dtype=torch.int16, device=dev)
+    y = torch.zeros(ntok, rows, device=dev)
+    pp, keep = dc._stages()
+    L, h = sm.lib(), dc.host
+
+    def call(nst=h.nstages, xp=x.data_ptr(), xd=sm.X_BF16, ldx=cols, n=ntok, yp=y.data_ptr(), ldy=rows):
+        return L.sparkmv_vq_prefill(pp, nst, h.dim, h.nc, rows, cols, h.v3, xp, xd, ldx, n, yp, ldy, 0, None)
+
+    assert call() == 0
+    torch.cuda.synchronize()
+    for kw, msg in [({"n": 0}, "at least one token"), ({"ldx": cols - 8}, "ldx/ldy"), ({"ldy": rows - 4}, "ldx/ldy"),
+                    ({"xd": 7}, "x dtype"), ({"xp": None}, "null pointer"), ({"yp": None}, "null pointer")]:
+        assert call(**kw) == -1, kw
+        assert msg in sm.last_error(), (kw, sm.last_error())
+
+
 def test_prefill_reference_layout(sm, ref, dev):
     import torch
     rows, cols, ntok = 48, 128, 20
