@@ -18,6 +18,7 @@
  * block's bytes follow, and the buffer's final block reads only its own bytes.
  */
 #include "kq.h"
+#include "xrange.h"
 
 #include <string.h>
 
@@ -93,10 +94,13 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t w, _Float16 bias, kq_h2 & l
  * Q6_K kernels' lanes read 128-column units, and the pad puts neighbouring
  * units on different LDS banks. */
 template <int XF32, int PADU = 0>
-__device__ __forceinline__ void kq_stage_x_by(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst,
-                                              int tid, int nthr) {
+__device__ __forceinline__ uint32_t kq_stage_x_by(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst,
+                                                  int tid, int nthr) {
     typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
     const bool vec = !((uintptr_t) x & 3) && (ncol == 1 || !(ldx & 1));
+    /* the largest staged |f16(x)|, as f16 bits (two lanes of a pair) */
+    typedef uint16_t ush2 __attribute__((ext_vector_type(2)));
+    ush2 m16 = {0, 0};
     if (vec) {
         constexpr int KB = 8, NV = XF32 ? 2 : 1;
         const int ng = cols >> 3, total = ncol * ng;
@@ -124,6 +128,14 @@ __device__ __forceinline__ void kq_stage_x_by(uint8_t * lds, const void * x, int
                 kq_h4 h0, h1;
 #pragma unroll
                 for (int q = 0; q < 4; q++) { h0[q] = (_Float16) f[q]; h1[q] = (_Float16) f[4 + q]; }
+                {
+                    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+                    const u2v a = __builtin_bit_cast(u2v, h0), b = __builtin_bit_cast(u2v, h1);
+                    m16 = __builtin_elementwise_max(m16, __builtin_bit_cast(ush2, (a.x & 0x7fff7fffu)));
+                    m16 = __builtin_elementwise_max(m16, __builtin_bit_cast(ush2, (a.y & 0x7fff7fffu)));
+                    m16 = __builtin_elementwise_max(m16, __builtin_bit_cast(ush2, (b.x & 0x7fff7fffu)));
+                    m16 = __builtin_elementwise_max(m16, __builtin_bit_cast(ush2, (b.y & 0x7fff7fffu)));
+                }
                 *(kq_h4 *) (lds + n * xst + off) = h0;
                 *(kq_h4 *) (lds + n * xst + off + 8) = h1;
                 if (XF32) {
@@ -138,22 +150,53 @@ __device__ __forceinline__ void kq_stage_x_by(uint8_t * lds, const void * x, int
                 }
             }
         }
-        return;
+        return max(m16.x, m16.y);
     }
+    uint32_t m = 0;
     for (int e = tid; e < ncol * cols; e += nthr) {
         const int n = e / cols, k = e - n * cols;
         const float v = kq_x(x, XF32, (size_t) n * ldx + k);
         const _Float16 hi = (_Float16) v;
+        m = max(m, (uint32_t) __builtin_bit_cast(uint16_t, hi) & 0x7fffu);
         const int off = (k >> 5) * 72 + (PADU ? (k >> 7) * 8 : 0) + 2 * (k & 31);
         *(_Float16 *) (lds + n * xst + off) = hi;
         if (XF32) *(_Float16 *) (lds + (ncol + n) * xst + off) = (_Float16) (v - (float) hi);
     }
+    return m;
 }
 
 /* The whole workgroup stages x. */
 template <int XF32, int PADU = 0>
-__device__ __forceinline__ void kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
-    kq_stage_x_by<XF32, PADU>(lds, x, ldx, ncol, cols, xst, (int) threadIdx.x, (int) blockDim.x);
+__device__ __forceinline__ uint32_t kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
+    return kq_stage_x_by<XF32, PADU>(lds, x, ldx, ncol, cols, xst, (int) threadIdx.x, (int) blockDim.x);
+}
+
+/* After the staging barrier, every thread of the workgroup: when the staged
+ * x looks out of f16's comfortable range, find the workgroup's largest
+ * finite |x| (x read again) and, unless that is in range, stage x again as
+ * x * 2^-k (one element per thread and step, the same layout) and return k;
+ * otherwise return 0 with x as staged. */
+template <int XF32, int PADU = 0>
+__device__ __forceinline__ int kq_x_range(uint8_t * lds, uint32_t * xr, const void * x, int ldx, int ncol, int cols,
+                                          int xst, int first = 0) {
+    if (!xr_out(xr, first)) return 0;
+    uint32_t m = 0;
+    for (int e = threadIdx.x; e < ncol * cols; e += blockDim.x) {
+        const int n = e / cols, c = e - n * cols;
+        m = max(m, xr_fin(xr_mag(kq_x(x, XF32, (size_t) n * ldx + c))));
+    }
+    const int k = xr_shift(xr, m);
+    if (!k) return 0;
+    for (int e = threadIdx.x; e < ncol * cols; e += blockDim.x) {
+        const int n = e / cols, c = e - n * cols;
+        const float v = __builtin_ldexpf(kq_x(x, XF32, (size_t) n * ldx + c), -k);
+        const _Float16 hi = (_Float16) v;
+        const int off = (c >> 5) * 72 + (PADU ? (c >> 7) * 8 : 0) + 2 * (c & 31);
+        *(_Float16 *) (lds + n * xst + off) = hi;
+        if (XF32) *(_Float16 *) (lds + (ncol + n) * xst + off) = (_Float16) (v - (float) hi);
+    }
+    __syncthreads();
+    return k;
 }
 
 /* ---------------------------------- Q8_0 --------------------------------- */
@@ -173,8 +216,11 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, 
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int UB = 4 / RPL;   /* blocks of each row per pass: four loads in flight per lane */
     const int bpr = cols / 32, xst = bpr * 72;
-    kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
+    uint32_t * xr = (uint32_t *) (lds + xr_off((XF32 ? 2 : 1) * ncol * xst));
+    const uint32_t xm = kq_stage_x<XF32>(lds, x, ldx, ncol, cols, xst);
+    xr_note_f16(xr, xm);
     __syncthreads();
+    const int xk = kq_x_range<XF32>(lds, xr, x, ldx, ncol, cols, xst);
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const size_t total = (size_t) rows * bpr;
     const int row_step = gridDim.x * (blockDim.x >> 6) * 4 * RPL;
@@ -245,7 +291,7 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, 
             if (n < ncol) {
 #pragma unroll
                 for (int i = 0; i < RPL; i++) {
-                    const float v = sum16(acc[i][n]);
+                    const float v = xr_unscale(sum16(acc[i][n]), xk);
                     const int row = r0 + RPL * g + i;
                     if (j == 0 && row < rows) {
                         float * yp = y + (size_t) n * ldy + row;
@@ -267,8 +313,11 @@ __global__ __launch_bounds__(256) void q6k_gemv_kernel(const uint8_t * blocks, i
                                                        int ldx, int ncol, float * y, int ldy, int accumulate) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int bpr = cols / 256, units = 2 * bpr, xst = (cols / 32) * 72 + (cols / 128) * 8;
-    kq_stage_x<XF32, 1>(lds, x, ldx, ncol, cols, xst);
+    uint32_t * xr = (uint32_t *) (lds + xr_off((XF32 ? 2 : 1) * ncol * xst));
+    const uint32_t xm = kq_stage_x<XF32, 1>(lds, x, ldx, ncol, cols, xst);
+    xr_note_f16(xr, xm);
     __syncthreads();
+    const int xk = kq_x_range<XF32, 1>(lds, xr, x, ldx, ncol, cols, xst);
     const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
     const int row_step = gridDim.x * (blockDim.x >> 6) * 4;
     for (int r0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 4; r0 < rows; r0 += row_step) {
@@ -324,7 +373,7 @@ __global__ __launch_bounds__(256) void q6k_gemv_kernel(const uint8_t * blocks, i
 #pragma unroll
         for (int n = 0; n < NC; n++) {
             if (n < ncol) {
-                const float v = sum16(acc[n]);
+                const float v = xr_unscale(sum16(acc[n]), xk);
                 if (j == 0 && row < rows) {
                     float * yp = y + (size_t) n * ldy + row;
                     *yp = (accumulate ? *yp : 0.0f) + v;
@@ -383,8 +432,11 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
         load_stream<2>(blk + 192 + 8 * h, scw[k], true);
     }
     /* x after the blocks are requested: both latencies overlap */
-    kq_stage_x<XF32, 1>(lds, x, ldx, ncol, cols, xst);
+    uint32_t * xr = (uint32_t *) (lds + xr_off((XF32 ? 2 : 1) * ncol * xst));
+    const uint32_t xm = kq_stage_x<XF32, 1>(lds, x, ldx, ncol, cols, xst);
+    xr_note_f16(xr, xm);
     __syncthreads();
+    const int xk = kq_x_range<XF32, 1>(lds, xr, x, ldx, ncol, cols, xst);
     float acc[NC];
 #pragma unroll
     for (int n = 0; n < NC; n++) acc[n] = 0.0f;
@@ -436,6 +488,7 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
             float v = acc[n];
 #pragma unroll
             for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            v = xr_unscale(v, xk);
             if (j == 0 && row < rows) {
                 float * yp = y + (size_t) n * ldy + row;
                 *yp = (accumulate ? *yp : 0.0f) + v;
@@ -484,9 +537,13 @@ __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * b
     const int row0 = blockIdx.x * rpw, nrow = min(rpw, rows - row0);
     const uint32_t xoff = (uint32_t) ((rpw * rowbytes + 15) & ~15u);
     const uint32_t reg = (uint32_t) wv * rowbytes;            /* this wave's row, a byte offset in LDS */
+    uint32_t * xr = (uint32_t *) (lds + xoff + xr_off((XF32 ? 2 : 1) * ncol * xst));
+    uint32_t xm = 0;
     if (wv >= rpw) {
-        /* x: the x waves' loads and LDS stores, complete before the barrier */
-        kq_stage_x_by<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst, threadIdx.x - 64 * rpw, 64 * xw);
+        /* x: the x waves' loads, LDS stores and range verdicts, complete
+         * before the barrier */
+        xm = kq_stage_x_by<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst, threadIdx.x - 64 * rpw, 64 * xw);
+        xr_note_f16(xr, xm);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     } else if (wv < nrow) {
         const uint8_t * src = blocks + (size_t) (row0 + wv) * rowbytes;
@@ -500,6 +557,8 @@ __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * b
      * keeps the compiler from moving LDS reads above it): no wave waits for
      * its row copy here. */
     asm volatile("s_barrier" ::: "memory");
+    /* every wave takes the (uniform) range decision before any leaves */
+    const int xk = kq_x_range<XF32, 1>(lds + xoff, xr, x, ldx, ncol, cols, xst, rpw);
     if (wv >= nrow) return;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* this wave's row */
     float acc[NC];
@@ -556,6 +615,7 @@ __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * b
             float v = acc[n];
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            v = xr_unscale(v, xk);
             if (lane == 0) {
                 float * yp = y + (size_t) n * ldy + row0 + wv;
                 *yp = (accumulate ? *yp : 0.0f) + v;
@@ -611,7 +671,8 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
     const int threads = 256;
     const int rows_per_block = (threads / 64) * 4;
     /* Q6_K slots carry 8 bytes of pad per 128 columns */
-    const size_t lds = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (kind == 6 ? (cols / 128) * 8 : 0));
+    const size_t lds = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (kind == 6 ? (cols / 128) * 8 : 0)) +
+                       kXrBytes;
     if (lds > 160 * 1024) { set_error("%d activation columns of %d do not fit LDS", ncol, cols); return -1; }
     int grid = (rows + rows_per_block - 1) / rows_per_block;
     const int cap = cu_count() * 16;
@@ -632,7 +693,7 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
          * (rows of at least 1 KB, the size of one copy) plus the wave that
          * stages x, the rows' blocks and x within LDS */
         const size_t rowbytes = (size_t) (cols / 256) * 210;
-        const size_t xbytes = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (cols / 128) * 8);
+        const size_t xbytes = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (cols / 128) * 8) + kXrBytes;
         int rpw = (rows + cu_count() - 1) / cu_count();
         rpw = rpw < 2 ? 2 : (rpw > 12 ? 12 : rpw);
         while (rpw > 2 && ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes > 160 * 1024) rpw--;

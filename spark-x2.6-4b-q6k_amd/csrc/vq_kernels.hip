@@ -22,6 +22,7 @@
  *                   codeword times gain is exact in f32, one rounding per add).
  */
 #include "vq.h"
+#include "xrange.h"
 
 #include <hip/hip_fp16.h>
 #include <string.h>
@@ -149,9 +150,9 @@ __device__ __forceinline__ uint32_t step_addr(const Words<NST, EXT, XG> & W, int
     return (uint32_t) s * cbb + a;
 }
 
-template <int NST, int XF32, int EXT, int XG = 0>
+template <int NST, int XF32, int EXT, int XG = 0, int SCX = 0>
 __device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8_t * lds, uint32_t cbb,
-                                      const uint8_t * xb, const uint8_t * xbl, f4 * acc) {
+                                      const uint8_t * xb, const uint8_t * xbl, f4 * acc, float sc = 1.0f) {
     h4 cw[8][NST], b[8], bl[8];
 #pragma unroll
     for (int s = 0; s < NST; s++) {
@@ -167,12 +168,15 @@ __device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8
 #pragma unroll
     for (int t = 0; t < 8; t++) {
         if constexpr (XG != 0) {
-            /* bf16 pairs to f16 (exact for the activations' range) */
+            /* bf16 pairs to f16 (exact from 2^-14 to 65504); SCX: times
+             * the power of two sc first (the out-of-range redo) */
             const uint32_t u0 = W.xg[2 * t], u1 = W.xg[2 * t + 1];
-            b[t][0] = (_Float16) __uint_as_float(u0 << 16);
-            b[t][1] = (_Float16) __uint_as_float(u0 & 0xffff0000u);
-            b[t][2] = (_Float16) __uint_as_float(u1 << 16);
-            b[t][3] = (_Float16) __uint_as_float(u1 & 0xffff0000u);
+            const float f0 = __uint_as_float(u0 << 16), f1 = __uint_as_float(u0 & 0xffff0000u);
+            const float f2 = __uint_as_float(u1 << 16), f3 = __uint_as_float(u1 & 0xffff0000u);
+            b[t][0] = (_Float16) (SCX ? f0 * sc : f0);
+            b[t][1] = (_Float16) (SCX ? f1 * sc : f1);
+            b[t][2] = (_Float16) (SCX ? f2 * sc : f2);
+            b[t][3] = (_Float16) (SCX ? f3 * sc : f3);
         } else {
             b[t] = *(const h4 *) (xb + 8 * t);
             if (XF32) bl[t] = *(const h4 *) (xbl + 8 * t);
@@ -208,6 +212,9 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
     const uint32_t cbb = (uint32_t) A.nc * 8u;
     uint8_t * lx = lds + NST * cbb;
     float * red = (float *) (lx + (XF32 ? 2 : 1) * A.ncol * A.xstride);
+    /* the x range verdicts, after the reduction area */
+    uint32_t * xr = (uint32_t *) (lds + xr_off(NST * cbb + (XF32 ? 2 : 1) * A.ncol * A.xstride +
+                                               (A.threads >> 6) * kRedStride * 4));
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m16 = lane & 15, q = lane >> 4;
     /* the workgroup's matrix: every record is read at once (independent
@@ -341,6 +348,8 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * 10 loads per thread cover from seven waves up */
     constexpr int K = 10;
     const int bd = A.threads, tid = threadIdx.x;
+    uint32_t xm = 0;          /* the largest |x| this thread staged, as f32 bits */
+    xr_u16x2 xm2 = {0, 0};    /* the same for bf16 x, by pairs */
     if constexpr (MC) {
         /* Several activation columns (speculative verify): codebooks and x
          * are staged in batches of unconditional 16-byte loads (indices past
@@ -377,6 +386,8 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
             for (int k = 0; k < KXM; k++) {
                 const int n = ci[k] / xq, e = 8 * (ci[k] - n * xq);
                 uint8_t * dst = lx + n * A.xstride + 264 * (e >> 7) + 2 * (e & 127);
+                xr_acc_bf16x2(xm2, xv[k].x); xr_acc_bf16x2(xm2, xv[k].y);
+                xr_acc_bf16x2(xm2, xv[k].z); xr_acc_bf16x2(xm2, xv[k].w);
                 h4 lo4, hi4;
                 lo4[0] = (_Float16) __uint_as_float(xv[k].x << 16);
                 lo4[1] = (_Float16) __uint_as_float(xv[k].x & 0xffff0000u);
@@ -438,6 +449,8 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                 /* eight bf16 columns -> eight f16 in the padded layout */
                 const int e = 8 * min(i, xq - 1);
                 uint8_t * dst = lx + 264 * (e >> 7) + 2 * (e & 127);
+                xr_acc_bf16x2(xm2, xv[k].x); xr_acc_bf16x2(xm2, xv[k].y);
+                xr_acc_bf16x2(xm2, xv[k].z); xr_acc_bf16x2(xm2, xv[k].w);
                 h4 lo4, hi4;
                 lo4[0] = (_Float16) __uint_as_float(xv[k].x << 16);
                 lo4[1] = (_Float16) __uint_as_float(xv[k].x & 0xffff0000u);
@@ -469,7 +482,11 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                     if (base + k * bd + tid < xpr) xv[k] = x_load(n, base + k * bd + tid);
 #pragma unroll
                 for (int k = 0; k < K; k++)
-                    if (base + k * bd + tid < xpr) x_store(n, base + k * bd + tid, xv[k]);
+                    if (base + k * bd + tid < xpr) {
+                        x_store(n, base + k * bd + tid, xv[k]);
+                        if (XF32) xm = max(xm, xr_mag_f32w(xv[k]));
+                        else xr_acc_bf16x2(xm2, xv[k]);
+                    }
             }
         }
         point(first);
@@ -480,7 +497,35 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         const int s = tid >> 1, k = tid & 1;
         ((uint32_t *) (lds + s * cbb))[4 * n16 + k] = ((const uint32_t *) ((s ? stp[NST - 1] : stp[0]) + 24))[4 * n16 + k];
     }
+    if constexpr (XG == 0) xr_note(xr, XF32 ? xm : xr_bf16_max(xm2));
     __syncthreads();
+    /* x outside f16's comfortable range: stage it again as x * 2^-xk (one
+     * element per thread and step, the staging's layout) and scale the sums
+     * back by 2^xk. XG kernels stage no x and check each unit instead. */
+    int xk = 0;
+    if constexpr (XG == 0) {
+        if (xr_out(xr)) {
+            auto xval = [&](int e) {
+                const int n = e / A.cols, kk = e - n * A.cols;
+                const size_t xi = (size_t) n * A.ldx + kk;
+                return XF32 ? ((const float *) A.x)[xi] : bf16_to_f32(((const uint16_t *) A.x)[xi]);
+            };
+            uint32_t fm = 0;   /* the largest finite |x| of this thread's elements */
+            for (int e = tid; e < ncol * A.cols; e += bd) fm = max(fm, xr_fin(xr_mag(xval(e))));
+            xk = xr_shift(xr, fm);
+            if (xk) {
+                for (int e = tid; e < ncol * A.cols; e += bd) {
+                    const int n = e / A.cols, kk = e - n * A.cols;
+                    const float f = __builtin_ldexpf(xval(e), -xk);
+                    const _Float16 hi = (_Float16) f;
+                    const int off = 264 * (kk >> 7) + 2 * (kk & 127);
+                    *(_Float16 *) (lx + n * A.xstride + off) = hi;
+                    if (XF32) *(_Float16 *) (lx + (ncol + n) * A.xstride + off) = (_Float16) (f - (float) hi);
+                }
+                __syncthreads();
+            }
+        }
+    }
 
     /* One unit: the tile's MS macro steps, then the epilogue. The index
      * words and gains of the tile are already requested. */
@@ -507,6 +552,50 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                 }
             }
         }
+        /* the factor 2^uk that the unit's sums carry back */
+        int uk = xk;
+        if constexpr (XG != 0) {
+            /* x read per step, converted per step: an |x| past f16's range
+             * shows as a non-finite sum. Then, when the wave's largest finite
+             * |x| over the unit is 2^15 or more, it sets uk and the unit runs
+             * again, one step at a time, with x * 2^-uk (an infinity or NaN in
+             * x stays one). Small x is not rescaled here: below 2^-14 it keeps
+             * f16's subnormal spacing, 2^-24. */
+            if (active) {
+                bool bad = false;
+#pragma unroll
+                for (int s = 0; s < NST; s++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) bad = bad || !__builtin_isfinite(acc[s][i]);
+                if (__builtin_amdgcn_ballot_w64(bad)) {
+                    typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+                    uint32_t m = 0;
+#pragma unroll 1
+                    for (int u = 0; u < MS; u++) {
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            const u4x v = ((const u4x *) (xgp + 256 * u))[k];
+#pragma unroll
+                            for (int h = 0; h < 4; h++)
+                                m = max(m, max(xr_fin((v[h] << 16) & 0x7fffffffu), xr_fin(v[h] & 0x7fff0000u)));
+                        }
+                    }
+                    m = xr_wave_max(m);   /* the largest finite |x| of the unit */
+                    if (m >= kXrOver) {
+                        uk = xr_shift_of(m);
+                        const float sc = __uint_as_float((uint32_t) (127 - uk) << 23);
+#pragma unroll
+                        for (int s = 0; s < NST; s++) acc[s] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+                        for (int u = 0; u < MS; u++) {
+                            Words<NST, EXT, XG> W1;
+                            load_words<NST, EXT, XG>(W1, rp, pp, xgp, u);
+                            mstep<NST, XF32, EXT, XG, 1>(W1, lds, cbb, xb, xbl, acc, sc);
+                        }
+                    }
+                }
+            }
+        }
         /* stages combine with their row gains; entry C[4q + i][m16] of this
          * lane goes to the wave's reduction area */
         float * R = red + wave * kRedStride;
@@ -520,7 +609,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                     float v = 0.0f;
 #pragma unroll
                     for (int s = 0; s < NST; s++) v += f16_to_f32((uint16_t) gw[s][i]) * acc[s][i];
-                    R[(4 * q + i) * 17 + m16] = v;
+                    R[(4 * q + i) * 17 + m16] = xr_unscale(v, uk);
                 }
                 if (lane < rpt) {
                     float part[16];
@@ -547,7 +636,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                 float v = 0.0f;
 #pragma unroll
                 for (int s = 0; s < NST; s++) v += f16_to_f32((uint16_t) gw[s][i]) * acc[s][i];
-                R[(4 * q + i) * 17 + m16] = v;
+                R[(4 * q + i) * 17 + m16] = xr_unscale(v, uk);
             }
         }
         /* with one wave per tile the wave only reads its own area back: its
@@ -786,7 +875,7 @@ static int fast_xstride(int cols, int S) { (void) S; return 264 * (cols / 128) +
 
 static size_t fast_lds(const VqCall & c, int nst, int S, int W, int xg = 0) {
     return (size_t) nst * c.nc * 8 + (xg ? 0 : (size_t) (c.xf32 ? 2 : 1) * c.ncol * fast_xstride(c.cols, S)) +
-           (size_t) W * kRedStride * 4;
+           (size_t) W * kRedStride * 4 + kXrBytes;
 }
 
 /* Several bf16 columns with x read from global memory: each lane loads its
