@@ -247,6 +247,52 @@ int sparkmv_manifest_count(const void * manifest);
 int sparkmv_manifest_entry(const void * manifest, int i, char * name, int cap, int * rows, int * cols, int * stages);
 int sparkmv_manifest_read(void * manifest, const char * name, const void ** data, size_t * nbytes, int * kind);
 
+/* ---- the decode forward: one token through every layer on the GPU ----
+ * The reference's CPU forward (tools/vq-runtime/src/model.rs:441-591) and
+ * its GPU runtime's (tools/vq/gpu/vq-model-gpu.cu:776-835): embedding row,
+ * per layer rms_norm (f64 sums), qkv and the per-head attention gate, rope
+ * over the first head_dim * partial elements, the KV store, GQA attention
+ * over the full or sliding window times sigmoid(gate), the output projection
+ * added to the residual, rms_norm, exact-erf gelu(gate) * up, down added to
+ * the residual; final rms_norm and the tied head. The trunk's matrices are
+ * VQ containers with one geometry (dim, nc, nstages, v3); the head is VQ (the
+ * reference GPU runtime's embedding) or Q8_0 (the GGUF's token_embd). x_dtype
+ * is what the matvecs read: SPARKMV_X_F32 follows the f32 reference, bf16
+ * halves their activation bytes. The model owns its KV cache and scratch
+ * (one device allocation at create); weights stay the caller's. */
+typedef struct {
+    int hidden, layers, heads, kv_heads, head_dim, intermediate, vocab;
+    float eps;
+    int sliding_window;                          /* positions a sliding layer sees */
+    double rope_full_theta, rope_full_partial;   /* config.rs:87-108 */
+    double rope_slide_theta, rope_slide_partial;
+    int max_ctx;                                 /* KV cache positions, at most 38400 */
+    int x_dtype;
+    int dim, nc, nstages, v3;                    /* the VQ geometry of every matrix */
+} sparkmv_model_cfg;
+
+typedef struct {
+    const float * in_norm, * post_norm;          /* device f32 [hidden] */
+    const void * qkv[4];                         /* [q_dim + 2 kv_dim] x hidden, stage pointers */
+    const void * attn_gate[4];                   /* [heads] x hidden */
+    const void * out[4];                         /* hidden x q_dim */
+    const void * gate[4], * up[4];               /* intermediate x hidden */
+    const void * down[4];                        /* hidden x intermediate */
+    int full;                                    /* 1 full attention, 0 sliding (config.rs:95-100) */
+} sparkmv_model_layer;
+
+void * sparkmv_model_create(const sparkmv_model_cfg * cfg);   /* NULL on refusal */
+void sparkmv_model_destroy(void * model);
+int sparkmv_model_set_layer(void * model, int layer, const sparkmv_model_layer * weights);
+/* kind 0: a VQ head (stages), 8: Q8_0 blocks [vocab][hidden / 32]; final_norm device f32 [hidden]. */
+int sparkmv_model_set_head(void * model, int kind, const void * const * stages, const void * blocks,
+                           const float * final_norm);
+/* One token at pos (model.rs:441): fills the cache row pos of every layer
+ * and writes vocab f32 logits. Asynchronous on stream. */
+int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits, void * stream);
+/* The device rows of layer's K and V cache ([max_ctx][kv_dim] f32 each). */
+int sparkmv_model_kv(void * model, int layer, float ** k, float ** v);
+
 /* ---- synthetic workloads (host memory; no reference counterpart) ----
  * A named, seeded generator so every test and benchmark can rebuild the same
  * inputs: xoshiro256** seeded through splitmix64; normals by Box-Muller in

@@ -13,6 +13,8 @@ Interface mirror (the reference's Rust surface this stands beside):
                            directory of RQVQ containers and RQVF sidecars)
   Gguf                     tools/dspark/src/gguf.rs:95-190 (Gguf::open,
                            tensor_bytes, get_*), with Q6_K tensors handed out
+  Model.forward            tools/vq-runtime/src/model.rs:441-591 (Model::forward),
+                           as the GPU runtime runs it, tools/vq/gpu/vq-model-gpu.cu:776-835
 """
 import ctypes
 import os
@@ -47,6 +49,22 @@ class VqMatrix(ctypes.Structure):
 class GgufTensor(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 256), ("ndims", ctypes.c_int), ("dims", ctypes.c_uint64 * 4),
                 ("dtype", ctypes.c_uint32), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
+class ModelCfg(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("layers", ctypes.c_int), ("heads", ctypes.c_int),
+                ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("intermediate", ctypes.c_int),
+                ("vocab", ctypes.c_int), ("eps", ctypes.c_float), ("sliding_window", ctypes.c_int),
+                ("rope_full_theta", ctypes.c_double), ("rope_full_partial", ctypes.c_double),
+                ("rope_slide_theta", ctypes.c_double), ("rope_slide_partial", ctypes.c_double),
+                ("max_ctx", ctypes.c_int), ("x_dtype", ctypes.c_int), ("dim", ctypes.c_int), ("nc", ctypes.c_int),
+                ("nstages", ctypes.c_int), ("v3", ctypes.c_int)]
+
+
+class ModelLayer(ctypes.Structure):
+    _fields_ = [("in_norm", ctypes.c_void_p), ("post_norm", ctypes.c_void_p), ("qkv", ctypes.c_void_p * 4),
+                ("attn_gate", ctypes.c_void_p * 4), ("out", ctypes.c_void_p * 4), ("gate", ctypes.c_void_p * 4),
+                ("up", ctypes.c_void_p * 4), ("down", ctypes.c_void_p * 4), ("full", ctypes.c_int)]
 
 
 # ggml tensor types the GGUF reader hands out
@@ -114,6 +132,12 @@ SIGNATURES = {
     "sparkmv_manifest_entry": (_I, [_P, _I, ctypes.c_char_p, _I, ctypes.POINTER(_I), ctypes.POINTER(_I),
                                     ctypes.POINTER(_I)]),
     "sparkmv_manifest_read": (_I, [_P, ctypes.c_char_p, _PP, ctypes.POINTER(_S), ctypes.POINTER(_I)]),
+    "sparkmv_model_create": (_P, [ctypes.POINTER(ModelCfg)]),
+    "sparkmv_model_destroy": (None, [_P]),
+    "sparkmv_model_set_layer": (_I, [_P, _I, ctypes.POINTER(ModelLayer)]),
+    "sparkmv_model_set_head": (_I, [_P, _I, _PP, _P, _P]),
+    "sparkmv_model_forward": (_I, [_P, ctypes.c_uint32, _I, _P, _P]),
+    "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
     "sparkmv_synth_container_bytes": (_S, [_I] * 6),
     "sparkmv_synth_vq_container": (_I, [_U64, _I, _I, _I, _I, _I, _I, _P, _S]),
     "sparkmv_synth_q6k": (_I, [_U64, _I, _I, _P]),
@@ -439,6 +463,57 @@ def kquant_gemv(kind, blocks, rows, cols, x, y, ncols=1, accumulate=False, strea
 def kquant_dequant(kind, blocks, rows, cols, out, stream=None):
     fn = lib().sparkmv_q6k_dequant if kind == "q6_k" else lib().sparkmv_q8_0_dequant
     check(fn(blocks.data_ptr(), rows, cols, out.data_ptr(), _stream_ptr(stream)), kind + " dequant")
+
+
+class Model:
+    """The decode forward on the GPU (sparkmv_model_*): one token through
+    every layer, tools/vq-runtime/src/model.rs:441-591 (Model::forward).
+
+    cfg: dict of the sparkmv_model_cfg fields. layers: per layer a dict with
+    in_norm, post_norm (device f32 tensors), qkv, attn_gate, out, gate, up,
+    down (DeviceContainers) and full (bool). head: a DeviceContainer (VQ) or
+    a device uint8 tensor of Q8_0 blocks; final_norm a device f32 tensor.
+    The model keeps references to everything it was given."""
+
+    def __init__(self, cfg, layers, head, final_norm):
+        c = ModelCfg(**cfg)
+        self.cfg = dict(cfg)
+        self.h = lib().sparkmv_model_create(ctypes.byref(c))
+        if not self.h:
+            raise SparkmvError("model create: " + last_error())
+        self.keep = [layers, head, final_norm]
+        for i, L in enumerate(layers):
+            w = ModelLayer()
+            w.in_norm = L["in_norm"].data_ptr()
+            w.post_norm = L["post_norm"].data_ptr()
+            for name in ("qkv", "attn_gate", "out", "gate", "up", "down"):
+                arr = getattr(w, name)
+                for s, p in enumerate(L[name].stage_ptrs):
+                    arr[s] = p
+            w.full = int(bool(L["full"]))
+            check(lib().sparkmv_model_set_layer(self.h, i, ctypes.byref(w)), "model layer %d" % i)
+        if isinstance(head, DeviceContainer):
+            arr = (ctypes.c_void_p * 4)(*(head.stage_ptrs + [None] * (4 - len(head.stage_ptrs))))
+            check(lib().sparkmv_model_set_head(self.h, 0, ctypes.cast(arr, _PP), None, final_norm.data_ptr()),
+                  "model head")
+        else:
+            check(lib().sparkmv_model_set_head(self.h, 8, None, head.data_ptr(), final_norm.data_ptr()), "model head")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().sparkmv_model_destroy(self.h)
+            self.h = None
+
+    def forward(self, token, pos, logits, stream=None):
+        """logits: device f32 [vocab]; asynchronous on stream."""
+        check(lib().sparkmv_model_forward(self.h, int(token), int(pos), logits.data_ptr(), _stream_ptr(stream)),
+              "model forward")
+
+    def kv(self, layer):
+        """(k, v) device pointers of the layer's cache, [max_ctx][kv_dim] f32 each."""
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        check(lib().sparkmv_model_kv(self.h, layer, ctypes.byref(k), ctypes.byref(v)), "model kv")
+        return k.value, v.value
 
 
 class Plan:

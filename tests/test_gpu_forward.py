@@ -1,0 +1,118 @@
+"""The decode forward on the GPU (sparkmv_model_forward) against the oracle's
+restatement of tools/vq-runtime/src/model.rs:441-591 (oracle/forward.py),
+on a small model with the reference's structure: GQA (4 query heads over 2
+kv heads), a sliding layer on each side of a full one (3-position window,
+partial rope on the full layer), VQ matrices throughout, and a tied head
+that is Q8_0 blocks or a VQ container. Tokens run past the window.
+
+Bars: with f32 activations into the matvecs (the reference's arithmetic) the
+logits of every step meet 1e-5 relative L2 (measured 7e-7) and the KV cache
+1e-5. With bf16
+activations (rounded at each matvec's input, as the decode benchmark runs)
+the logits meet 2e-2 (measured 6e-3).
+"""
+import numpy as np
+import pytest
+
+import forward as fw
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(hidden=256, layers=3, heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=320, eps=1e-6,
+           sliding_window=3, rope_full_theta=5.0e6, rope_full_partial=0.25, rope_slide_theta=1.0e4,
+           rope_slide_partial=1.0, max_ctx=16)
+FULL = [False, True, False]
+TOKENS = [5, 17, 3, 250, 42, 7, 17]
+
+
+def rel_l2(a, b):
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+
+def build(sm, ref, dev, head_kind, x_dtype):
+    import torch
+    c = CFG
+    hd, heads, kvh, hid, inter = c["head_dim"], c["heads"], c["kv_heads"], c["hidden"], c["intermediate"]
+    qd, kvd = heads * hd, kvh * hd
+    shapes = dict(qkv=(qd + 2 * kvd, hid), attn_gate=(heads, hid), out=(hid, qd), gate=(inter, hid),
+                  up=(inter, hid), down=(hid, inter))
+    rng = np.random.default_rng(11)
+    dev_layers, host_layers = [], []
+    for li in range(c["layers"]):
+        dl, hl = {}, {}
+        for k, name in enumerate(shapes):
+            r, cc = shapes[name]
+            data = sm.synth_container(1000 * li + k + 1, r, cc)
+            dl[name] = sm.DeviceContainer(data, dev)
+            hl[name] = ref.decode(data)
+        for name in ("in_norm", "post_norm"):
+            v = (1 + 0.2 * rng.standard_normal(hid)).astype(np.float32)
+            hl[name] = v
+            dl[name] = torch.from_numpy(v).to(dev)
+        dl["full"] = hl["full"] = FULL[li]
+        dev_layers.append(dl)
+        host_layers.append(hl)
+    norm = (1 + 0.2 * rng.standard_normal(hid)).astype(np.float32)
+    if head_kind == "q8_0":
+        blocks = sm.synth_q8_0(77, c["vocab"], hid)
+        embed = ref.q8_0_dequant(blocks, c["vocab"], hid)
+        head = torch.from_numpy(blocks).to(dev)
+    else:
+        data = sm.synth_container(78, c["vocab"], hid)
+        embed = ref.decode(data)
+        head = sm.DeviceContainer(data, dev)
+    cfg = dict(c, x_dtype=x_dtype, dim=4, nc=4096, nstages=2, v3=1)
+    model = sm.Model(cfg, dev_layers, head, torch.from_numpy(norm).to(dev))
+    oracle = fw.Forward(c, host_layers, embed.astype(np.float32), norm)
+    return model, oracle
+
+
+@pytest.mark.parametrize("head_kind", ["q8_0", "vq"])
+@pytest.mark.parametrize("xd", ["f32", "bf16"])
+def test_forward_against_oracle(sm, ref, dev, head_kind, xd):
+    import torch
+    x_dtype = sm.X_F32 if xd == "f32" else sm.X_BF16
+    model, oracle = build(sm, ref, dev, head_kind, x_dtype)
+    logits = torch.full((CFG["vocab"],), float("nan"), device=dev)
+    bar = 1e-5 if xd == "f32" else 2e-2
+    worst = 0.0
+    for pos, tok in enumerate(TOKENS):
+        model.forward(tok, pos, logits)
+        torch.cuda.synchronize()
+        want = oracle.forward(tok, pos)
+        err = rel_l2(logits.cpu().numpy(), want)
+        worst = max(worst, err)
+        print(f"head {head_kind} x {xd} pos {pos} token {tok}: logits relL2 {err:.2e}")
+        assert err <= bar
+    if xd == "f32":
+        # the KV cache rows, copied out of the model's buffer device to device
+        import ctypes
+        hip = ctypes.CDLL("libamdhip64.so")
+        kvd = CFG["kv_heads"] * CFG["head_dim"]
+        n = len(TOKENS)
+        for li in range(CFG["layers"]):
+            for ptr, want in zip(model.kv(li), (oracle.kv_k[li], oracle.kv_v[li])):
+                buf = torch.empty((n, kvd), dtype=torch.float32, device=dev)
+                assert hip.hipMemcpy(ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(ptr),
+                                     ctypes.c_size_t(n * kvd * 4), ctypes.c_int(3)) == 0   # device to device
+                err = rel_l2(buf.cpu().numpy(), want[:n])
+                print(f"layer {li} cache relL2 {err:.2e}")
+                assert err <= 1e-5, li
+    print(f"head {head_kind} x {xd}: worst relL2 {worst:.2e}")
+
+
+def test_forward_refusals(sm, ref, dev):
+    import torch
+    model, _ = build(sm, ref, dev, "q8_0", sm.X_F32)
+    logits = torch.zeros(CFG["vocab"], device=dev)
+    with pytest.raises(sm.SparkmvError):
+        model.forward(CFG["vocab"], 0, logits)
+    assert "outside the vocabulary" in sm.last_error()
+    with pytest.raises(sm.SparkmvError):
+        model.forward(1, CFG["max_ctx"], logits)
+    assert "exceeds" in sm.last_error()
+    bad = sm.ModelCfg(**dict(CFG, heads=3, x_dtype=sm.X_F32, dim=4, nc=4096, nstages=2, v3=1))
+    import ctypes
+    assert not sm.lib().sparkmv_model_create(ctypes.byref(bad))
+    assert "multiple of kv_heads" in sm.last_error()
