@@ -7,9 +7,8 @@ that is Q8_0 blocks or a VQ container. Tokens run past the window.
 
 Bars: with f32 activations into the matvecs (the reference's arithmetic) the
 logits of every step meet 1e-5 relative L2 (measured 7e-7) and the KV cache
-1e-5. With bf16
-activations (rounded at each matvec's input, as the decode benchmark runs)
-the logits meet 2e-2 (measured 6e-3).
+1e-5. With bf16 activations (rounded at each matvec's input, as the decode
+benchmark runs) the logits meet 2e-2 (measured 6e-3).
 """
 import numpy as np
 import pytest
