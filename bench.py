@@ -13,7 +13,7 @@ replayed as one HIP graph (native plan, sparkmv_plan_*). Weights and inputs
 are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--mode graph|eager]
-                    [--workload decode-set|ffn-up|q6k-down|verify8|prefill512]
+                    [--workload decode-set|ffn-up|q6k-down|verify8|prefill512|forward]
 
 Prints one JSON line (rank 0). The metric is time per token (lower is
 better); achieved GB/s over the algorithmic bytes (container + bf16 x + f32 y
@@ -222,6 +222,109 @@ def bench_decode_set(args, sm, torch, dev):
     return out
 
 
+FW_WINDOW = 512   # sliding_window; 9 of the 36 layers are full attention (every fourth)
+
+
+def bench_forward(args, sm, torch, dev):
+    """The whole decode token on the GPU (sparkmv_model_forward): embedding
+    row, 36 layers of norm / qkv + head gate / rope + KV store / attention /
+    out / norm / gate + up / gelu / down, final norm, Q8_0 tied head. The
+    cache is first filled with `context` tokens (untimed); then each step is
+    one token at the next position, replayed as one HIP graph."""
+    P = args.context
+    max_ctx = P + args.warmup + args.steps + 8
+    cfg = dict(hidden=HIDDEN, layers=LAYERS, heads=NHEAD, kv_heads=KVD // (QD // NHEAD), head_dim=QD // NHEAD,
+               intermediate=FFN, vocab=args.head_rows, eps=1e-6, sliding_window=FW_WINDOW, rope_full_theta=5.0e6,
+               rope_full_partial=0.25, rope_slide_theta=1.0e4, rope_slide_partial=1.0, max_ctx=max_ctx,
+               x_dtype=sm.X_BF16, dim=VQ["dim"], nc=VQ["nc"], nstages=VQ["nstages"], v3=VQ["v3"])
+    shapes = [("qkv", QD + 2 * KVD, HIDDEN), ("attn_gate", NHEAD, HIDDEN), ("out", HIDDEN, QD),
+              ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN)]
+    t0 = time.time()
+    rng = np.random.default_rng(5)
+
+    def gen(l):
+        return [sm.synth_container(seed_of(l, 20 + i), r, c, VQ["dim"], VQ["nc"], VQ["nstages"], VQ["v3"])
+                for i, (_, r, c) in enumerate(shapes)]
+
+    layers, mat_bytes = [], 0
+    with concurrent.futures.ThreadPoolExecutor(min(16, os.cpu_count() or 4)) as ex:
+        futs = [ex.submit(gen, l) for l in range(LAYERS)]
+        head = sm.synth_q8_0(0x4EAD, args.head_rows, HIDDEN)
+        for l, f in enumerate(futs):
+            hosts = f.result()
+            L = {name: sm.DeviceContainer(h, dev) for (name, _, _), h in zip(shapes, hosts)}
+            mat_bytes += sum(h.nbytes for h in hosts)
+            for name in ("in_norm", "post_norm"):
+                L[name] = torch.from_numpy((1 + 0.1 * rng.standard_normal(HIDDEN)).astype(np.float32)).to(dev)
+            L["full"] = l % 4 == 3
+            layers.append(L)
+    norm = torch.from_numpy((1 + 0.1 * rng.standard_normal(HIDDEN)).astype(np.float32)).to(dev)
+    model = sm.Model(cfg, layers, torch.from_numpy(head).to(dev), norm)
+    log(f"generated and uploaded the model in {time.time() - t0:.1f} s")
+    stream = torch.cuda.Stream(device=dev)
+    logits = torch.zeros(args.head_rows, device=dev)
+    toks = np.random.default_rng(6).integers(0, args.head_rows, size=max_ctx)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t0 = time.time()
+        for p in range(P):
+            model.forward(int(toks[p]), p, logits, stream)
+        torch.cuda.synchronize()
+        log(f"filled {P} positions of the cache in {time.time() - t0:.1f} s")
+        a, b = ev(), ev()
+        a.record(stream)
+        for p in range(P, P + 4):
+            model.forward(int(toks[p]), p, logits, stream)
+        b.record(stream)
+        torch.cuda.synchronize()
+        eager_us = a.elapsed_time(b) / 4 * 1e3
+        model.capture(logits, stream)
+        pos = P + 4
+        for _ in range(args.warmup):
+            model.replay(int(toks[pos]), pos, stream)
+            pos += 1
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record(stream)
+        for _ in range(args.steps):
+            model.replay(int(toks[pos]), pos, stream)
+            pos += 1
+        b.record(stream)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    assert bool(torch.isfinite(logits).all()), "non-finite logits"
+    kvd = KVD
+    n_full = sum(1 for L in layers if L["full"])
+    mid = P + 4 + args.warmup + args.steps // 2
+    kv_bytes = (n_full * mid + (LAYERS - n_full) * min(FW_WINDOW, mid)) * kvd * 4 * 2
+    total = mat_bytes + head.nbytes + kv_bytes
+    log(f"  step {ms * 1e3:.1f} us (graph), {eager_us:.1f} us eager; context {P}; "
+        f"{total / (ms * 1e-3) / 1e9:.1f} GB/s over weights + KV")
+    return {
+        "metric": "decode forward us/token (whole model: embedding, 36 layers, tied Q8_0 head)",
+        "value": round(ms * 1e3, 2),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16xf16->f32 matvecs (bf16 x), f32 elementwise, f64 norm sums",
+        "data": "synthetic (seeded, random-init weights of the real shapes)",
+        "config": {"workload": "decode forward, one token per step at context " + str(P), "layers": LAYERS,
+                   "hidden": HIDDEN, "ffn": FFN, "heads": NHEAD, "kv_heads": cfg["kv_heads"],
+                   "head_dim": cfg["head_dim"], "sliding_window": FW_WINDOW, "full_layers": n_full,
+                   "vq": "dim 4, nc 4096, 2 stages, DQV3 12-bit", "head": f"Q8_0 {args.head_rows}x{HIDDEN}",
+                   "mode": "graph (token and position in device memory)"},
+        "eager_us_per_token": round(eager_us, 1),
+        "bytes_per_token": int(total),
+        "achieved_gbps": round(total / (ms * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(total / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
+    }
+
+
 def recorded_traffic(ncol):
     """HBM bytes per VQ launch measured by rocprofv3 --pmc (FETCH_SIZE and
     WRITE_SIZE in separate runs, each scaled by the same counter's reading
@@ -374,7 +477,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--workload", default="decode-set",
-                    choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512"])
+                    choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512", "forward"])
+    ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -403,6 +507,8 @@ def main():
             log(f"cpu baseline took {time.time() - t:.1f} s")
     elif args.workload == "prefill512":
         out = bench_prefill(args, sm, torch, dev)
+    elif args.workload == "forward":
+        out = bench_forward(args, sm, torch, dev)
     else:
         out = bench_single(args, sm, torch, dev)
     out["device"] = name

@@ -266,7 +266,7 @@ typedef struct {
     int sliding_window;                          /* positions a sliding layer sees */
     double rope_full_theta, rope_full_partial;   /* config.rs:87-108 */
     double rope_slide_theta, rope_slide_partial;
-    int max_ctx;                                 /* KV cache positions, at most 38400 */
+    int max_ctx;                                 /* KV cache positions, at most 262144 */
     int x_dtype;
     int dim, nc, nstages, v3;                    /* the VQ geometry of every matrix */
 } sparkmv_model_cfg;
@@ -290,6 +290,14 @@ int sparkmv_model_set_head(void * model, int kind, const void * const * stages, 
 /* One token at pos (model.rs:441): fills the cache row pos of every layer
  * and writes vocab f32 logits. Asynchronous on stream. */
 int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits, void * stream);
+/* Record one token's launches as a HIP graph that writes logits, on a
+ * created (non-null) stream; token and position are read from device memory
+ * the replay sets. Run sparkmv_model_forward once first (first-call setup
+ * stays outside the capture). No launch in the graph clears memory with a
+ * memset. */
+int sparkmv_model_capture(void * model, float * logits, void * stream);
+/* Set token and position, then replay the recorded graph (as forward). */
+int sparkmv_model_replay(void * model, uint32_t token, int pos, void * stream);
 /* The device rows of layer's K and V cache ([max_ctx][kv_dim] f32 each). */
 int sparkmv_model_kv(void * model, int layer, float ** k, float ** v);
 

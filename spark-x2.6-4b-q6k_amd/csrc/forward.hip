@@ -24,6 +24,13 @@
  * KV store are one launch, and the norms and activations write the
  * matvecs' input in the form they read (f32, or bf16 when the model runs its
  * matvecs on bf16 activations). Activations stay f32 between kernels.
+ *
+ * The token and position live in device memory (two ints the chain's first
+ * launch sets), and every kernel that depends on them reads them there: the
+ * embedding row, rope and the KV row, the attention window. The chain's
+ * launches are then the same for every token, so it is recorded once as a
+ * HIP graph and replayed per token (sparkmv_model_capture / _replay); each
+ * attention launch reserves LDS for its longest window.
  */
 #include "kq.h"
 #include "vq.h"
@@ -50,111 +57,231 @@ __global__ void fw_fill_kernel(float * p, int n, float v) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x) p[i] = v;
 }
 
+/* st[0] = token, st[1] = position, and the position's rope tables for the
+ * full and the sliding layers (model.rs:416-428, f32): tab[r][0][i] = cos,
+ * tab[r][1][i] = sin of pos * theta_r^(-2i / pdim_r), i < pdim_r / 2 <= 128. */
+__global__ void fw_set_state_kernel(int * st, int token, int pos, float theta0, int pdim0, float theta1, int pdim1,
+                                    float * tab) {
+    const int i = threadIdx.x;
+    if (i == 0) {
+        st[0] = token;
+        st[1] = pos;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const float theta = r ? theta1 : theta0;
+        const int pdim = r ? pdim1 : pdim0;
+        if (i < pdim / 2) {
+            const float freq = 1.0f / powf(theta, (float) (2 * i) / (float) pdim);
+            const float a = (float) pos * freq;
+            tab[r * 256 + i] = cosf(a);
+            tab[r * 256 + 128 + i] = sinf(a);
+        }
+    }
+}
+
+/* The embedding row of a Q8_0 tied head: row st[0], d * q exactly. */
+__global__ void fw_q8_0_row_kernel(const uint8_t * blocks, int cols, const int * st, float * out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= cols) return;
+    const uint8_t * b = blocks + ((size_t) st[0] * (cols >> 5) + (i >> 5)) * 34;
+    _Float16 d;
+    __builtin_memcpy(&d, b, 2);
+    out[i] = (float) d * (float) (int8_t) b[2 + (i & 31)];
+}
+
 /* out = x * inv * w with inv = 1 / sqrt(mean(x^2) + eps), the sum of squares in
  * f64 and inv rounded once to f32 (model.rs:236-245). One workgroup. */
+template <int PER>
 __global__ __launch_bounds__(256) void fw_rmsnorm_kernel(const float * x, const float * w, float * out,
                                                          uint16_t * out16, int n, float eps) {
     __shared__ double part[4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    double s = 0.0;
-    for (int i = t; i < n; i += 256) {
-        const double v = (double) x[i];
-        s += v * v;
+    /* x and w of this thread's elements requested together: one memory
+     * round trip before the reduction */
+    float xv[PER], wv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = t + 256 * k;
+        xv[k] = i < n ? x[i] : 0.0f;
+        wv[k] = i < n ? w[i] : 0.0f;
     }
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; k++) s += (double) xv[k] * (double) xv[k];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
     if (lane == 0) part[wave] = s;
     __syncthreads();
     const double tot = (part[0] + part[1]) + (part[2] + part[3]);
     const float inv = (float) (1.0 / sqrt(tot / (double) n + (double) eps));
-    for (int i = t; i < n; i += 256) {
-        const float v = x[i] * inv * w[i];
-        if (out) out[i] = v;
-        if (out16) out16[i] = fw_bf16(v);
-    }
-}
-
-/* Rope and the KV store in one launch. Items [0, (heads + kv_heads) * half)
- * rotate the pair (i, i + half) of one q or k head over its first pdim
- * elements with the f32 table of model.rs:416-428 (apply_rope, :430-438); a
- * rotated k pair also goes to the cache. Items [0, kvd) store v[item] and
- * the k elements past pdim, which rope leaves alone. */
-__global__ void fw_rope_kv_kernel(float * qkv, int qd, int kvd, int heads, int kv_heads, int hd, int pdim,
-                                  float theta, int pos, float * kc, float * vc) {
-    const int half = pdim / 2;
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < (heads + kv_heads) * half) {
-        const int h = t / half, i = t - h * half;
-        const float freq = 1.0f / powf(theta, (float) (2 * i) / (float) pdim);
-        const float a = (float) pos * freq;
-        const float c = cosf(a), s = sinf(a);
-        float * base = h < heads ? qkv + (size_t) h * hd : qkv + qd + (size_t) (h - heads) * hd;
-        const float x0 = base[i], x1 = base[i + half];
-        const float r0 = x0 * c - x1 * s, r1 = x1 * c + x0 * s;
-        base[i] = r0;
-        base[i + half] = r1;
-        if (h >= heads) {
-            float * k = kc + (size_t) pos * kvd + (size_t) (h - heads) * hd;
-            k[i] = r0;
-            k[i + half] = r1;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = t + 256 * k;
+        if (i < n) {
+            const float v = xv[k] * inv * wv[k];
+            if (out) out[i] = v;
+            if (out16) out16[i] = fw_bf16(v);
         }
     }
-    if (t < kvd) {
-        vc[(size_t) pos * kvd + t] = qkv[qd + kvd + t];
-        if (t % hd >= 2 * half) kc[(size_t) pos * kvd + t] = qkv[qd + t];
+}
+
+/* Rope, the KV store and attention over the layer's window of the cache,
+ * positions start .. pos (model.rs:484-557; window 0: every position), split
+ * by positions so that a long window keeps many CUs busy:
+ *
+ *   fw_attn_part_kernel: workgroup (chunk, kv head), one wave per query head
+ *     of the kv head's group, kAttnChunk positions. Each lane holds VPL
+ *     consecutive elements of a head. The wave rotates its query head in
+ *     registers (rope over the first pdim elements with the position's f32
+ *     table, model.rs:416-428, which the state kernel computes once per token
+ *     for each layer type; the pair partner of element e is e +- pdim/2, in the
+ *     lane pdim/2/VPL away, fetched with a lane permute). The chunk holding
+ *     pos rotates the new key the same way, uses it and the new value from
+ *     registers, and its first wave stores both in the cache (model.rs:
+ *     498-503); other chunks read only older rows. A score is a lane-local dot
+ *     and a butterfly; the wave keeps its chunk's maximum m, sum
+ *     l = sum_j e^(s_j - m) and unnormalized o = sum_j e^(s_j - m) V[j].
+ *   fw_attn_combine_kernel: workgroup per query head; rescales the chunks to
+ *     the overall maximum M, divides by L = sum_c l_c e^(m_c - M) and applies
+ *     the head's sigmoid gate. Its four waves take every fourth chunk.
+ *
+ * That is the CPU's softmax with the sum regrouped by chunk. Launch shapes
+ * are fixed (the longest window), so a captured graph serves every position:
+ * chunks past the current window do nothing. */
+constexpr int kAttnChunk = 16;
+
+template <int VPL>
+__global__ __launch_bounds__(256) void fw_attn_part_kernel(const float * qkv, int qd, int kvd, float * kc, float * vc,
+                                                            const int * st, int window, int heads, int kv_heads,
+                                                            int pdim, const float * rtab, float scale, int nch_max,
+                                                            float * part) {
+    constexpr int hd = 64 * VPL, C = kAttnChunk;
+    typedef float fv __attribute__((ext_vector_type(VPL)));
+    const int pos = st[1];
+    const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
+    const int n = pos + 1 - start;
+    const int chunk = blockIdx.x, kvh = blockIdx.y;
+    const int G = heads / kv_heads;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int j0 = chunk * C;
+    if (j0 >= n) return;                        /* uniform: the combine reads chunks < ceil(n / chunk) */
+    const int jn = min(C, n - j0);
+    const int h = kvh * G + wave;               /* h * kv_heads / heads == kvh */
+    const int half = pdim / 2;                  /* a multiple of VPL (the host checks) */
+    /* x rotated by position pos: element e < half pairs with e + half,
+     * e in [half, pdim) with e - half (apply_rope, model.rs:430-438) */
+    auto rope = [&](fv x) -> fv {
+        const int e0 = lane * VPL;
+        const int pl = e0 < half ? lane + half / VPL : (e0 < pdim ? lane - half / VPL : lane);
+        fv p, r = x;
+#pragma unroll
+        for (int v = 0; v < VPL; v++) p[v] = __shfl(x[v], pl, 64);
+#pragma unroll
+        for (int v = 0; v < VPL; v++) {
+            const int e = e0 + v;
+            if (e < 2 * half) {
+                const int i = e < half ? e : e - half;
+                const float c = rtab[i], sn = rtab[128 + i];
+                r[v] = e < half ? x[v] * c - p[v] * sn : x[v] * c + p[v] * sn;
+            }
+        }
+        return r;
+    };
+    const fv q = rope(*(const fv *) (qkv + (size_t) h * hd + lane * VPL));
+    const float * kb = kc + (size_t) (start + j0) * kvd + (size_t) kvh * hd + lane * VPL;
+    const float * vb = vc + (size_t) (start + j0) * kvd + (size_t) kvh * hd + lane * VPL;
+    /* every K and V row of the chunk requested at once (rows past the
+     * window re-read the last one and get weight zero) */
+    fv kr[C], vr[C];
+#pragma unroll
+    for (int j = 0; j < C; j++) kr[j] = *(const fv *) (kb + (size_t) min(j, jn - 1) * kvd);
+#pragma unroll
+    for (int j = 0; j < C; j++) vr[j] = *(const fv *) (vb + (size_t) min(j, jn - 1) * kvd);
+    if (j0 + jn == n) {
+        /* this chunk ends at pos: the new key and value, from qkv */
+        const fv kn = rope(*(const fv *) (qkv + qd + (size_t) kvh * hd + lane * VPL));
+        const fv vn = *(const fv *) (qkv + qd + kvd + (size_t) kvh * hd + lane * VPL);
+#pragma unroll
+        for (int j = 0; j < C; j++)
+            if (j == jn - 1) { kr[j] = kn; vr[j] = vn; }
+        if (wave == 0) {
+            *(fv *) (kc + (size_t) pos * kvd + (size_t) kvh * hd + lane * VPL) = kn;
+            *(fv *) (vc + (size_t) pos * kvd + (size_t) kvh * hd + lane * VPL) = vn;
+        }
+    }
+    float sc[C];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int v = 0; v < VPL; v++) s += q[v] * kr[j][v];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        sc[j] = s * scale;
+        if (j < jn) m = fmaxf(m, sc[j]);
+    }
+    float l = 0.0f;
+    fv o = (fv) 0.0f;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        const float e = j < jn ? expf(sc[j] - m) : 0.0f;
+        l += e;
+        o += e * vr[j];
+    }
+    float * P = part + ((size_t) h * nch_max + chunk) * (hd + 2);
+    *(fv *) (P + lane * VPL) = o;
+    if (lane == 0) {
+        P[hd] = m;
+        P[hd + 1] = l;
     }
 }
 
-/* One workgroup (4 waves) per query head over positions start .. start+n-1 of
- * the cache (model.rs:508-557). Scores: wave w takes positions w, w+4, ...,
- * its lanes split the head's elements and meet in a butterfly. Softmax with
- * the running max, then thread d sums p_j * V[j][d] in position order and
- * applies the head's sigmoid gate. The scores sit in LDS (n floats). */
-__global__ __launch_bounds__(256) void fw_attn_kernel(const float * qkv, int qd, int kvd, const float * gate,
-                                                      const float * kc, const float * vc, int start, int n, int heads,
-                                                      int kv_heads, int hd, float scale, float * out,
-                                                      uint16_t * out16) {
-    extern __shared__ float sc[];
+template <int VPL>
+__global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part, const float * gate, const int * st,
+                                                              int window, int nch_max, float * out, uint16_t * out16) {
+    constexpr int hd = 64 * VPL;
+    typedef float fv __attribute__((ext_vector_type(VPL)));
+    extern __shared__ float wts[];             /* e^(m_c - M) per chunk */
     __shared__ float red[8];
+    __shared__ fv acc[4][64];
+    const int pos = st[1];
+    const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
+    const int nch = (pos + 1 - start + kAttnChunk - 1) / kAttnChunk;
     const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int kvh = h * kv_heads / heads;
-    const float * q = qkv + (size_t) h * hd;
-    const float * kb = kc + (size_t) start * kvd + (size_t) kvh * hd;
-    for (int j = wave; j < n; j += 4) {
-        const float * k = kb + (size_t) j * kvd;
-        float s = 0.0f;
-        for (int d = lane; d < hd; d += 64) s += q[d] * k[d];
+    const float * P = part + (size_t) h * nch_max * (hd + 2);
+    float M = -INFINITY;
+    for (int c = t; c < nch; c += 256) M = fmaxf(M, P[(size_t) c * (hd + 2) + hd]);
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-        if (lane == 0) sc[j] = s * scale;
-    }
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) red[wave] = M;
     __syncthreads();
-    float mx = -INFINITY;
-    for (int j = t; j < n; j += 256) mx = fmaxf(mx, sc[j]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sum = 0.0f;
-    for (int j = t; j < n; j += 256) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float L = 0.0f;
+    for (int c = t; c < nch; c += 256) {
+        const float w = expf(P[(size_t) c * (hd + 2) + hd] - M);
+        wts[c] = w;
+        L += w * P[(size_t) c * (hd + 2) + hd + 1];
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    if (lane == 0) red[4 + wave] = sum;
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    if (lane == 0) red[4 + wave] = L;
     __syncthreads();
-    const float inv = 1.0f / ((red[4] + red[5]) + (red[6] + red[7]));
-    const float g = 1.0f / (1.0f + expf(-gate[h]));
-    const float * vb = vc + (size_t) start * kvd + (size_t) kvh * hd;
-    for (int d = t; d < hd; d += 256) {
-        float o = 0.0f;
-        for (int j = 0; j < n; j++) o += sc[j] * inv * vb[(size_t) j * kvd + d];
-        const float r = o * g;
-        out[(size_t) h * hd + d] = r;
-        if (out16) out16[(size_t) h * hd + d] = fw_bf16(r);
+    /* wave w sums chunks w, w + 4, ... over the lane's VPL elements */
+    fv o = (fv) 0.0f;
+    for (int c = wave; c < nch; c += 4) o += wts[c] * *(const fv *) (P + (size_t) c * (hd + 2) + lane * VPL);
+    acc[wave][lane] = o;
+    __syncthreads();
+    if (wave == 0) {
+        const float inv = 1.0f / ((red[4] + red[5]) + (red[6] + red[7]));
+        const float g = 1.0f / (1.0f + expf(-gate[h]));
+        const fv r = ((acc[0][lane] + acc[1][lane]) + (acc[2][lane] + acc[3][lane])) * inv * g;
+#pragma unroll
+        for (int v = 0; v < VPL; v++) {
+            out[(size_t) h * hd + lane * VPL + v] = r[v];
+            if (out16) out16[(size_t) h * hd + lane * VPL + v] = fw_bf16(r[v]);
+        }
     }
 }
 
@@ -186,9 +313,22 @@ struct Model {
     void * mem = nullptr;
     float * h, * xn, * qkv, * g, * attn, * mg, * mu, * act, * kv;
     uint16_t * xn16, * attn16, * act16;
+    int * st;                            /* token, position */
+    float * part;                        /* attention partials [heads][nch_max][head_dim + 2] */
+    float * rtab;                        /* rope tables [full, sliding][cos, sin][128] */
+    int nch_max;
+    /* the recorded chain */
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t) 255; }
+
+/* the rotated prefix of a head: (head_dim * partial) as usize, at most head_dim (model.rs:419) */
+int rope_dim(int hd, double partial) {
+    const int d = (int) ((float) hd * (float) partial);
+    return d > hd ? hd : d;
+}
 
 int check_launch(const char * what) {
     hipError_t e = hipGetLastError();
@@ -229,8 +369,12 @@ int gemv2(const Model & m, const void * const * st0, int rows0, float * y0, cons
 
 int rmsnorm(const Model & m, const float * x, const float * w, hipStream_t s) {
     const bool b16 = m.c.x_dtype == SPARKMV_X_BF16;
-    hipLaunchKernelGGL(fw_rmsnorm_kernel, dim3(1), dim3(256), 0, s, x, w, m.xn, b16 ? m.xn16 : nullptr,
-                       m.c.hidden, m.c.eps);
+    const int per = (m.c.hidden + 255) / 256;
+    uint16_t * o16 = b16 ? m.xn16 : nullptr;
+    if (per <= 4) hipLaunchKernelGGL(fw_rmsnorm_kernel<4>, dim3(1), dim3(256), 0, s, x, w, m.xn, o16, m.c.hidden, m.c.eps);
+    else if (per <= 12) hipLaunchKernelGGL(fw_rmsnorm_kernel<12>, dim3(1), dim3(256), 0, s, x, w, m.xn, o16, m.c.hidden, m.c.eps);
+    else if (per <= 32) hipLaunchKernelGGL(fw_rmsnorm_kernel<32>, dim3(1), dim3(256), 0, s, x, w, m.xn, o16, m.c.hidden, m.c.eps);
+    else { set_error("hidden %d is above 8192", m.c.hidden); return -1; }
     return check_launch("rms norm launch");
 }
 
@@ -255,14 +399,22 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     if (c.x_dtype != SPARKMV_X_F32 && c.x_dtype != SPARKMV_X_BF16) { set_error("unknown x dtype %d", c.x_dtype); return nullptr; }
     if (c.nstages < 1 || c.nstages > 4) { set_error("stage count %d is outside 1..4", c.nstages); return nullptr; }
     if (!(c.eps > 0.0f)) { set_error("eps must be positive"); return nullptr; }
-    /* the attention kernel keeps one score per position in LDS */
-    const long span = (long) c.max_ctx;
-    if (span * 4 > 150 * 1024) { set_error("max_ctx %d needs more than 150 KB of attention scores", c.max_ctx); return nullptr; }
-    if (span * 4 > 65536) {
-        hipError_t e = hipFuncSetAttribute((const void *) fw_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int) (span * 4));
-        if (e != hipSuccess) { fail_hip("LDS opt-in for the attention kernel", e); return nullptr; }
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) {
+        set_error("head_dim %d is not 64, 128 or 256", c.head_dim);
+        return nullptr;
     }
+    if (c.heads / c.kv_heads > 4) { set_error("more than 4 query heads per kv head"); return nullptr; }
+    for (double partial : {c.rope_full_partial, c.rope_slide_partial}) {
+        const int half = rope_dim(c.head_dim, partial) / 2;
+        if (half % (c.head_dim / 64)) {
+            set_error("rope half-width %d is not a multiple of head_dim / 64", half);
+            return nullptr;
+        }
+    }
+    /* the combine keeps one weight per position chunk in LDS */
+    const long nch_max = ((long) c.max_ctx + kAttnChunk - 1) / kAttnChunk;
+    if (nch_max * 4 > 65536) { set_error("max_ctx %d is above %d", c.max_ctx, 16384 * kAttnChunk); return nullptr; }
+    if (c.hidden > 8192) { set_error("hidden %d is above 8192", c.hidden); return nullptr; }
     Model * m = new Model;
     m->c = c;
     m->layers.resize(c.layers);
@@ -275,6 +427,9 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     const size_t o_mu = take(c.intermediate * 4), o_act = take(c.intermediate * 4);
     const size_t o_xn16 = take(c.hidden * 2), o_attn16 = take(qd * 2), o_act16 = take(c.intermediate * 2);
     const size_t o_kv = take((size_t) c.layers * c.max_ctx * kvd * 4 * 2);
+    const size_t o_st = take(2 * sizeof(int));
+    const size_t o_part = take((size_t) c.heads * nch_max * (c.head_dim + 2) * 4);
+    const size_t o_rtab = take(512 * 4);
     hipError_t e = hipMalloc(&m->mem, off);
     if (e != hipSuccess) {
         fail_hip("model buffers", e);
@@ -287,12 +442,18 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     m->mu = (float *) (b + o_mu); m->act = (float *) (b + o_act);
     m->xn16 = (uint16_t *) (b + o_xn16); m->attn16 = (uint16_t *) (b + o_attn16); m->act16 = (uint16_t *) (b + o_act16);
     m->kv = (float *) (b + o_kv);
+    m->st = (int *) (b + o_st);
+    m->part = (float *) (b + o_part);
+    m->rtab = (float *) (b + o_rtab);
+    m->nch_max = (int) nch_max;
     return m;
 }
 
 void sparkmv_model_destroy(void * model) {
     Model * m = (Model *) model;
     if (!m) return;
+    if (m->exec) (void) hipGraphExecDestroy(m->exec);
+    if (m->graph) (void) hipGraphDestroy(m->graph);
     if (m->mem) (void) hipFree(m->mem);
     delete m;
 }
@@ -334,16 +495,34 @@ int sparkmv_model_set_head(void * model, int kind, const void * const * stages, 
     return 0;
 }
 
-int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits, void * stream) {
-    Model * m = (Model *) model;
-    if (!m || !logits) { set_error("model or logits is null"); return -1; }
-    const sparkmv_model_cfg & c = m->c;
-    if ((long) token >= c.vocab) { set_error("token %u is outside the vocabulary", token); return -1; }
-    if (pos < 0 || pos >= c.max_ctx) { set_error("position %d exceeds the %d-token cache", pos, c.max_ctx); return -1; }
+}  // extern "C"
+
+namespace {
+
+int ready(const Model * m) {
     if (m->head_kind < 0) { set_error("the model has no head"); return -1; }
-    for (int li = 0; li < c.layers; li++)
+    for (int li = 0; li < m->c.layers; li++)
         if (!m->layer_set[li]) { set_error("layer %d has no weights", li); return -1; }
-    hipStream_t s = (hipStream_t) stream;
+    return 0;
+}
+
+int check_step(const Model * m, uint32_t token, int pos) {
+    if ((long) token >= m->c.vocab) { set_error("token %u is outside the vocabulary", token); return -1; }
+    if (pos < 0 || pos >= m->c.max_ctx) { set_error("position %d exceeds the %d-token cache", pos, m->c.max_ctx); return -1; }
+    return 0;
+}
+
+int set_state(Model * m, uint32_t token, int pos, hipStream_t s) {
+    const sparkmv_model_cfg & c = m->c;
+    hipLaunchKernelGGL(fw_set_state_kernel, dim3(1), dim3(128), 0, s, m->st, (int) token, pos,
+                       (float) c.rope_full_theta, rope_dim(c.head_dim, c.rope_full_partial), (float) c.rope_slide_theta,
+                       rope_dim(c.head_dim, c.rope_slide_partial), m->rtab);
+    return check_launch("state launch");
+}
+
+/* Every launch of one token, reading token and position from m->st. */
+int chain(Model * m, float * logits, hipStream_t s) {
+    const sparkmv_model_cfg & c = m->c;
     const bool b16 = c.x_dtype == SPARKMV_X_BF16;
     const int qd = c.heads * c.head_dim, kvd = c.kv_heads * c.head_dim, hd = c.head_dim;
 
@@ -353,11 +532,11 @@ int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits,
         if (check_launch("fill launch")) return -1;
         const Layout L = make_layout(c.dim, c.nc, c.vocab, c.hidden, c.v3);
         for (int st = 0; st < c.nstages; st++)
-            if (vq_row_dequant_launch(m->head_stages[st], L, (int) token, m->h, s)) return -1;
+            if (vq_row_dequant_dev_launch(m->head_stages[st], L, m->st, m->h, s)) return -1;
     } else {
-        const size_t rowbytes = (size_t) (c.hidden / 32) * 34;
-        if (kq_dequant_launch(8, (const uint8_t *) m->head_blocks + (size_t) token * rowbytes, 1, c.hidden, m->h, s))
-            return -1;
+        hipLaunchKernelGGL(fw_q8_0_row_kernel, dim3((c.hidden + 255) / 256), dim3(256), 0, s,
+                           (const uint8_t *) m->head_blocks, c.hidden, (const int *) m->st, m->h);
+        if (check_launch("embedding launch")) return -1;
     }
 
     const float scale = 1.0f / sqrtf((float) hd);
@@ -371,21 +550,27 @@ int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits,
         const void * xin = b16 ? (const void *) m->xn16 : (const void *) m->xn;
         if (gemv2(*m, L.qkv, qd + 2 * kvd, m->qkv, L.attn_gate, c.heads, m->g, c.hidden, xin, s)) return -1;
 
-        /* rope and the KV store (model.rs:484-503) */
-        const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
-        const double partial = full ? c.rope_full_partial : c.rope_slide_partial;
-        int pdim = (int) ((float) hd * (float) partial);
-        if (pdim > hd) pdim = hd;
-        const int items = (c.heads + c.kv_heads) * (pdim / 2) > kvd ? (c.heads + c.kv_heads) * (pdim / 2) : kvd;
-        hipLaunchKernelGGL(fw_rope_kv_kernel, dim3((items + 255) / 256), dim3(256), 0, s, m->qkv, qd, kvd, c.heads,
-                           c.kv_heads, hd, pdim, (float) theta, pos, kc, vc);
-        if (check_launch("rope launch")) return -1;
-
-        /* attention over the layer's window (model.rs:508-557) */
-        const int start = full ? 0 : (pos + 1 > c.sliding_window ? pos + 1 - c.sliding_window : 0);
-        const int n = pos + 1 - start;
-        hipLaunchKernelGGL(fw_attn_kernel, dim3(c.heads), dim3(256), (uint32_t) (n * 4), s, m->qkv, qd, kvd, m->g, kc,
-                           vc, start, n, c.heads, c.kv_heads, hd, scale, m->attn, b16 ? m->attn16 : nullptr);
+        /* rope, the KV store and attention (model.rs:484-557), launched for
+         * the longest window this layer can see */
+        const int pdim = rope_dim(hd, full ? c.rope_full_partial : c.rope_slide_partial);
+        const float * rtab = m->rtab + (full ? 0 : 256);
+        const int window = full ? 0 : c.sliding_window;
+        const int span = full || c.sliding_window > c.max_ctx ? c.max_ctx : c.sliding_window;
+        const int nch = (span + kAttnChunk - 1) / kAttnChunk;
+        const dim3 pg((unsigned) nch, (unsigned) c.kv_heads), pb((unsigned) (64 * (c.heads / c.kv_heads)));
+        const uint32_t wl = (uint32_t) (nch * 4);
+        uint16_t * a16 = b16 ? m->attn16 : nullptr;
+#define FW_ATTN(V)                                                                                                  \
+    do {                                                                                                            \
+        hipLaunchKernelGGL(fw_attn_part_kernel<V>, pg, pb, 0, s, m->qkv, qd, kvd, kc, vc, (const int *) m->st,        \
+                           window, c.heads, c.kv_heads, pdim, rtab, scale, m->nch_max, m->part);                    \
+        hipLaunchKernelGGL(fw_attn_combine_kernel<V>, dim3(c.heads), dim3(256), wl, s, m->part, m->g,               \
+                           (const int *) m->st, window, m->nch_max, m->attn, a16);                                  \
+    } while (0)
+        if (hd == 64) FW_ATTN(1);
+        else if (hd == 128) FW_ATTN(2);
+        else FW_ATTN(4);
+#undef FW_ATTN
         if (check_launch("attention launch")) return -1;
         if (gemv(*m, L.out, c.hidden, qd, b16 ? (const void *) m->attn16 : (const void *) m->attn, m->h, 1, s))
             return -1;
@@ -406,6 +591,53 @@ int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits,
     const void * xin = b16 ? (const void *) m->xn16 : (const void *) m->xn;
     if (m->head_kind == 0) return gemv(*m, m->head_stages, c.vocab, c.hidden, xin, logits, 0, s);
     return kq_gemv_launch(8, m->head_blocks, c.vocab, c.hidden, xin, b16 ? 0 : 1, c.hidden, 1, logits, c.vocab, 0, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits, void * stream) {
+    Model * m = (Model *) model;
+    if (!m || !logits) { set_error("model or logits is null"); return -1; }
+    if (check_step(m, token, pos) || ready(m)) return -1;
+    hipStream_t s = (hipStream_t) stream;
+    if (set_state(m, token, pos, s)) return -1;
+    return chain(m, logits, s);
+}
+
+int sparkmv_model_capture(void * model, float * logits, void * stream) {
+    Model * m = (Model *) model;
+    if (!m || !logits) { set_error("model or logits is null"); return -1; }
+    if (!stream) { set_error("capture needs a created stream, not the null stream"); return -1; }
+    if (ready(m)) return -1;
+    hipStream_t s = (hipStream_t) stream;
+    hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return fail_hip("begin capture", e);
+    const int rc = chain(m, logits, s);
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(s, &g);
+    if (rc) { if (g) hipGraphDestroy(g); return -1; }
+    if (e != hipSuccess) return fail_hip("end capture", e);
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) { hipGraphDestroy(g); return fail_hip("graph instantiate", e); }
+    if (m->exec) hipGraphExecDestroy(m->exec);
+    if (m->graph) hipGraphDestroy(m->graph);
+    m->graph = g;
+    m->exec = x;
+    return 0;
+}
+
+int sparkmv_model_replay(void * model, uint32_t token, int pos, void * stream) {
+    Model * m = (Model *) model;
+    if (!m) { set_error("model is null"); return -1; }
+    if (!m->exec) { set_error("the model has no recorded forward: call sparkmv_model_capture first"); return -1; }
+    if (check_step(m, token, pos)) return -1;
+    hipStream_t s = (hipStream_t) stream;
+    if (set_state(m, token, pos, s)) return -1;
+    hipError_t e = hipGraphLaunch(m->exec, s);
+    return e == hipSuccess ? 0 : fail_hip("graph launch", e);
 }
 
 /* The layer's KV cache rows (device pointers), for tests and inspection. */

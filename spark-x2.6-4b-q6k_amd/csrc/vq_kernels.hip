@@ -795,9 +795,12 @@ __global__ void vq_dequant_kernel(const uint8_t * p, const Layout L, float * out
         o[d] = __fadd_rn(accumulate ? o[d] : 0.0f, __fmul_rn(f16_to_f32(cb[(size_t) v * L.dim + d]), g));
 }
 
-__global__ void vq_row_dequant_kernel(const uint8_t * p, const Layout L, int row, float * out) {
+/* drow, when given, holds the row in device memory (a captured graph reads
+ * the token it is replayed for); rows past the matrix decode nothing. */
+__global__ void vq_row_dequant_kernel(const uint8_t * p, const Layout L, int row, const int * drow, float * out) {
     const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= L.nidx_row) return;
+    if (drow) row = *drow;
+    if (i >= L.nidx_row || row < 0 || row >= L.rows) return;
     const uint16_t * cb = (const uint16_t *) (p + L.cb_off);
     const float g = f16_to_f32(((const uint16_t *) (p + L.gain_off))[row]);
     const uint32_t v = rd_index(p + L.stream_off, L, (size_t) row, i);
@@ -1248,7 +1251,15 @@ int vq_dequant_launch(const void * payload, const Layout & L, float * out, int a
 int vq_row_dequant_launch(const void * payload, const Layout & L, int row, float * out, hipStream_t s) {
     const int threads = 256;
     hipLaunchKernelGGL(vq_row_dequant_kernel, dim3((unsigned) ((L.nidx_row + threads - 1) / threads)), dim3(threads),
-                       0, s, (const uint8_t *) payload, L, row, out);
+                       0, s, (const uint8_t *) payload, L, row, (const int *) nullptr, out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail_hip("row dequant launch", e);
+}
+
+int vq_row_dequant_dev_launch(const void * payload, const Layout & L, const int * drow, float * out, hipStream_t s) {
+    const int threads = 256;
+    hipLaunchKernelGGL(vq_row_dequant_kernel, dim3((unsigned) ((L.nidx_row + threads - 1) / threads)), dim3(threads),
+                       0, s, (const uint8_t *) payload, L, 0, drow, out);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("row dequant launch", e);
 }

@@ -137,6 +137,8 @@ SIGNATURES = {
     "sparkmv_model_set_layer": (_I, [_P, _I, ctypes.POINTER(ModelLayer)]),
     "sparkmv_model_set_head": (_I, [_P, _I, _PP, _P, _P]),
     "sparkmv_model_forward": (_I, [_P, ctypes.c_uint32, _I, _P, _P]),
+    "sparkmv_model_capture": (_I, [_P, _P, _P]),
+    "sparkmv_model_replay": (_I, [_P, ctypes.c_uint32, _I, _P]),
     "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
     "sparkmv_synth_container_bytes": (_S, [_I] * 6),
     "sparkmv_synth_vq_container": (_I, [_U64, _I, _I, _I, _I, _I, _I, _P, _S]),
@@ -508,6 +510,15 @@ class Model:
         """logits: device f32 [vocab]; asynchronous on stream."""
         check(lib().sparkmv_model_forward(self.h, int(token), int(pos), logits.data_ptr(), _stream_ptr(stream)),
               "model forward")
+
+    def capture(self, logits, stream):
+        """Record one token's launches as a HIP graph writing logits (run
+        forward once first); stream must be a created torch stream."""
+        check(lib().sparkmv_model_capture(self.h, logits.data_ptr(), _stream_ptr(stream)), "model capture")
+        self.keep.append(logits)
+
+    def replay(self, token, pos, stream):
+        check(lib().sparkmv_model_replay(self.h, int(token), int(pos), _stream_ptr(stream)), "model replay")
 
     def kv(self, layer):
         """(k, v) device pointers of the layer's cache, [max_ctx][kv_dim] f32 each."""

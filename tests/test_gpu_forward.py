@@ -115,3 +115,31 @@ def test_forward_refusals(sm, ref, dev):
     import ctypes
     assert not sm.lib().sparkmv_model_create(ctypes.byref(bad))
     assert "multiple of kv_heads" in sm.last_error()
+
+
+@pytest.mark.parametrize("head_kind", ["q8_0", "vq"])
+def test_forward_graph_replay(sm, ref, dev, head_kind):
+    """The forward recorded once as a HIP graph and replayed per token, with
+    eager forwards of the same model between replays (both write the KV
+    cache) and a synchronization and the oracle's step after each one."""
+    import torch
+    model, oracle = build(sm, ref, dev, head_kind, sm.X_F32)
+    stream = torch.cuda.Stream(device=dev)
+    logits = torch.full((CFG["vocab"],), float("nan"), device=dev)
+    with torch.cuda.stream(stream):
+        model.forward(TOKENS[0], 0, logits, stream)
+        stream.synchronize()
+        assert rel_l2(logits.cpu().numpy(), oracle.forward(TOKENS[0], 0)) <= 1e-5
+        model.capture(logits, stream)
+        for pos in range(1, len(TOKENS)):
+            tok = TOKENS[pos]
+            if pos % 3 == 2:
+                model.forward(tok, pos, logits, stream)
+            else:
+                model.replay(tok, pos, stream)
+            stream.synchronize()
+            err = rel_l2(logits.cpu().numpy(), oracle.forward(tok, pos))
+            print(f"head {head_kind} pos {pos} ({'eager' if pos % 3 == 2 else 'replay'}): relL2 {err:.2e}")
+            assert err <= 1e-5
+    with pytest.raises(sm.SparkmvError):
+        model.replay(1, CFG["max_ctx"], stream)
