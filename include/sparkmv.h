@@ -266,7 +266,7 @@ typedef struct {
     int sliding_window;                          /* positions a sliding layer sees */
     double rope_full_theta, rope_full_partial;   /* config.rs:87-108 */
     double rope_slide_theta, rope_slide_partial;
-    int max_ctx;                                 /* KV cache positions, at most 262144 */
+    int max_ctx;                                 /* KV cache positions, at most 131072 */
     int x_dtype;
     int dim, nc, nstages, v3;                    /* the VQ geometry of every matrix */
 } sparkmv_model_cfg;

@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part
                                                               int window, int nch_max, float * out, uint16_t * out16) {
     constexpr int hd = 64 * VPL;
     typedef float fv __attribute__((ext_vector_type(VPL)));
-    extern __shared__ float wts[];             /* e^(m_c - M) per chunk */
+    extern __shared__ float wts[];             /* per chunk: m_c, then e^(m_c - M); then l_c */
     __shared__ float red[8];
     __shared__ fv acc[4][64];
     const int pos = st[1];
@@ -251,8 +251,14 @@ __global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part
     const int nch = (pos + 1 - start + kAttnChunk - 1) / kAttnChunk;
     const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float * P = part + (size_t) h * nch_max * (hd + 2);
+    float * ls = wts + nch;
     float M = -INFINITY;
-    for (int c = t; c < nch; c += 256) M = fmaxf(M, P[(size_t) c * (hd + 2) + hd]);
+    for (int c = t; c < nch; c += 256) {
+        const float mc = P[(size_t) c * (hd + 2) + hd], lc = P[(size_t) c * (hd + 2) + hd + 1];
+        wts[c] = mc;
+        ls[c] = lc;
+        M = fmaxf(M, mc);
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
     if (lane == 0) red[wave] = M;
@@ -260,17 +266,28 @@ __global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part
     M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float L = 0.0f;
     for (int c = t; c < nch; c += 256) {
-        const float w = expf(P[(size_t) c * (hd + 2) + hd] - M);
+        const float w = expf(wts[c] - M);
         wts[c] = w;
-        L += w * P[(size_t) c * (hd + 2) + hd + 1];
+        L += w * ls[c];
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
     if (lane == 0) red[4 + wave] = L;
     __syncthreads();
-    /* wave w sums chunks w, w + 4, ... over the lane's VPL elements */
+    /* wave w sums chunks w, w + 4, ... over the lane's VPL elements, four
+     * chunks' loads in flight at a time */
     fv o = (fv) 0.0f;
-    for (int c = wave; c < nch; c += 4) o += wts[c] * *(const fv *) (P + (size_t) c * (hd + 2) + lane * VPL);
+    const float * Pl = P + lane * VPL;
+    int c = wave;
+    for (; c + 12 < nch; c += 16) {
+        const fv a0 = *(const fv *) (Pl + (size_t) c * (hd + 2)), a1 = *(const fv *) (Pl + (size_t) (c + 4) * (hd + 2));
+        const fv a2 = *(const fv *) (Pl + (size_t) (c + 8) * (hd + 2)), a3 = *(const fv *) (Pl + (size_t) (c + 12) * (hd + 2));
+        o += wts[c] * a0;
+        o += wts[c + 4] * a1;
+        o += wts[c + 8] * a2;
+        o += wts[c + 12] * a3;
+    }
+    for (; c < nch; c += 4) o += wts[c] * *(const fv *) (Pl + (size_t) c * (hd + 2));
     acc[wave][lane] = o;
     __syncthreads();
     if (wave == 0) {
@@ -411,9 +428,9 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
             return nullptr;
         }
     }
-    /* the combine keeps one weight per position chunk in LDS */
+    /* the combine keeps two floats per position chunk in LDS */
     const long nch_max = ((long) c.max_ctx + kAttnChunk - 1) / kAttnChunk;
-    if (nch_max * 4 > 65536) { set_error("max_ctx %d is above %d", c.max_ctx, 16384 * kAttnChunk); return nullptr; }
+    if (nch_max * 8 > 65536) { set_error("max_ctx %d is above %d", c.max_ctx, 8192 * kAttnChunk); return nullptr; }
     if (c.hidden > 8192) { set_error("hidden %d is above 8192", c.hidden); return nullptr; }
     Model * m = new Model;
     m->c = c;
@@ -558,7 +575,7 @@ int chain(Model * m, float * logits, hipStream_t s) {
         const int span = full || c.sliding_window > c.max_ctx ? c.max_ctx : c.sliding_window;
         const int nch = (span + kAttnChunk - 1) / kAttnChunk;
         const dim3 pg((unsigned) nch, (unsigned) c.kv_heads), pb((unsigned) (64 * (c.heads / c.kv_heads)));
-        const uint32_t wl = (uint32_t) (nch * 4);
+        const uint32_t wl = (uint32_t) (nch * 8);
         uint16_t * a16 = b16 ? m->attn16 : nullptr;
 #define FW_ATTN(V)                                                                                                  \
     do {                                                                                                            \
