@@ -179,7 +179,7 @@ __device__ __forceinline__ uint32_t kq_stage_x(uint8_t * lds, const void * x, in
 template <int XF32, int PADU = 0>
 __device__ __forceinline__ int kq_x_range(uint8_t * lds, uint32_t * xr, const void * x, int ldx, int ncol, int cols,
                                           int xst, int first = 0) {
-    if (!xr_out(xr, first)) return 0;
+    if (!xr_out_lanes(xr[threadIdx.x & 15u], first)) return 0;
     uint32_t m = 0;
     for (int e = threadIdx.x; e < ncol * cols; e += blockDim.x) {
         const int n = e / cols, c = e - n * cols;

@@ -93,6 +93,17 @@ __device__ __forceinline__ bool xr_out(const uint32_t * xr, int first = 0) {
     return (b & 1u) || (!(b & 2u) && (b & 4u));
 }
 
+/* The same from one word per lane, lane i holding wave i's verdict: one
+ * LDS read and three ballots. */
+__device__ __forceinline__ bool xr_out_lanes(uint32_t w, int first = 0) {
+    const int lane = (int) (threadIdx.x & 63u), nw = (int) (blockDim.x >> 6);
+    const uint32_t b = lane >= first && lane < nw ? w : 0u;
+    const bool over = __builtin_amdgcn_ballot_w64(b & 1u) != 0;
+    const bool big = __builtin_amdgcn_ballot_w64(b & 2u) != 0;
+    const bool nonzero = __builtin_amdgcn_ballot_w64(b & 4u) != 0;
+    return over || (!big && nonzero);
+}
+
 __device__ __forceinline__ uint32_t xr_wave_max(uint32_t m) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t) __shfl_xor((int) m, o, 64));
