@@ -298,6 +298,19 @@ int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits,
 int sparkmv_model_capture(void * model, float * logits, void * stream);
 /* Set token and position, then replay the recorded graph (as forward). */
 int sparkmv_model_replay(void * model, uint32_t token, int pos, void * stream);
+/* A speculative-verify block (vq-model-gpu.cu:955-969 verify_logits over
+ * forward_batch, :858-953): ntok <= 8 consecutive tokens at positions
+ * pos .. pos + ntok - 1, each attending causally to the positions up to its
+ * own; every matvec runs once over the block's columns and the head gives
+ * logits [ntok][vocab] (a Q8_0 head column equals its one-column result bit
+ * for bit). Fills those cache rows. The first block allocates the model's
+ * block buffers. */
+int sparkmv_model_verify(void * model, const uint32_t * tokens, int ntok, int pos, float * logits, void * stream);
+/* Keep the first pos cached positions (model.rs:361-381 rollback): refused
+ * past the cached length; later steps overwrite the rows it drops. */
+int sparkmv_model_rollback(void * model, int pos);
+/* The cached length: one past the last position a step wrote, or as rolled back. */
+int sparkmv_model_len(void * model);
 /* The device rows of layer's K and V cache ([max_ctx][kv_dim] f32 each). */
 int sparkmv_model_kv(void * model, int layer, float ** k, float ** v);
 

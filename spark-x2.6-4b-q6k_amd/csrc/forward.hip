@@ -97,6 +97,10 @@ __global__ __launch_bounds__(256) void fw_rmsnorm_kernel(const float * x, const 
                                                          uint16_t * out16, int n, float eps) {
     __shared__ double part[4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    /* workgroup b normalizes column b (a verify block's tokens) */
+    x += (size_t) blockIdx.x * n;
+    if (out) out += (size_t) blockIdx.x * n;
+    if (out16) out16 += (size_t) blockIdx.x * n;
     /* x and w of this thread's elements requested together: one memory
      * round trip before the reduction */
     float xv[PER], wv[PER];
@@ -302,6 +306,166 @@ __global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part
     }
 }
 
+/* ---- a verify block: ntok <= 8 consecutive tokens at positions pos0 .. ----
+ * (vq-model-gpu.cu:858-969 forward_batch + verify_logits). Each step of the
+ * forward runs once for the whole block; token t attends causally to the
+ * positions up to pos0 + t. Positions and tokens are kernel arguments: the
+ * block path runs eagerly. */
+struct FwTok8 {
+    int t[8];
+};
+
+/* Embedding rows of a Q8_0 head for the block's tokens: column t = row tok[t]. */
+__global__ void fw_q8_0_rows_kernel(const uint8_t * blocks, int cols, FwTok8 tok, float * out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    if (i >= cols) return;
+    const uint8_t * b = blocks + ((size_t) tok.t[t] * (cols >> 5) + (i >> 5)) * 34;
+    _Float16 d;
+    __builtin_memcpy(&d, b, 2);
+    out[(size_t) t * cols + i] = (float) d * (float) (int8_t) b[2 + (i & 31)];
+}
+
+/* Rope and the KV store for token t = blockIdx.y at position pos0 + t:
+ * items [0, (heads + kv_heads) * half) rotate a pair of one q or k head in
+ * place (model.rs:416-438, f32 table), items [0, kvd) store v and the k
+ * elements past pdim; a rotated k pair goes to the cache too. */
+__global__ void fw_rope_kv_n_kernel(float * qkv, int ldq, int qd, int kvd, int heads, int kv_heads, int hd, int pdim,
+                                    float theta, int pos0, float * kc, float * vc) {
+    const int half = pdim / 2, t = blockIdx.y, pos = pos0 + t;
+    const int i0 = blockIdx.x * blockDim.x + threadIdx.x;
+    float * row = qkv + (size_t) t * ldq;
+    if (i0 < (heads + kv_heads) * half) {
+        const int h = i0 / half, i = i0 - h * half;
+        const float freq = 1.0f / powf(theta, (float) (2 * i) / (float) pdim);
+        const float a = (float) pos * freq;
+        const float c = cosf(a), sn = sinf(a);
+        float * base = h < heads ? row + (size_t) h * hd : row + qd + (size_t) (h - heads) * hd;
+        const float x0 = base[i], x1 = base[i + half];
+        const float r0 = x0 * c - x1 * sn, r1 = x1 * c + x0 * sn;
+        base[i] = r0;
+        base[i + half] = r1;
+        if (h >= heads) {
+            float * k = kc + (size_t) pos * kvd + (size_t) (h - heads) * hd;
+            k[i] = r0;
+            k[i + half] = r1;
+        }
+    }
+    if (i0 < kvd) {
+        vc[(size_t) pos * kvd + i0] = row[qd + kvd + i0];
+        if (i0 % hd >= 2 * half) kc[(size_t) pos * kvd + i0] = row[qd + i0];
+    }
+}
+
+/* Attention partials of token t = blockIdx.z (query rotated in qkv, every
+ * key in the cache), as fw_attn_part_kernel otherwise. */
+template <int VPL>
+__global__ __launch_bounds__(256) void fw_attn_part_n_kernel(const float * qkv, int ldq, int kvd, const float * kc,
+                                                              const float * vc, int pos0, int window, int heads,
+                                                              int kv_heads, float scale, int nch_max, float * part) {
+    constexpr int hd = 64 * VPL, C = kAttnChunk;
+    typedef float fv __attribute__((ext_vector_type(VPL)));
+    const int t = blockIdx.z, pos = pos0 + t;
+    const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
+    const int n = pos + 1 - start;
+    const int chunk = blockIdx.x, kvh = blockIdx.y;
+    const int G = heads / kv_heads;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int j0 = chunk * C;
+    if (j0 >= n) return;
+    const int jn = min(C, n - j0);
+    const int h = kvh * G + wave;
+    const fv q = *(const fv *) (qkv + (size_t) t * ldq + (size_t) h * hd + lane * VPL);
+    const float * kb = kc + (size_t) (start + j0) * kvd + (size_t) kvh * hd + lane * VPL;
+    const float * vb = vc + (size_t) (start + j0) * kvd + (size_t) kvh * hd + lane * VPL;
+    fv kr[C], vr[C];
+#pragma unroll
+    for (int j = 0; j < C; j++) kr[j] = *(const fv *) (kb + (size_t) min(j, jn - 1) * kvd);
+#pragma unroll
+    for (int j = 0; j < C; j++) vr[j] = *(const fv *) (vb + (size_t) min(j, jn - 1) * kvd);
+    float sc[C];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int v = 0; v < VPL; v++) s += q[v] * kr[j][v];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+        sc[j] = s * scale;
+        if (j < jn) m = fmaxf(m, sc[j]);
+    }
+    float l = 0.0f;
+    fv o = (fv) 0.0f;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+        const float e = j < jn ? expf(sc[j] - m) : 0.0f;
+        l += e;
+        o += e * vr[j];
+    }
+    float * P = part + (((size_t) t * heads + h) * nch_max + chunk) * (hd + 2);
+    *(fv *) (P + lane * VPL) = o;
+    if (lane == 0) {
+        P[hd] = m;
+        P[hd + 1] = l;
+    }
+}
+
+/* The combine of token t = blockIdx.y: gates at gate + t * ldg, output row t. */
+template <int VPL>
+__global__ __launch_bounds__(256) void fw_attn_combine_n_kernel(const float * part, const float * gate, int ldg,
+                                                                int pos0, int window, int heads, int nch_max,
+                                                                float * out, uint16_t * out16) {
+    constexpr int hd = 64 * VPL;
+    typedef float fv __attribute__((ext_vector_type(VPL)));
+    extern __shared__ float wts[];
+    __shared__ float red[8];
+    __shared__ fv acc[4][64];
+    const int t = blockIdx.y, pos = pos0 + t;
+    const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
+    const int nch = (pos + 1 - start + kAttnChunk - 1) / kAttnChunk;
+    const int h = blockIdx.x, th = threadIdx.x, lane = th & 63, wave = th >> 6;
+    const float * P = part + ((size_t) t * heads + h) * nch_max * (hd + 2);
+    float * ls = wts + nch;
+    float M = -INFINITY;
+    for (int c = th; c < nch; c += 256) {
+        const float mc = P[(size_t) c * (hd + 2) + hd], lc = P[(size_t) c * (hd + 2) + hd + 1];
+        wts[c] = mc;
+        ls[c] = lc;
+        M = fmaxf(M, mc);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) red[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float L = 0.0f;
+    for (int c = th; c < nch; c += 256) {
+        const float w = expf(wts[c] - M);
+        wts[c] = w;
+        L += w * ls[c];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    if (lane == 0) red[4 + wave] = L;
+    __syncthreads();
+    fv o = (fv) 0.0f;
+    const float * Pl = P + lane * VPL;
+    for (int c = wave; c < nch; c += 4) o += wts[c] * *(const fv *) (Pl + (size_t) c * (hd + 2));
+    acc[wave][lane] = o;
+    __syncthreads();
+    if (wave == 0) {
+        const float inv = 1.0f / ((red[4] + red[5]) + (red[6] + red[7]));
+        const float g = 1.0f / (1.0f + expf(-gate[(size_t) t * ldg + h]));
+        const fv r = ((acc[0][lane] + acc[1][lane]) + (acc[2][lane] + acc[3][lane])) * inv * g;
+        const size_t ob = (size_t) t * heads * hd + (size_t) h * hd + lane * VPL;
+#pragma unroll
+        for (int v = 0; v < VPL; v++) {
+            out[ob + v] = r[v];
+            if (out16) out16[ob + v] = fw_bf16(r[v]);
+        }
+    }
+}
+
 /* act = gelu(g) * u with torch's exact gelu, erf in f64 as model.rs:253-258
  * calls it. */
 __global__ void fw_gelu_mul_kernel(const float * g, const float * u, float * act, uint16_t * act16, int n) {
@@ -337,6 +501,13 @@ struct Model {
     /* the recorded chain */
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    /* cached positions (model.rs:453, :361-381) */
+    int len = 0;
+    /* verify-block buffers, allocated at the first block: 8 columns of each
+     * activation, gate rows at the qkv stride, partials per token */
+    void * vmem = nullptr;
+    float * vh, * vxn, * vqkv, * vg, * vattn, * vmg, * vmu, * vact, * vpart;
+    uint16_t * vxn16, * vattn16, * vact16;
 };
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t) 255; }
@@ -353,7 +524,7 @@ int check_launch(const char * what) {
 }
 
 int gemv(const Model & m, const void * const * st, int rows, int cols, const void * x, float * y, int acc,
-         hipStream_t s) {
+         hipStream_t s, int ncol = 1, int ldy = 0) {
     VqMatDesc d;
     memset(&d, 0, sizeof d);
     for (int i = 0; i < m.c.nstages; i++) d.stages[i] = st[i];
@@ -363,13 +534,13 @@ int gemv(const Model & m, const void * const * st, int rows, int cols, const voi
     memset(&c, 0, sizeof c);
     c.dim = m.c.dim; c.nc = m.c.nc; c.cols = cols; c.v3 = m.c.v3; c.nst = m.c.nstages;
     c.mats = &d; c.nmat = 1;
-    c.x = x; c.ldx = cols; c.xf32 = m.c.x_dtype == SPARKMV_X_F32; c.ncol = 1; c.ldy = rows;
+    c.x = x; c.ldx = cols; c.xf32 = m.c.x_dtype == SPARKMV_X_F32; c.ncol = ncol; c.ldy = ldy ? ldy : rows;
     c.accumulate = acc; c.stream = s;
     return vq_launch(c);
 }
 
 int gemv2(const Model & m, const void * const * st0, int rows0, float * y0, const void * const * st1, int rows1,
-          float * y1, int cols, const void * x, hipStream_t s) {
+          float * y1, int cols, const void * x, hipStream_t s, int ncol = 1, int ldy = 0) {
     VqMatDesc d[2];
     memset(d, 0, sizeof d);
     for (int i = 0; i < m.c.nstages; i++) { d[0].stages[i] = st0[i]; d[1].stages[i] = st1[i]; }
@@ -379,18 +550,21 @@ int gemv2(const Model & m, const void * const * st0, int rows0, float * y0, cons
     memset(&c, 0, sizeof c);
     c.dim = m.c.dim; c.nc = m.c.nc; c.cols = cols; c.v3 = m.c.v3; c.nst = m.c.nstages;
     c.mats = d; c.nmat = 2;
-    c.x = x; c.ldx = cols; c.xf32 = m.c.x_dtype == SPARKMV_X_F32; c.ncol = 1; c.ldy = rows0;
+    c.x = x; c.ldx = cols; c.xf32 = m.c.x_dtype == SPARKMV_X_F32; c.ncol = ncol; c.ldy = ldy ? ldy : rows0;
     c.accumulate = 0; c.stream = s;
     return vq_launch(c);
 }
 
-int rmsnorm(const Model & m, const float * x, const float * w, hipStream_t s) {
+int rmsnorm(const Model & m, const float * x, const float * w, hipStream_t s, int ncol = 1, float * out = nullptr,
+            uint16_t * out16 = nullptr) {
     const bool b16 = m.c.x_dtype == SPARKMV_X_BF16;
     const int per = (m.c.hidden + 255) / 256;
-    uint16_t * o16 = b16 ? m.xn16 : nullptr;
-    if (per <= 4) hipLaunchKernelGGL(fw_rmsnorm_kernel<4>, dim3(1), dim3(256), 0, s, x, w, m.xn, o16, m.c.hidden, m.c.eps);
-    else if (per <= 12) hipLaunchKernelGGL(fw_rmsnorm_kernel<12>, dim3(1), dim3(256), 0, s, x, w, m.xn, o16, m.c.hidden, m.c.eps);
-    else if (per <= 32) hipLaunchKernelGGL(fw_rmsnorm_kernel<32>, dim3(1), dim3(256), 0, s, x, w, m.xn, o16, m.c.hidden, m.c.eps);
+    float * o = out ? out : m.xn;
+    uint16_t * o16 = b16 ? (out16 ? out16 : m.xn16) : nullptr;
+    const dim3 g((unsigned) ncol);
+    if (per <= 4) hipLaunchKernelGGL(fw_rmsnorm_kernel<4>, g, dim3(256), 0, s, x, w, o, o16, m.c.hidden, m.c.eps);
+    else if (per <= 12) hipLaunchKernelGGL(fw_rmsnorm_kernel<12>, g, dim3(256), 0, s, x, w, o, o16, m.c.hidden, m.c.eps);
+    else if (per <= 32) hipLaunchKernelGGL(fw_rmsnorm_kernel<32>, g, dim3(256), 0, s, x, w, o, o16, m.c.hidden, m.c.eps);
     else { set_error("hidden %d is above 8192", m.c.hidden); return -1; }
     return check_launch("rms norm launch");
 }
@@ -472,6 +646,7 @@ void sparkmv_model_destroy(void * model) {
     if (m->exec) (void) hipGraphExecDestroy(m->exec);
     if (m->graph) (void) hipGraphDestroy(m->graph);
     if (m->mem) (void) hipFree(m->mem);
+    if (m->vmem) (void) hipFree(m->vmem);
     delete m;
 }
 
@@ -610,6 +785,104 @@ int chain(Model * m, float * logits, hipStream_t s) {
     return kq_gemv_launch(8, m->head_blocks, c.vocab, c.hidden, xin, b16 ? 0 : 1, c.hidden, 1, logits, c.vocab, 0, s);
 }
 
+int alloc_verify(Model * m) {
+    const sparkmv_model_cfg & c = m->c;
+    const size_t qd = (size_t) c.heads * c.head_dim, kvd = (size_t) c.kv_heads * c.head_dim, N = 8;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
+    const size_t o_h = take(N * c.hidden * 4), o_xn = take(N * c.hidden * 4), o_qkv = take(N * (qd + 2 * kvd) * 4);
+    const size_t o_g = take(N * (qd + 2 * kvd) * 4), o_attn = take(N * qd * 4), o_mg = take(N * c.intermediate * 4);
+    const size_t o_mu = take(N * c.intermediate * 4), o_act = take(N * c.intermediate * 4);
+    const size_t o_xn16 = take(N * c.hidden * 2), o_attn16 = take(N * qd * 2), o_act16 = take(N * c.intermediate * 2);
+    const size_t o_part = take(N * c.heads * (size_t) m->nch_max * (c.head_dim + 2) * 4);
+    hipError_t e = hipMalloc(&m->vmem, off);
+    if (e != hipSuccess) { m->vmem = nullptr; return fail_hip("verify-block buffers", e); }
+    uint8_t * b = (uint8_t *) m->vmem;
+    m->vh = (float *) (b + o_h); m->vxn = (float *) (b + o_xn); m->vqkv = (float *) (b + o_qkv);
+    m->vg = (float *) (b + o_g); m->vattn = (float *) (b + o_attn); m->vmg = (float *) (b + o_mg);
+    m->vmu = (float *) (b + o_mu); m->vact = (float *) (b + o_act); m->vpart = (float *) (b + o_part);
+    m->vxn16 = (uint16_t *) (b + o_xn16); m->vattn16 = (uint16_t *) (b + o_attn16);
+    m->vact16 = (uint16_t *) (b + o_act16);
+    return 0;
+}
+
+/* A verify block: the forward of ntok consecutive tokens at pos .. pos + ntok - 1
+ * with every matvec over ntok columns (weights decoded once for the block),
+ * then the head over the same columns; logits are [ntok][vocab]. */
+int block(Model * m, const uint32_t * tokens, int N, int pos, float * logits, hipStream_t s) {
+    const sparkmv_model_cfg & c = m->c;
+    const bool b16 = c.x_dtype == SPARKMV_X_BF16;
+    const int qd = c.heads * c.head_dim, kvd = c.kv_heads * c.head_dim, hd = c.head_dim, ldq = qd + 2 * kvd;
+    FwTok8 tk;
+    for (int t = 0; t < 8; t++) tk.t[t] = t < N ? (int) tokens[t] : 0;
+    if (m->head_kind == 0) {
+        hipLaunchKernelGGL(fw_fill_kernel, dim3((N * c.hidden + 255) / 256), dim3(256), 0, s, m->vh, N * c.hidden, 0.0f);
+        if (check_launch("fill launch")) return -1;
+        const Layout L = make_layout(c.dim, c.nc, c.vocab, c.hidden, c.v3);
+        for (int t = 0; t < N; t++)
+            for (int st = 0; st < c.nstages; st++)
+                if (vq_row_dequant_launch(m->head_stages[st], L, (int) tokens[t], m->vh + (size_t) t * c.hidden, s))
+                    return -1;
+    } else {
+        hipLaunchKernelGGL(fw_q8_0_rows_kernel, dim3((c.hidden + 255) / 256, N), dim3(256), 0, s,
+                           (const uint8_t *) m->head_blocks, c.hidden, tk, m->vh);
+        if (check_launch("embedding launch")) return -1;
+    }
+    const float scale = 1.0f / sqrtf((float) hd);
+    const void * xin = b16 ? (const void *) m->vxn16 : (const void *) m->vxn;
+    for (int li = 0; li < c.layers; li++) {
+        const sparkmv_model_layer & L = m->layers[li];
+        const bool full = L.full != 0;
+        float * kc = m->kv + (size_t) li * 2 * c.max_ctx * kvd;
+        float * vc = kc + (size_t) c.max_ctx * kvd;
+        if (rmsnorm(*m, m->vh, L.in_norm, s, N, m->vxn, m->vxn16)) return -1;
+        if (gemv2(*m, L.qkv, ldq, m->vqkv, L.attn_gate, c.heads, m->vg, c.hidden, xin, s, N, ldq)) return -1;
+        const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
+        const int pdim = rope_dim(hd, full ? c.rope_full_partial : c.rope_slide_partial);
+        const int items = (c.heads + c.kv_heads) * (pdim / 2) > kvd ? (c.heads + c.kv_heads) * (pdim / 2) : kvd;
+        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3((items + 255) / 256, N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd,
+                           c.heads, c.kv_heads, hd, pdim, (float) theta, pos, kc, vc);
+        if (check_launch("rope launch")) return -1;
+        const int window = full ? 0 : c.sliding_window;
+        const int last = pos + N - 1;
+        const int span = full || c.sliding_window > last + 1 ? last + 1 : c.sliding_window;
+        const int nch = (span + kAttnChunk - 1) / kAttnChunk;
+        const dim3 pg((unsigned) nch, (unsigned) c.kv_heads, (unsigned) N), pb((unsigned) (64 * (c.heads / c.kv_heads)));
+        uint16_t * a16 = b16 ? m->vattn16 : nullptr;
+#define FW_ATTN_N(V)                                                                                                \
+    do {                                                                                                            \
+        hipLaunchKernelGGL(fw_attn_part_n_kernel<V>, pg, pb, 0, s, m->vqkv, ldq, kvd, kc, vc, pos, window, c.heads,   \
+                           c.kv_heads, scale, m->nch_max, m->vpart);                                                \
+        hipLaunchKernelGGL(fw_attn_combine_n_kernel<V>, dim3(c.heads, N), dim3(256), (uint32_t) (nch * 8), s,       \
+                           m->vpart, m->vg, ldq, pos, window, c.heads, m->nch_max, m->vattn, a16);                  \
+    } while (0)
+        if (hd == 64) FW_ATTN_N(1);
+        else if (hd == 128) FW_ATTN_N(2);
+        else FW_ATTN_N(4);
+#undef FW_ATTN_N
+        if (check_launch("attention launch")) return -1;
+        if (gemv(*m, L.out, c.hidden, qd, b16 ? (const void *) m->vattn16 : (const void *) m->vattn, m->vh, 1, s, N,
+                 c.hidden))
+            return -1;
+        if (rmsnorm(*m, m->vh, L.post_norm, s, N, m->vxn, m->vxn16)) return -1;
+        if (gemv2(*m, L.gate, c.intermediate, m->vmg, L.up, c.intermediate, m->vmu, c.hidden, xin, s, N,
+                  c.intermediate))
+            return -1;
+        hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * c.intermediate + 255) / 256), dim3(256), 0, s, m->vmg, m->vmu,
+                           m->vact, b16 ? m->vact16 : nullptr, N * c.intermediate);
+        if (check_launch("gelu launch")) return -1;
+        if (gemv(*m, L.down, c.hidden, c.intermediate, b16 ? (const void *) m->vact16 : (const void *) m->vact, m->vh,
+                 1, s, N, c.hidden))
+            return -1;
+    }
+    if (rmsnorm(*m, m->vh, m->final_norm, s, N, m->vxn, m->vxn16)) return -1;
+    /* the head over the block's columns; the Q8_0 kernel gives each column
+     * exactly its one-column result (the verify-head requirement,
+     * Spark-X2.6-4B-Base-handoff.md:299-302) */
+    if (m->head_kind == 0) return gemv(*m, m->head_stages, c.vocab, c.hidden, xin, logits, 0, s, N, c.vocab);
+    return kq_gemv_launch(8, m->head_blocks, c.vocab, c.hidden, xin, b16 ? 0 : 1, c.hidden, N, logits, c.vocab, 0, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -620,7 +893,9 @@ int sparkmv_model_forward(void * model, uint32_t token, int pos, float * logits,
     if (check_step(m, token, pos) || ready(m)) return -1;
     hipStream_t s = (hipStream_t) stream;
     if (set_state(m, token, pos, s)) return -1;
-    return chain(m, logits, s);
+    if (chain(m, logits, s)) return -1;
+    m->len = pos + 1;
+    return 0;
 }
 
 int sparkmv_model_capture(void * model, float * logits, void * stream) {
@@ -654,7 +929,39 @@ int sparkmv_model_replay(void * model, uint32_t token, int pos, void * stream) {
     hipStream_t s = (hipStream_t) stream;
     if (set_state(m, token, pos, s)) return -1;
     hipError_t e = hipGraphLaunch(m->exec, s);
-    return e == hipSuccess ? 0 : fail_hip("graph launch", e);
+    if (e != hipSuccess) return fail_hip("graph launch", e);
+    m->len = pos + 1;
+    return 0;
+}
+
+int sparkmv_model_verify(void * model, const uint32_t * tokens, int ntok, int pos, float * logits, void * stream) {
+    Model * m = (Model *) model;
+    if (!m || !tokens || !logits) { set_error("model, tokens or logits is null"); return -1; }
+    if (ntok < 1 || ntok > 8) { set_error("a verify block holds 1..8 tokens, not %d", ntok); return -1; }
+    if (pos < 0 || pos + ntok > m->c.max_ctx) {
+        set_error("positions %d..%d exceed the %d-token cache", pos, pos + ntok - 1, m->c.max_ctx);
+        return -1;
+    }
+    for (int t = 0; t < ntok; t++)
+        if ((long) tokens[t] >= m->c.vocab) { set_error("token %u is outside the vocabulary", tokens[t]); return -1; }
+    if (ready(m)) return -1;
+    if (!m->vmem && alloc_verify(m)) return -1;
+    if (block(m, tokens, ntok, pos, logits, (hipStream_t) stream)) return -1;
+    m->len = pos + ntok;
+    return 0;
+}
+
+int sparkmv_model_rollback(void * model, int pos) {
+    Model * m = (Model *) model;
+    if (!m) { set_error("model is null"); return -1; }
+    if (pos < 0 || pos > m->len) { set_error("rollback to %d exceeds the %d cached positions", pos, m->len); return -1; }
+    m->len = pos;
+    return 0;
+}
+
+int sparkmv_model_len(void * model) {
+    Model * m = (Model *) model;
+    return m ? m->len : -1;
 }
 
 /* The layer's KV cache rows (device pointers), for tests and inspection. */

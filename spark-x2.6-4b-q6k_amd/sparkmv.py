@@ -139,6 +139,9 @@ SIGNATURES = {
     "sparkmv_model_forward": (_I, [_P, ctypes.c_uint32, _I, _P, _P]),
     "sparkmv_model_capture": (_I, [_P, _P, _P]),
     "sparkmv_model_replay": (_I, [_P, ctypes.c_uint32, _I, _P]),
+    "sparkmv_model_verify": (_I, [_P, ctypes.POINTER(ctypes.c_uint32), _I, _I, _P, _P]),
+    "sparkmv_model_rollback": (_I, [_P, _I]),
+    "sparkmv_model_len": (_I, [_P]),
     "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
     "sparkmv_synth_container_bytes": (_S, [_I] * 6),
     "sparkmv_synth_vq_container": (_I, [_U64, _I, _I, _I, _I, _I, _I, _P, _S]),
@@ -519,6 +522,20 @@ class Model:
 
     def replay(self, token, pos, stream):
         check(lib().sparkmv_model_replay(self.h, int(token), int(pos), _stream_ptr(stream)), "model replay")
+
+    def verify(self, tokens, pos, logits, stream=None):
+        """A block of up to 8 tokens at pos .. (vq-model-gpu.cu:955-969);
+        logits: device f32 [len(tokens), vocab]."""
+        arr = (ctypes.c_uint32 * len(tokens))(*[int(t) for t in tokens])
+        check(lib().sparkmv_model_verify(self.h, arr, len(tokens), int(pos), logits.data_ptr(), _stream_ptr(stream)),
+              "model verify")
+
+    def rollback(self, pos):
+        """Keep the first pos cached positions (model.rs:361-381)."""
+        check(lib().sparkmv_model_rollback(self.h, int(pos)), "model rollback")
+
+    def __len__(self):
+        return lib().sparkmv_model_len(self.h)
 
     def kv(self, layer):
         """(k, v) device pointers of the layer's cache, [max_ctx][kv_dim] f32 each."""

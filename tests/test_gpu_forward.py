@@ -143,3 +143,49 @@ def test_forward_graph_replay(sm, ref, dev, head_kind):
             assert err <= 1e-5
     with pytest.raises(sm.SparkmvError):
         model.replay(1, CFG["max_ctx"], stream)
+
+
+@pytest.mark.parametrize("head_kind", ["q8_0", "vq"])
+@pytest.mark.parametrize("xd", ["f32", "bf16"])
+def test_verify_block_and_rollback(sm, ref, dev, head_kind, xd):
+    """Speculative verify (vq-model-gpu.cu:955-969): three tokens one at a
+    time, then a block of 8 at position 3 (past the 3-position window); every
+    row of the block's logits against the oracle stepping the same tokens one
+    at a time. Then the target keeps 2 of the 8: rollback to 5
+    (model.rs:361-381) and the next token at 5 must match an oracle that saw
+    only the prefix and the 2 kept tokens."""
+    import torch
+    x_dtype = sm.X_F32 if xd == "f32" else sm.X_BF16
+    bar = 1e-5 if xd == "f32" else 2e-2
+    model, oracle = build(sm, ref, dev, head_kind, x_dtype)
+    kept = fw.Forward(oracle.c, oracle.layers, oracle.embed, oracle.norm)
+    prefix, block = [5, 17, 3], [250, 42, 7, 17, 99, 1, 300, 12]
+    one = torch.empty(CFG["vocab"], device=dev)
+    for p, t in enumerate(prefix):
+        model.forward(t, p, one)
+        oracle.forward(t, p)
+        kept.forward(t, p)
+    logits = torch.full((len(block), CFG["vocab"]), float("nan"), device=dev)
+    model.verify(block, len(prefix), logits)
+    torch.cuda.synchronize()
+    got = logits.cpu().numpy()
+    for i, t in enumerate(block):
+        err = rel_l2(got[i], oracle.forward(t, len(prefix) + i))
+        print(f"head {head_kind} x {xd} block row {i} (pos {len(prefix) + i}): relL2 {err:.2e}")
+        assert err <= bar
+    assert len(model) == len(prefix) + len(block)
+    model.rollback(len(prefix) + 2)
+    assert len(model) == len(prefix) + 2
+    for i in range(2):
+        kept.forward(block[i], len(prefix) + i)
+    model.forward(77, len(prefix) + 2, one)
+    torch.cuda.synchronize()
+    err = rel_l2(one.cpu().numpy(), kept.forward(77, len(prefix) + 2))
+    print(f"after rollback: relL2 {err:.2e}")
+    assert err <= bar
+    with pytest.raises(sm.SparkmvError):
+        model.rollback(len(prefix) + 4)
+    assert "exceeds" in sm.last_error()
+    with pytest.raises(sm.SparkmvError):
+        model.verify(list(range(9)), 0, logits)
+    assert "1..8 tokens" in sm.last_error()
