@@ -13,7 +13,7 @@ replayed as one HIP graph (native plan, sparkmv_plan_*). Weights and inputs
 are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--mode graph|eager]
-                    [--workload decode-set|ffn-up|q6k-down|verify8|prefill512|forward]
+                    [--workload decode-set|ffn-up|q6k-down|verify8|prefill512|forward|verify-block]
 
 Prints one JSON line (rank 0). The metric is time per token (lower is
 better); achieved GB/s over the algorithmic bytes (container + bf16 x + f32 y
@@ -232,7 +232,7 @@ def bench_forward(args, sm, torch, dev):
     cache is first filled with `context` tokens (untimed); then each step is
     one token at the next position, replayed as one HIP graph."""
     P = args.context
-    max_ctx = P + args.warmup + args.steps + 8
+    max_ctx = P + args.warmup + args.steps + 16
     cfg = dict(hidden=HIDDEN, layers=LAYERS, heads=NHEAD, kv_heads=KVD // (QD // NHEAD), head_dim=QD // NHEAD,
                intermediate=FFN, vocab=args.head_rows, eps=1e-6, sliding_window=FW_WINDOW, rope_full_theta=5.0e6,
                rope_full_partial=0.25, rope_slide_theta=1.0e4, rope_slide_partial=1.0, max_ctx=max_ctx,
@@ -278,6 +278,35 @@ def bench_forward(args, sm, torch, dev):
         b.record(stream)
         torch.cuda.synchronize()
         eager_us = a.elapsed_time(b) / 4 * 1e3
+        if args.workload == "verify-block":
+            # a block of 8 drafted tokens at position P + 4, rolled back after each step
+            blk = torch.zeros((8, args.head_rows), device=dev)
+            P4 = P + 4
+            for _ in range(args.warmup):
+                model.verify([int(t) for t in toks[P4:P4 + 8]], P4, blk, stream)
+                model.rollback(P4)
+            torch.cuda.synchronize()
+            a, b = ev(), ev()
+            a.record(stream)
+            for _ in range(args.steps):
+                model.verify([int(t) for t in toks[P4:P4 + 8]], P4, blk, stream)
+                model.rollback(P4)
+            b.record(stream)
+            torch.cuda.synchronize()
+            vms = a.elapsed_time(b) / args.steps
+            log(f"  verify block of 8: {vms * 1e3:.1f} us (eager), {vms * 1e3 / 8:.1f} us per token; "
+                f"single token {eager_us:.1f} us eager")
+            return {
+                "metric": "speculative verify block us/step (8 tokens, whole model, tied Q8_0 head)",
+                "value": round(vms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+                "warmup": args.warmup, "ms_per_step": round(vms, 4), "higher_is_better": False, "scaling": "weak",
+                "vs_baseline": None, "dtype": "f16xf16->f32 matvecs (bf16 x), f32 elementwise, f64 norm sums",
+                "data": "synthetic (seeded, random-init weights of the real shapes)",
+                "config": {"workload": f"verify block of 8 tokens at context {P4}", "layers": LAYERS,
+                           "hidden": HIDDEN, "ffn": FFN, "heads": NHEAD, "sliding_window": FW_WINDOW,
+                           "head": f"Q8_0 {args.head_rows}x{HIDDEN}", "mode": "eager"},
+                "single_token_eager_us": round(eager_us, 1),
+            }
         model.capture(logits, stream)
         pos = P + 4
         for _ in range(args.warmup):
@@ -477,7 +506,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--workload", default="decode-set",
-                    choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512", "forward"])
+                    choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512", "forward",
+                             "verify-block"])
     ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -507,7 +537,7 @@ def main():
             log(f"cpu baseline took {time.time() - t:.1f} s")
     elif args.workload == "prefill512":
         out = bench_prefill(args, sm, torch, dev)
-    elif args.workload == "forward":
+    elif args.workload in ("forward", "verify-block"):
         out = bench_forward(args, sm, torch, dev)
     else:
         out = bench_single(args, sm, torch, dev)
