@@ -314,6 +314,35 @@ int sparkmv_model_len(void * model);
 /* The device rows of layer's K and V cache ([max_ctx][kv_dim] f32 each). */
 int sparkmv_model_kv(void * model, int layer, float ** k, float ** v);
 
+/* ---- the per-artifact tuning profile (VQPROF 1) ----
+ * tools/vq/gpu/vq-profile.h:10-30 (format, FNV-1a fingerprint, trust rules),
+ * written by tools/vq-tune/src/artifact.rs:148-171. Host only. */
+typedef struct {
+    int kind;                    /* 0 gemv, 1 prefill */
+    int dim, nc, rows, cols, v3;
+    int variant;
+    int threads;                 /* gemv */
+    int bn, bk;                  /* prefill */
+    double rate;                 /* the measured GB/s (gemv) or tokens/s (prefill) column */
+} sparkmv_profile_entry;
+
+/* The artifact directory's fingerprint (vq-profile.h:118-146). */
+int sparkmv_profile_fingerprint(const char * dir, uint64_t * out);
+/* Parse a profile; NULL unless it carries version 1 (vq-profile.h:155-193). */
+void * sparkmv_profile_load(const char * path);
+void sparkmv_profile_close(void * profile);
+/* 1 when the profile's fingerprint and device name match, 0 when not (the
+ * reason in the error text), -1 on bad arguments. */
+int sparkmv_profile_trusted(const void * profile, uint64_t artifact, const char * gpu);
+int sparkmv_profile_count(const void * profile);
+int sparkmv_profile_entry_at(const void * profile, int i, sparkmv_profile_entry * out);
+/* The entry for one geometry (vq-profile.h:195-203), -1 when there is none. */
+int sparkmv_profile_find(const void * profile, int kind, int dim, int nc, int rows, int cols, int v3,
+                         sparkmv_profile_entry * out);
+/* Write a profile in the reference's format (at most 512 entries). */
+int sparkmv_profile_write(const char * path, uint64_t artifact, const char * gpu, const char * driver,
+                          const sparkmv_profile_entry * entries, int n);
+
 /* ---- synthetic workloads (host memory; no reference counterpart) ----
  * A named, seeded generator so every test and benchmark can rebuild the same
  * inputs: xoshiro256** seeded through splitmix64; normals by Box-Muller in

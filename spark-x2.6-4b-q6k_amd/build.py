@@ -19,7 +19,7 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib", "libsparkmv.so")
 
 HIP_SOURCES = ["vq_kernels.hip", "kq_kernels.hip", "prefill.hip", "forward.hip"]
-CXX_SOURCES = ["abi.cpp", "plan.cpp", "host/vq_format.cpp", "host/synth.cpp", "host/artifacts.cpp"]
+CXX_SOURCES = ["abi.cpp", "plan.cpp", "host/vq_format.cpp", "host/synth.cpp", "host/artifacts.cpp", "host/profile.cpp"]
 
 ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function"]

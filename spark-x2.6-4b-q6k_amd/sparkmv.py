@@ -13,6 +13,8 @@ Interface mirror (the reference's Rust surface this stands beside):
                            directory of RQVQ containers and RQVF sidecars)
   Gguf                     tools/dspark/src/gguf.rs:95-190 (Gguf::open,
                            tensor_bytes, get_*), with Q6_K tensors handed out
+  Profile / tune_gemv      tools/vq/gpu/vq-profile.h (VQPROF 1 reader, trust gate),
+                           tools/vq-tune/src/artifact.rs:148-171 (writer, sweep)
   Model.forward            tools/vq-runtime/src/model.rs:441-591 (Model::forward),
                            as the GPU runtime runs it, tools/vq/gpu/vq-model-gpu.cu:776-835
 """
@@ -65,6 +67,12 @@ class ModelLayer(ctypes.Structure):
     _fields_ = [("in_norm", ctypes.c_void_p), ("post_norm", ctypes.c_void_p), ("qkv", ctypes.c_void_p * 4),
                 ("attn_gate", ctypes.c_void_p * 4), ("out", ctypes.c_void_p * 4), ("gate", ctypes.c_void_p * 4),
                 ("up", ctypes.c_void_p * 4), ("down", ctypes.c_void_p * 4), ("full", ctypes.c_int)]
+
+
+class ProfileEntry(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("dim", ctypes.c_int), ("nc", ctypes.c_int), ("rows", ctypes.c_int),
+                ("cols", ctypes.c_int), ("v3", ctypes.c_int), ("variant", ctypes.c_int), ("threads", ctypes.c_int),
+                ("bn", ctypes.c_int), ("bk", ctypes.c_int), ("rate", ctypes.c_double)]
 
 
 # ggml tensor types the GGUF reader hands out
@@ -143,6 +151,15 @@ SIGNATURES = {
     "sparkmv_model_rollback": (_I, [_P, _I]),
     "sparkmv_model_len": (_I, [_P]),
     "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
+    "sparkmv_profile_fingerprint": (_I, [ctypes.c_char_p, ctypes.POINTER(_U64)]),
+    "sparkmv_profile_load": (_P, [ctypes.c_char_p]),
+    "sparkmv_profile_close": (None, [_P]),
+    "sparkmv_profile_trusted": (_I, [_P, _U64, ctypes.c_char_p]),
+    "sparkmv_profile_count": (_I, [_P]),
+    "sparkmv_profile_entry_at": (_I, [_P, _I, ctypes.POINTER(ProfileEntry)]),
+    "sparkmv_profile_find": (_I, [_P, _I, _I, _I, _I, _I, _I, ctypes.POINTER(ProfileEntry)]),
+    "sparkmv_profile_write": (_I, [ctypes.c_char_p, _U64, ctypes.c_char_p, ctypes.c_char_p,
+                                   ctypes.POINTER(ProfileEntry), _I]),
     "sparkmv_synth_container_bytes": (_S, [_I] * 6),
     "sparkmv_synth_vq_container": (_I, [_U64, _I, _I, _I, _I, _I, _I, _P, _S]),
     "sparkmv_synth_q6k": (_I, [_U64, _I, _I, _P]),
@@ -542,6 +559,86 @@ class Model:
         k, v = ctypes.c_void_p(), ctypes.c_void_p()
         check(lib().sparkmv_model_kv(self.h, layer, ctypes.byref(k), ctypes.byref(v)), "model kv")
         return k.value, v.value
+
+
+def profile_fingerprint(dirpath):
+    """The VQ artifact directory's FNV-1a fingerprint (tools/vq/gpu/vq-profile.h:118-146)."""
+    h = ctypes.c_uint64()
+    check(lib().sparkmv_profile_fingerprint(os.fsencode(dirpath), ctypes.byref(h)), "profile fingerprint")
+    return h.value
+
+
+class Profile:
+    """A VQPROF 1 tuning profile (tools/vq/gpu/vq-profile.h): entries per
+    geometry, trusted only for the artifact and device that measured it."""
+
+    def __init__(self, path):
+        self.h = lib().sparkmv_profile_load(os.fsencode(path))
+        if not self.h:
+            raise SparkmvError("profile load: " + last_error())
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().sparkmv_profile_close(self.h)
+            self.h = None
+
+    def trusted(self, artifact, gpu):
+        rc = lib().sparkmv_profile_trusted(self.h, artifact, gpu.encode())
+        check(0 if rc >= 0 else -1, "profile trust")
+        return rc == 1
+
+    def entries(self):
+        out = []
+        for i in range(lib().sparkmv_profile_count(self.h)):
+            e = ProfileEntry()
+            check(lib().sparkmv_profile_entry_at(self.h, i, ctypes.byref(e)), "profile entry")
+            out.append(e)
+        return out
+
+    def find(self, kind, dim, nc, rows, cols, v3):
+        """The entry for a geometry, or None (kind 0 gemv, 1 prefill)."""
+        e = ProfileEntry()
+        if lib().sparkmv_profile_find(self.h, kind, dim, nc, rows, cols, v3, ctypes.byref(e)) != 0:
+            return None
+        return e
+
+
+def profile_write(path, artifact, gpu, driver, entries):
+    arr = (ProfileEntry * max(1, len(entries)))(*entries)
+    check(lib().sparkmv_profile_write(os.fsencode(path), artifact, gpu.encode(), driver.encode(), arr, len(entries)),
+          "profile write")
+
+
+def tune_gemv(mats, iters=20, widths=(64, 128, 256)):
+    """Measure every ready GEMV variant and launch width of each
+    (DeviceContainer) geometry on the current device, stage by stage through
+    the reference ABI (vqg_gemv_t, f32 x), and return one profile entry per
+    geometry: the fastest (tools/vq-tune's gemv sweep)."""
+    torch = _torch()
+    out, seen = [], set()
+    for m in mats:
+        h = m.host
+        key = (h.dim, h.nc, h.rows, h.cols, h.v3)
+        if key in seen:
+            continue
+        seen.add(key)
+        x = torch.randn(h.cols, device="cuda")
+        y = torch.zeros(h.rows, device="cuda")
+        best = None
+        for variant in (1, 2, 3):
+            if not lib().vqg_gemv_ready(h.dim, h.nc, h.rows, h.cols, h.v3, variant):
+                continue
+            for th in (widths if variant != 3 else (0,)):
+                ms = ctypes.c_double()
+                check(lib().vqg_gemv_t(m.stage_ptrs[0], h.dim, h.nc, h.rows, h.cols, h.v3, x.data_ptr(), y.data_ptr(),
+                                       variant, th, iters, ctypes.byref(ms)), "vqg_gemv_t")
+                gbs = h.stage_bytes / (ms.value * 1e-3) / 1e9
+                if best is None or gbs > best[2]:
+                    best = (variant, th, gbs)
+        e = ProfileEntry(kind=0, dim=h.dim, nc=h.nc, rows=h.rows, cols=h.cols, v3=h.v3, variant=best[0],
+                         threads=best[1], rate=best[2])
+        out.append(e)
+    return out
 
 
 class Plan:
