@@ -29,9 +29,9 @@ def rel_l2(a, b):
     return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
 
 
-def build(sm, ref, dev, head_kind, x_dtype):
+def build(sm, ref, dev, head_kind, x_dtype, cfg=None):
     import torch
-    c = CFG
+    c = cfg or CFG
     hd, heads, kvh, hid, inter = c["head_dim"], c["heads"], c["kv_heads"], c["hidden"], c["intermediate"]
     qd, kvd = heads * hd, kvh * hd
     shapes = dict(qkv=(qd + 2 * kvd, hid), attn_gate=(heads, hid), out=(hid, qd), gate=(inter, hid),
@@ -189,3 +189,30 @@ def test_verify_block_and_rollback(sm, ref, dev, head_kind, xd):
     with pytest.raises(sm.SparkmvError):
         model.verify(list(range(9)), 0, logits)
     assert "1..8 tokens" in sm.last_error()
+
+
+@pytest.mark.parametrize("hd,heads,kvh", [(128, 4, 2), (256, 4, 1)], ids=["hd128", "hd256"])
+def test_forward_wider_heads(sm, ref, dev, hd, heads, kvh):
+    """Heads of 128 and 256 elements (two and four per lane in the attention
+    kernels; 256 is the reference model's, with a 64-element rotated prefix on
+    the full layer), 4 query heads per kv head included, against the oracle
+    over tokens past the window, single steps and one verify block."""
+    import torch
+    cfg = dict(CFG, head_dim=hd, heads=heads, kv_heads=kvh)
+    model, oracle = build(sm, ref, dev, "q8_0", sm.X_F32, cfg)
+    one = torch.empty(cfg["vocab"], device=dev)
+    for p, t in enumerate(TOKENS[:4]):
+        model.forward(t, p, one)
+        torch.cuda.synchronize()
+        err = rel_l2(one.cpu().numpy(), oracle.forward(t, p))
+        print(f"hd {hd} pos {p}: relL2 {err:.2e}")
+        assert err <= 1e-5
+    block = [9, 8, 7, 6]
+    logits = torch.empty((len(block), cfg["vocab"]), device=dev)
+    model.verify(block, 4, logits)
+    torch.cuda.synchronize()
+    got = logits.cpu().numpy()
+    for i, t in enumerate(block):
+        err = rel_l2(got[i], oracle.forward(t, 4 + i))
+        print(f"hd {hd} block row {i}: relL2 {err:.2e}")
+        assert err <= 1e-5
