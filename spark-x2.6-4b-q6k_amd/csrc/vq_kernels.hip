@@ -380,10 +380,12 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
             for (int k = 0; k < KXM; k++) {
                 ci[k] = min(base + k * bd + tid, nx - 1);
                 const int n = ci[k] / xq, cc = ci[k] - n * xq;
-                xv[k] = *(const u4v *) ((const uint16_t *) A.x + (size_t) n * A.ldx + 8 * cc);
+                /* a slot wholly past x (uniform) would only repeat the last chunk */
+                if (base + k * bd < nx) xv[k] = *(const u4v *) ((const uint16_t *) A.x + (size_t) n * A.ldx + 8 * cc);
             }
 #pragma unroll
             for (int k = 0; k < KXM; k++) {
+                if (base + k * bd >= nx) continue;
                 const int n = ci[k] / xq, e = 8 * (ci[k] - n * xq);
                 uint8_t * dst = lx + n * A.xstride + 264 * (e >> 7) + 2 * (e & 127);
                 xr_acc_bf16x2(xm2, xv[k].x); xr_acc_bf16x2(xm2, xv[k].y);
