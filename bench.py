@@ -13,7 +13,8 @@ replayed as one HIP graph (native plan, sparkmv_plan_*). Weights and inputs
 are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--mode graph|eager]
-                    [--workload decode-set|ffn-up|q6k-down|verify8|prefill512|forward|verify-block]
+                    [--workload decode-set|ffn-up|q6k-down|verify8|prefill512|forward|verify-block|
+                                decode-set-q6k]
 
 Prints one JSON line (rank 0). The metric is time per token (lower is
 better); achieved GB/s over the algorithmic bytes (container + bf16 x + f32 y
@@ -103,6 +104,67 @@ def build_decode_set(sm, torch, dev, ncol=1, head_rows=VOCAB, layers=LAYERS):
     torch.cuda.synchronize()
     log(f"uploaded in {time.time() - t0:.1f} s total")
     return plan, np.array(op_bytes, dtype=np.float64), op_kind
+
+
+def bench_decode_set_q6k(args, sm, torch, dev):
+    """The same 36-layer N=1 chain with the trunk as ggml Q6_K blocks (the
+    GGUF's trunk, one k-quant launch per matrix) and the tied Q8_0 head."""
+    stream = torch.cuda.Stream(device=dev)
+    t0 = time.time()
+    with torch.cuda.stream(stream):
+        xs = {c: torch.from_numpy(sm.synth_bf16(c, c).view(np.int16).reshape(1, c).copy()).to(dev)
+              for c in (HIDDEN, QD, FFN)}
+        plan = sm.Plan()
+        op_bytes = []
+        with concurrent.futures.ThreadPoolExecutor(min(16, os.cpu_count() or 4)) as ex:
+            futs = [[ex.submit(sm.synth_q6k, seed_of(l, i), r, c) for i, (_, r, c, _) in enumerate(LAYER_MATS)]
+                    for l in range(LAYERS)]
+            head = sm.synth_q8_0(0x4EAD, args.head_rows, HIDDEN)
+            for l in range(LAYERS):
+                # the matrices that share x are stacked by rows into one launch
+                # (q, k, v, head gate; gate, up), as the reference's own fused
+                # qkv tensor is (model.rs:44-55): rows are independent, so each
+                # row's result is the one a separate launch gives
+                for grp in range(4):
+                    idx = [i for i, m in enumerate(LAYER_MATS) if m[3] == grp]
+                    c = LAYER_MATS[idx[0]][2]
+                    r = sum(LAYER_MATS[i][1] for i in idx)
+                    blocks = np.concatenate([futs[l][i].result() for i in idx])
+                    d = torch.from_numpy(blocks).to(dev)
+                    y = torch.zeros(r, device=dev)
+                    plan.add_kquant("q6_k", d, r, c, xs[c], y,
+                                    label=f"L{l}:" + "+".join(LAYER_MATS[i][0] for i in idx))
+                    plan.keep.append((d, y))
+                    op_bytes.append(blocks.nbytes + 2 * c + 4 * r)
+                futs[l] = None
+        hb = torch.from_numpy(head).to(dev)
+        logits = torch.zeros(args.head_rows, device=dev)
+        plan.add_kquant("q8_0", hb, args.head_rows, HIDDEN, xs[HIDDEN], logits, label="head")
+        plan.keep.append((hb, logits, xs))
+        op_bytes.append(head.nbytes + 2 * HIDDEN + 4 * args.head_rows)
+        torch.cuda.synchronize()
+        log(f"generated and uploaded the Q6_K trunk in {time.time() - t0:.1f} s")
+        ms = time_steps(plan, torch, stream, args.steps, args.warmup, args.mode)
+        op_ms = plan.time_ops(stream, iters=max(3, min(args.steps, 10)))
+    op_bytes = np.array(op_bytes, dtype=np.float64)
+    total = float(op_bytes.sum())
+    trunk_b, trunk_ms = float(op_bytes[:-1].sum()), float(op_ms[:-1].sum())
+    log(f"  step {ms * 1e3:.1f} us ({args.mode}); Q6_K kernels {trunk_ms * 1e3:.1f} us over {len(op_ms) - 1} launches "
+        f"({trunk_b / (trunk_ms * 1e-3) / 1e9:.1f} GB/s); head {op_ms[-1] * 1e3:.1f} us")
+    achieved = trunk_b / (trunk_ms * 1e-3) / 1e9
+    return {
+        "metric": "decode matvec us/token (36-layer Q6_K trunk, N=1, tied Q8_0 head)",
+        "value": round(ms * 1e3, 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 dot2 -> f32 (bf16 x)", "data": "synthetic (seeded, random-init Q6_K blocks of the real shapes)",
+        "config": {"workload": "36-layer N=1 decode matvec set, Q6_K trunk + Q8_0 head", "layers": LAYERS,
+                   "hidden": HIDDEN, "ffn": FFN, "launches_per_step": len(op_ms), "mode": args.mode},
+        "achieved_gbps": round(total / (ms * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(total / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
+        "algorithmic_bytes_per_step": int(total),
+        "roofline": {"bound": "hbm", "kernel": "q6k_gemv_staged_kernel", "achieved": round(achieved, 1),
+                     "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
+    }
 
 
 def time_steps(plan, torch, stream, steps, warmup, mode):
@@ -507,7 +569,7 @@ def main():
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--workload", default="decode-set",
                     choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512", "forward",
-                             "verify-block"])
+                             "verify-block", "decode-set-q6k"])
     ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -537,6 +599,8 @@ def main():
             log(f"cpu baseline took {time.time() - t:.1f} s")
     elif args.workload == "prefill512":
         out = bench_prefill(args, sm, torch, dev)
+    elif args.workload == "decode-set-q6k":
+        out = bench_decode_set_q6k(args, sm, torch, dev)
     elif args.workload in ("forward", "verify-block"):
         out = bench_forward(args, sm, torch, dev)
     else:
