@@ -577,8 +577,8 @@ def main():
                     help="first copy MIB MiB on the device (for counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the matvec path runs on a single MI355X, and "
-                                   "multi-GPU sharding (by output rows, zero exchange) is described, not built",
+        print(json.dumps({"error": "one GPU only: the matvec path runs on a single MI355X, and multi-GPU "
+                                   "sharding (by output rows, zero exchange) is described, not built",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch

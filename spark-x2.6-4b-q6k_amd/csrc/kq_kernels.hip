@@ -540,7 +540,7 @@ __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * b
     uint32_t * xr = (uint32_t *) (lds + xoff + xr_off((XF32 ? 2 : 1) * ncol * xst));
     uint32_t xm = 0;
     if (wv >= rpw) {
-        /* x: the x waves' loads, LDS stores and range verdicts, complete
+        /* x: the x waves' loads, LDS stores and range flags, complete
          * before the barrier */
         xm = kq_stage_x_by<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst, threadIdx.x - 64 * rpw, 64 * xw);
         xr_note_f16(xr, xm);

@@ -212,7 +212,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
     const uint32_t cbb = (uint32_t) A.nc * 8u;
     uint8_t * lx = lds + NST * cbb;
     float * red = (float *) (lx + (XF32 ? 2 : 1) * A.ncol * A.xstride);
-    /* the x range verdicts, after the reduction area */
+    /* the x range flags, after the reduction area */
     uint32_t * xr = (uint32_t *) (lds + xr_off(NST * cbb + (XF32 ? 2 : 1) * A.ncol * A.xstride +
                                                (A.threads >> 6) * kRedStride * 4));
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;

@@ -24,8 +24,8 @@
  * non-finite, and y with it, as in an f32 product; other columns keep their
  * precision.
  *
- * LDS: kXrWords words per workgroup (16 wave verdicts, 16 wave maxima), at
- * a 16-byte aligned offset (xr_off), so the verdicts come back in four
+ * LDS: kXrWords words per workgroup (16 wave flag words, 16 wave maxima), at
+ * a 16-byte aligned offset (xr_off), so the flagss come back in four
  * 16-byte reads. */
 #pragma once
 
@@ -68,7 +68,7 @@ __device__ __forceinline__ void xr_put(uint32_t * xr, bool over, bool big, bool 
 }
 
 /* Every wave, in uniform control flow, before the staging barrier: its
- * verdict from the largest |x| m that each lane staged, as f32 bits. */
+ * flags from the largest |x| m that each lane staged, as f32 bits. */
 __device__ __forceinline__ void xr_note(uint32_t * xr, uint32_t m) { xr_put(xr, m >= kXrOver, m >= kXrLow, m != 0u); }
 
 /* The same from the largest converted value, as f16 bits (2^15 is 0x7800,
@@ -93,7 +93,7 @@ __device__ __forceinline__ bool xr_out(const uint32_t * xr, int first = 0) {
     return (b & 1u) || (!(b & 2u) && (b & 4u));
 }
 
-/* The same from one word per lane, lane i holding wave i's verdict: one
+/* The same from one word per lane, lane i holding wave i's flags: one
  * LDS read and three ballots. */
 __device__ __forceinline__ bool xr_out_lanes(uint32_t w, int first = 0) {
     const int lane = (int) (threadIdx.x & 63u), nw = (int) (blockDim.x >> 6);

@@ -7,7 +7,8 @@ Sources of truth used here, none of them the oracle's own formulas:
   * numpy float32 sequential accumulation (np.add.accumulate) for the
     fused dot_row order;
   * hand-computed known answers for the 8-lane dot and for the Q6_K / Q8_0
-    block layouts (no reference code exists for those; see DESIGN.md);
+    block layouts (the reference holds no code for those: its k-quant
+    kernels come from ggml, which it does not vendor);
   * brute force on tiny inputs (pack known indices, read them back).
 """
 import glob
