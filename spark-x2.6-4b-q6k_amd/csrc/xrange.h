@@ -25,8 +25,9 @@
  * precision.
  *
  * LDS: kXrWords words per workgroup (16 wave flag words, 16 wave maxima), at
- * a 16-byte aligned offset (xr_off), so the flagss come back in four
- * 16-byte reads. */
+ * a 16-byte aligned offset (xr_off): the VQ kernels read all flag words in
+ * four 16-byte reads (xr_out), the k-quant kernels one word per lane
+ * (xr_out_lanes). */
 #pragma once
 
 #include <hip/hip_runtime.h>
