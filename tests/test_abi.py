@@ -160,3 +160,22 @@ def test_synth_is_deterministic(sm):
 def test_stage_bytes_agree(sm, ref):
     for args in [(1, 10240, 2560, 4, 4096), (1, 16, 2560, 4, 8192), (0, 3, 16, 4, 512), (1, 5, 12, 4, 1024)]:
         assert sm.lib().sparkmv_stage_bytes(*args) == ref.stage_bytes(*args)
+
+
+def test_model_config_refusals(sm):
+    """sparkmv_model_create refuses a configuration before touching the
+    device: each bad field with its own message."""
+    import ctypes
+    good = dict(hidden=256, layers=2, heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=320, eps=1e-6,
+                sliding_window=3, rope_full_theta=5e6, rope_full_partial=0.25, rope_slide_theta=1e4,
+                rope_slide_partial=1.0, max_ctx=16, x_dtype=sm.X_F32, dim=4, nc=4096, nstages=2, v3=1)
+    for bad, msg in ((dict(heads=3), "multiple of kv_heads"), (dict(head_dim=96), "not 64, 128 or 256"),
+                     (dict(heads=16, kv_heads=2), "more than 4 query heads"), (dict(max_ctx=10 ** 6), "is above"),
+                     (dict(x_dtype=7), "unknown x dtype"), (dict(nstages=5), "outside 1..4"),
+                     (dict(eps=0.0), "eps must be positive"), (dict(vocab=0), "non-positive"),
+                     (dict(rope_full_partial=0.05), "not a multiple")):
+        cfg = sm.ModelCfg(**dict(good, **bad))
+        if bad == dict(rope_full_partial=0.05):
+            cfg = sm.ModelCfg(**dict(good, head_dim=256, rope_full_partial=0.05))   # 12 rotated: half 6, lanes hold 4
+        assert not sm.lib().sparkmv_model_create(ctypes.byref(cfg)), bad
+        assert msg in sm.last_error(), (bad, sm.last_error())
