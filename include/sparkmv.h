@@ -204,6 +204,51 @@ int sparkmv_plan_launch(void * plan, void * stream);
  * op_ms receives sparkmv_plan_size(plan) values. */
 int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms);
 
+/* ---- decode chain: the per-token matvec chain as ONE persistent launch ----
+ * Replaces the launch-by-launch chain of tools/vq/gpu/vq-model-gpu.cu:776-835
+ * (gemv calls :795-833; rms_norm :364-380, gelu-mul :404-414 between them)
+ * with one launch of one workgroup per CU that walks the op list. An op
+ * that waits (wait = 1) reads only what every earlier op has published:
+ * the dependency between matvecs is a device-scope flag per workgroup,
+ * polled with bounded waits. Each op's input transform runs inside its
+ * staging: x_mode 0 takes bf16 x as is, 1 rounds f32 x to bf16, 2 applies
+ * rms_norm to f32 x (f64 sum of squares, tools/vq-runtime/src/model.rs:236-245;
+ * norm_w may be NULL for weight 1) and rounds to bf16. Each matrix writes
+ * y = y_add + W x (y_add may be NULL) in f32 and, when y_bf16 is set, a bf16
+ * copy. With act set, the op is a gate/up pair: two matrices of equal rows,
+ * and act[r] = bf16(gelu(y0[r]) * y1[r]) with exact-erf gelu (model.rs:253-258).
+ * x_out, when set, receives the staged bf16 x (the op's actual input).
+ * Geometry: DQV3, dim 4, two stages, 12-bit indices (an even nc of 2050..4096), columns a multiple
+ * of 128 up to 16384, 4-byte aligned stages. A chain needs the device to
+ * itself while it runs (every workgroup resident at once); the launch is
+ * asynchronous and can be captured into a HIP graph. */
+typedef struct {
+    const void * stages[4];   /* device stage payloads (two used) */
+    float * y;                /* f32 output, rows values (may be NULL if y_bf16 is set, or for a pair) */
+    uint16_t * y_bf16;        /* bf16 copy of y (may be NULL) */
+    const float * y_add;      /* addend (may be NULL; ignored for a pair) */
+    int rows;
+} sparkmv_chain_matrix;
+void * sparkmv_chain_create(void);
+void sparkmv_chain_destroy(void * chain);
+int sparkmv_chain_size(void * chain);
+/* Waves per workgroup (8, 12 or 16), macro steps of index words each wave
+ * keeps in flight (2 or 4), and the units per workgroup the shape search
+ * aims for; applies at the next launch. */
+int sparkmv_chain_tune(void * chain, int waves, int look, int min_units);
+int sparkmv_chain_add_vq(void * chain, const sparkmv_chain_matrix * mats, int nmat, int nstages, int dim, int nc,
+                         int cols, int v3, const void * x, int x_mode, const float * norm_w, float eps,
+                         uint16_t * x_out, uint16_t * act, int wait);
+/* An op with no matrix: out = bf16(rms_norm(x)) over n values (the head's input). */
+int sparkmv_chain_add_norm(void * chain, const float * x, int n, const float * norm_w, float eps, uint16_t * out,
+                           int wait);
+int sparkmv_chain_launch(void * chain, void * stream);
+/* 0, or -1 if a wait of any launch so far gave up (flags are then cleared);
+ * synchronizes the device. */
+int sparkmv_chain_status(void * chain);
+/* The shape chosen for op i: MFMA parts S, K chunks C, macro steps per unit. */
+int sparkmv_chain_op_shape(void * chain, int i, int * S, int * C, int * msc);
+
 /* ---- weight artifacts (host memory) ----
  * GGUF v2/v3 (ggml's layout), the reader of tools/dspark/src/gguf.rs:95-190
  * (Gguf::open, tensor_bytes, get_u64/get_f32/get_str/get_arr), extended to

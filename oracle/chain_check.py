@@ -1,0 +1,117 @@
+"""Oracle checks of a decode chain's outputs (sparkmv.DecodeChain).
+
+Test infrastructure only: tests/ and bench.py's output check use it as the
+checker; the product library never imports it.
+
+Every op of the chain is checked from what the GPU actually read: the
+inputs are rebuilt from the chain's own intermediate buffers with the
+reference's transforms (rms_norm model.rs:236-245, gelu model.rs:253-258,
+bf16 rounding to nearest even as the activations are stored), and each
+matvec is compared with the oracle's bit-exact decode of the container
+(lib.rs:197-211) times that input in f64 — the reference's own gate method
+(tools/vq/gpu/decode-gpu.c:469-484). The Q8_0 head is compared on sampled
+rows with the closed-form dequant (ggml block layout, 34 B per 32 weights).
+"""
+import numpy as np
+
+import forward as fw
+import sparkref as ref
+
+F32 = np.float32
+
+
+def bf16_bits(x):
+    """f32 -> bf16 bits, round to nearest even; NaN -> quiet NaN."""
+    u = np.ascontiguousarray(x, dtype=F32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint32)
+    return r.astype(np.uint16)
+
+
+def bf16_f32(bits):
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(F32)
+
+
+def rel_l2(got, want):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    den = np.linalg.norm(want)
+    return float(np.linalg.norm(got - want) / (den if den > 0 else 1.0))
+
+
+def norm_bf16(h, eps):
+    """bf16(rms_norm(h)) with weight 1, as the chain's staging computes it."""
+    return bf16_bits(fw.rms_norm(np.asarray(h, F32), np.ones(h.size, F32), eps))
+
+
+def gelu_mul_bf16(gate, up):
+    return bf16_bits((fw.gelu(gate) * np.asarray(up, F32)).astype(F32))
+
+
+def _u16(t):
+    return t.detach().cpu().numpy().view(np.uint16)
+
+
+def _f32(t):
+    return t.detach().cpu().numpy().astype(F32)
+
+
+def check_decode_chain(dc, host_layers, head_blocks, layers, head_sample=4096, seed=1, xouts=None):
+    """Check layers `layers` of a DecodeChain and a sample of its head rows.
+
+    host_layers[l][name] are the containers' host bytes (DECODE_MATS names).
+    xouts, when given, is the list of per-op staged-x tensors (x_out), and
+    the rebuilt inputs are also compared with them. Returns a dict: per op
+    kind the largest relative L2 error of the matvec, and per rebuilt input
+    the number of bf16 values that differ from the GPU's."""
+    out = {"q+k+v+g": 0.0, "o": 0.0, "gate+up": 0.0, "down": 0.0, "head": 0.0,
+           "x_mismatch": 0, "act_mismatch": 0, "q16_mismatch": 0, "hn_mismatch": 0}
+    eps = dc.eps
+
+    def mv(name, l, x):
+        W = ref.decode(host_layers[l][name])
+        return ref.matvec_f64(W, np.asarray(x, F32))
+
+    for l in layers:
+        h = _f32(dc.h[l])
+        hm = _f32(dc.hm[l])
+        h1 = _f32(dc.h[l + 1])
+        xa = norm_bf16(h, eps)
+        if xouts is not None:
+            out["x_mismatch"] += int(np.sum(_u16(xouts[4 * l]) != xa))
+        xa_f = bf16_f32(xa)
+        for name, buf in (("q", dc.q), ("k", dc.k), ("v", dc.v), ("g", dc.g)):
+            out["q+k+v+g"] = max(out["q+k+v+g"], rel_l2(_f32(buf[l]), mv(name, l, xa_f)))
+        q16 = _u16(dc.q16[l])
+        out["q16_mismatch"] += int(np.sum(q16 != bf16_bits(_f32(dc.q[l]))))
+        y = mv("o", l, bf16_f32(q16))
+        out["o"] = max(out["o"], float(np.linalg.norm(hm - (h.astype(np.float64) + y)) / max(np.linalg.norm(y), 1e-30)))
+        xc = norm_bf16(hm, eps)
+        if xouts is not None:
+            out["x_mismatch"] += int(np.sum(_u16(xouts[4 * l + 2]) != xc))
+        xc_f = bf16_f32(xc)
+        gate, up = _f32(dc.gate[l]), _f32(dc.up[l])
+        out["gate+up"] = max(out["gate+up"], rel_l2(gate, mv("gate", l, xc_f)), rel_l2(up, mv("up", l, xc_f)))
+        act = _u16(dc.act[l])
+        out["act_mismatch"] += int(np.sum(act != gelu_mul_bf16(gate, up)))
+        y = mv("down", l, bf16_f32(act))
+        out["down"] = max(out["down"],
+                          float(np.linalg.norm(h1 - (hm.astype(np.float64) + y)) / max(np.linalg.norm(y), 1e-30)))
+    hL = _f32(dc.h[dc.L])
+    hn = _u16(dc.hn)
+    out["hn_mismatch"] = int(np.sum(hn != norm_bf16(hL, eps)))
+    rng = np.random.default_rng(seed)
+    rows = np.sort(rng.choice(dc.head_rows, size=min(head_sample, dc.head_rows), replace=False))
+    hid = dc.hidden
+    blk = hid // 32 * 34
+    sub = np.ascontiguousarray(np.asarray(head_blocks).reshape(dc.head_rows, blk)[rows]).reshape(-1)
+    Wh = ref.q8_0_dequant(sub, len(rows), hid)
+    want = Wh.astype(np.float64) @ bf16_f32(hn).astype(np.float64)
+    out["head"] = rel_l2(_f32(dc.logits)[rows], want)
+    return out
+
+
+def worst_matvec(res):
+    return max(res[k] for k in ("q+k+v+g", "o", "gate+up", "down", "head"))
+

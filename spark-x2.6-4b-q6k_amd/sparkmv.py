@@ -75,6 +75,15 @@ class ProfileEntry(ctypes.Structure):
                 ("bn", ctypes.c_int), ("bk", ctypes.c_int), ("rate", ctypes.c_double)]
 
 
+class ChainMatrix(ctypes.Structure):
+    _fields_ = [("stages", ctypes.c_void_p * 4), ("y", ctypes.c_void_p), ("y_bf16", ctypes.c_void_p),
+                ("y_add", ctypes.c_void_p), ("rows", ctypes.c_int)]
+
+
+# chain op input transforms (sparkmv_chain_add_vq x_mode)
+X_MODE_BF16, X_MODE_F32, X_MODE_NORM = 0, 1, 2
+
+
 # ggml tensor types the GGUF reader hands out
 GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q6_K, GGML_BF16 = 0, 1, 8, 14, 30
 
@@ -121,6 +130,16 @@ SIGNATURES = {
     "sparkmv_plan_capture": (_I, [_P, _P]),
     "sparkmv_plan_launch": (_I, [_P, _P]),
     "sparkmv_plan_time_ops": (_I, [_P, _P, _I, _D]),
+    "sparkmv_chain_create": (_P, []),
+    "sparkmv_chain_destroy": (None, [_P]),
+    "sparkmv_chain_size": (_I, [_P]),
+    "sparkmv_chain_tune": (_I, [_P, _I, _I, _I]),
+    "sparkmv_chain_add_vq": (_I, [_P, ctypes.POINTER(ChainMatrix), _I, _I, _I, _I, _I, _I, _P, _I, _P,
+                                  ctypes.c_float, _P, _P, _I]),
+    "sparkmv_chain_add_norm": (_I, [_P, _P, _I, _P, ctypes.c_float, _P, _I]),
+    "sparkmv_chain_launch": (_I, [_P, _P]),
+    "sparkmv_chain_status": (_I, [_P]),
+    "sparkmv_chain_op_shape": (_I, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "sparkmv_gguf_open": (_P, [ctypes.c_char_p]),
     "sparkmv_gguf_close": (None, [_P]),
     "sparkmv_gguf_version": (_I, [_P]),
@@ -699,3 +718,140 @@ class Plan:
         out = (ctypes.c_double * n)()
         check(lib().sparkmv_plan_time_ops(self.h, _stream_ptr(stream), iters, out), "plan time")
         return np.array(out[:], dtype=np.float64)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+class Chain:
+    """A chain of VQ matvecs run as one persistent launch (sparkmv_chain_*).
+    Each op waits (wait=True) until every workgroup has published the ops
+    before it; holds references to every tensor it uses."""
+
+    def __init__(self):
+        self.h = lib().sparkmv_chain_create()
+        self.keep = []
+        self.labels = []
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().sparkmv_chain_destroy(self.h)
+            self.h = None
+
+    def __len__(self):
+        return lib().sparkmv_chain_size(self.h)
+
+    def tune(self, waves=16, look=2, min_units=16):
+        check(lib().sparkmv_chain_tune(self.h, waves, look, min_units), "chain tune")
+
+    def add_vq(self, mats, x, x_mode, ys=None, ys_bf16=None, y_add=None, norm_w=None, eps=1e-6, x_out=None,
+               act=None, wait=True, label="vq"):
+        """mats: DeviceContainers sharing x (two stages, dim 4, DQV3). x: the
+        input (bf16 as int16/uint16 for X_MODE_BF16, f32 otherwise). ys,
+        ys_bf16, y_add: per matrix tensors or None. act: bf16 output of a
+        gate/up pair (mats = [gate, up])."""
+        n = len(mats)
+        ys = ys or [None] * n
+        ys_bf16 = ys_bf16 or [None] * n
+        y_add = y_add or [None] * n
+        arr = (ChainMatrix * n)()
+        for i, m in enumerate(mats):
+            for s_, p in enumerate(m.stage_ptrs):
+                arr[i].stages[s_] = p
+            arr[i].y = _ptr(ys[i])
+            arr[i].y_bf16 = _ptr(ys_bf16[i])
+            arr[i].y_add = _ptr(y_add[i])
+            arr[i].rows = m.rows
+        h = mats[0].host
+        check(lib().sparkmv_chain_add_vq(self.h, arr, n, h.nstages, h.dim, h.nc, h.cols, h.v3, x.data_ptr(), x_mode,
+                                         _ptr(norm_w), eps, _ptr(x_out), _ptr(act), int(wait)), "chain add vq")
+        self.keep.append((mats, x, ys, ys_bf16, y_add, norm_w, x_out, act))
+        self.labels.append(label)
+
+    def add_norm(self, x, out, norm_w=None, eps=1e-6, wait=True, label="norm"):
+        check(lib().sparkmv_chain_add_norm(self.h, x.data_ptr(), x.numel(), _ptr(norm_w), eps, out.data_ptr(),
+                                           int(wait)), "chain add norm")
+        self.keep.append((x, out, norm_w))
+        self.labels.append(label)
+
+    def launch(self, stream=None):
+        check(lib().sparkmv_chain_launch(self.h, _stream_ptr(stream)), "chain launch")
+
+    def status(self):
+        check(lib().sparkmv_chain_status(self.h), "chain")
+
+    def op_shape(self, i):
+        S, C, msc = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib().sparkmv_chain_op_shape(self.h, i, ctypes.byref(S), ctypes.byref(C), ctypes.byref(msc)),
+              "chain shape")
+        return S.value, C.value, msc.value
+
+
+# The decode token's matvecs in the order the forward issues them
+# (tools/vq-runtime/src/model.rs:481-590; tools/vq/gpu/vq-model-gpu.cu:776-835).
+DECODE_MATS = ("q", "k", "v", "g", "o", "gate", "up", "down")
+
+
+class DecodeChain:
+    """The per-token matvec chain of the decode forward, without attention,
+    as one chain launch plus the tied Q8_0 head:
+
+        per layer l (h[l] the f32 residual):
+          q, k, v, g = W_qkvg  bf16(rms_norm(h[l]))         one op, four matrices
+          hm[l]      = h[l]  + W_o    bf16(q)                 attention left out: o reads q
+          gate, up   = W_gu   bf16(rms_norm(hm[l]))           a pair: act = bf16(gelu(gate) * up)
+          h[l + 1]   = hm[l] + W_down act
+        hn = bf16(rms_norm(h[L])); logits = Q8_0 head . hn    (a second launch)
+
+    Every op waits for the one before it, as in the forward. Every
+    intermediate is kept in its own buffer, so each op can be checked from
+    what the GPU actually read. layers: per layer a dict of DeviceContainers
+    keyed by DECODE_MATS; head: device Q8_0 blocks (head_rows x hidden)."""
+
+    def __init__(self, layers, head, head_rows, h0, eps=1e-6, device="cuda", record_inputs=False):
+        """record_inputs: every op also writes its staged bf16 input to
+        self.xouts[op] (4 ops per layer), for checks."""
+        torch = _torch()
+        self.L = len(layers)
+        self.layers = layers
+        self.eps = eps
+        hid = layers[0]["q"].cols
+        self.hidden = hid
+        qd, kvd, gd = layers[0]["q"].rows, layers[0]["k"].rows, layers[0]["g"].rows
+        ffn = layers[0]["gate"].rows
+        L = self.L
+        z = lambda *shape: torch.zeros(*shape, device=device)  # noqa: E731
+        zi = lambda *shape: torch.zeros(*shape, dtype=torch.int16, device=device)  # noqa: E731
+        self.h = z(L + 1, hid)
+        self.h[0].copy_(h0)
+        self.hm = z(L, hid)
+        self.q, self.k, self.v, self.g = z(L, qd), z(L, kvd), z(L, kvd), z(L, gd)
+        self.q16 = zi(L, qd)
+        self.gate, self.up = z(L, ffn), z(L, ffn)
+        self.act = zi(L, ffn)
+        self.hn = zi(hid)
+        self.head, self.head_rows = head, head_rows
+        self.logits = z(head_rows)
+        self.xouts = None
+        if record_inputs:
+            self.xouts = [zi(n) for _ in range(L) for n in (hid, qd, hid, ffn)]
+        xo = (lambda i: self.xouts[i]) if record_inputs else (lambda i: None)  # noqa: E731
+        c = Chain()
+        for l, m in enumerate(layers):
+            c.add_vq([m["q"], m["k"], m["v"], m["g"]], self.h[l], X_MODE_NORM,
+                     ys=[self.q[l], self.k[l], self.v[l], self.g[l]], ys_bf16=[self.q16[l], None, None, None],
+                     eps=eps, x_out=xo(4 * l), wait=l > 0, label=f"L{l}:q+k+v+g")
+            c.add_vq([m["o"]], self.q16[l], X_MODE_BF16, ys=[self.hm[l]], y_add=[self.h[l]], x_out=xo(4 * l + 1),
+                     label=f"L{l}:o")
+            c.add_vq([m["gate"], m["up"]], self.hm[l], X_MODE_NORM, ys=[self.gate[l], self.up[l]], eps=eps,
+                     act=self.act[l], x_out=xo(4 * l + 2), label=f"L{l}:gate+up")
+            c.add_vq([m["down"]], self.act[l], X_MODE_BF16, ys=[self.h[l + 1]], y_add=[self.hm[l]],
+                     x_out=xo(4 * l + 3), label=f"L{l}:down")
+        c.add_norm(self.h[L], self.hn, eps=eps, label="final norm")
+        self.chain = c
+
+    def launch(self, stream=None):
+        self.chain.launch(stream)
+        kquant_gemv("q8_0", self.head, self.head_rows, self.hidden, self.hn.view(1, -1), self.logits.view(1, -1),
+                    stream=stream)

@@ -179,3 +179,40 @@ def test_model_config_refusals(sm):
             cfg = sm.ModelCfg(**dict(good, head_dim=256, rope_full_partial=0.05))   # 12 rotated: half 6, lanes hold 4
         assert not sm.lib().sparkmv_model_create(ctypes.byref(cfg)), bad
         assert msg in sm.last_error(), (bad, sm.last_error())
+
+
+def test_chain_refusals(sm):
+    """sparkmv_chain_add_vq refuses what the chain kernel cannot run, before
+    any device call: indices other than 12-bit, columns that are not a
+    multiple of 128, unaligned stages, a pair of unequal row counts, a
+    matrix without an output, and tuning outside the built kernels."""
+    import ctypes
+    h = sm.lib().sparkmv_chain_create()
+    try:
+        def mats(n, rows=(64, 64), align=0, out=True):
+            arr = (sm.ChainMatrix * n)()
+            for i in range(n):
+                arr[i].stages[0] = 0x10000 + align
+                arr[i].stages[1] = 0x20000
+                arr[i].y = 0x30000 if out else None
+                arr[i].rows = rows[i]
+            return arr
+        x = ctypes.c_void_p(0x40000)
+
+        def add(arr, n, nc=4096, cols=256, act=None, xx=x):
+            return sm.lib().sparkmv_chain_add_vq(h, arr, n, 2, 4, nc, cols, 1, xx, 0, None, 1e-6, None, act, 1)
+
+        for args, msg in (((mats(1), 1, 1024), "12-bit indices"), ((mats(1), 1, 4095), "12-bit indices"),
+                          ((mats(1), 1, 4096, 200), "multiple of 128"), ((mats(1, align=2), 1), "not 4-byte aligned"),
+                          ((mats(1, out=False), 1), "has no output"),
+                          ((mats(2, rows=(64, 32)), 2, 4096, 256, ctypes.c_void_p(0x50000)), "equal row counts"),
+                          ((mats(1), 1, 4096, 256, ctypes.c_void_p(0x50000)), "two matrices"),
+                          ((mats(1), 1, 4096, 256, None, ctypes.c_void_p(0x40002)), "4-byte aligned")):
+            assert add(*args) == -1, msg
+            assert msg in sm.last_error(), (msg, sm.last_error())
+        assert add(mats(1), 1) == 0 and sm.lib().sparkmv_chain_size(h) == 1
+        assert sm.lib().sparkmv_chain_tune(h, 10, 2, 16) == -1 and "8, 12 or 16" in sm.last_error()
+        assert sm.lib().sparkmv_chain_tune(h, 16, 3, 16) == -1 and "2 or 4" in sm.last_error()
+        assert sm.lib().sparkmv_chain_tune(h, 12, 4, 24) == 0
+    finally:
+        sm.lib().sparkmv_chain_destroy(h)
