@@ -64,17 +64,40 @@ def algorithmic_bytes_vq(nbytes_container, rows, cols, ncol=1):
     return nbytes_container + 2 * cols * ncol + 4 * rows * ncol
 
 
-def build_decode_set(sm, torch, dev, ncol=1, head_rows=VOCAB, layers=LAYERS):
-    """Generate, upload and record the per-token chain. Returns the plan and
-    the byte accounting per op."""
+class DecodeSet:
+    """The per-token decode matvec set as recorded: the plan, every op's
+    output tensor, the shared inputs, and (for the layers asked for) the
+    host containers, so the outputs can be checked after timing."""
+
+    def __init__(self):
+        self.plan = None
+        self.op_bytes = None
+        self.op_kind = []
+        self.hosts = {}      # layer -> list of container bytes (LAYER_MATS order), for kept layers
+        self.ys = {}         # layer -> list of (matrix index, y tensor [ncol, >= rows])
+        self.xs = {}         # cols -> (device bf16 [ncol, cols], host f32 [ncol, cols])
+        self.head = None     # host Q8_0 blocks
+        self.head_rows = 0
+        self.logits = None
+        self.ncol = 1
+
+
+def build_decode_set(sm, torch, dev, ncol=1, head_rows=VOCAB, layers=LAYERS, keep_hosts=()):
+    """Generate, upload and record the per-token chain. Returns a DecodeSet;
+    the host containers of the layers in keep_hosts stay in it."""
+    ds = DecodeSet()
+    ds.ncol, ds.head_rows = ncol, head_rows
     t0 = time.time()
     with concurrent.futures.ThreadPoolExecutor(min(16, os.cpu_count() or 4)) as ex:
         hosts = list(ex.map(lambda l: gen_layer(sm, l), range(layers)))
         head_future = ex.submit(sm.synth_q8_0, 0x4EAD, head_rows, HIDDEN)
         head = head_future.result()
     log(f"generated {layers} layers + head in {time.time() - t0:.1f} s")
-    xs = {c: torch.from_numpy(sm.synth_bf16(c, ncol * c).view(np.int16).reshape(ncol, c).copy()).to(dev)
-          for c in (HIDDEN, QD, FFN)}
+    for c in (HIDDEN, QD, FFN):
+        xb = sm.synth_bf16(c, ncol * c)
+        ds.xs[c] = (torch.from_numpy(xb.view(np.int16).reshape(ncol, c).copy()).to(dev),
+                    sm.bf16_to_f32(xb).reshape(ncol, c))
+    xs = {c: v[0] for c, v in ds.xs.items()}
     plan = sm.Plan()
     op_bytes, op_kind = [], []
     devs = []
@@ -94,6 +117,9 @@ def build_decode_set(sm, torch, dev, ncol=1, head_rows=VOCAB, layers=LAYERS):
                         label=f"L{l}:" + "+".join(LAYER_MATS[i][0] for i in idx))
             op_bytes.append(sum(algorithmic_bytes_vq(hosts[l][i].nbytes, LAYER_MATS[i][1], cols, ncol) for i in idx))
             op_kind.append("vq")
+        ds.ys[l] = list(enumerate(ys))
+        if l in keep_hosts:
+            ds.hosts[l] = hosts[l]
         hosts[l] = None
     hb = torch.from_numpy(head).to(dev)
     logits = torch.zeros(ncol, head_rows, device=dev)
@@ -103,7 +129,19 @@ def build_decode_set(sm, torch, dev, ncol=1, head_rows=VOCAB, layers=LAYERS):
     plan.keep.append((devs, hb, logits, xs))
     torch.cuda.synchronize()
     log(f"uploaded in {time.time() - t0:.1f} s total")
-    return plan, np.array(op_bytes, dtype=np.float64), op_kind
+    ds.plan, ds.op_bytes, ds.op_kind = plan, np.array(op_bytes, dtype=np.float64), op_kind
+    ds.head, ds.logits = head, logits
+    return ds
+
+
+def check_decode_set(ds, layers):
+    """The checker (oracle, after timing): each kept layer's outputs against
+    the oracle's bit-exact decode times x in f64, every row and column, and
+    every head row against the closed-form Q8_0 dot. Returns the largest
+    relative L2 error per launch group."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import chain_check as cc
+    return cc.check_decode_set(ds, LAYER_MATS, layers)
 
 
 def bench_decode_set_q6k(args, sm, torch, dev):
@@ -227,10 +265,13 @@ def cpu_baseline_decode_set(sample_layers=LAYERS, head_rows=VOCAB, reps=9):
 def bench_decode_set(args, sm, torch, dev):
     stream = torch.cuda.Stream(device=dev)
     ncol = 8 if args.workload == "verify8" else 1
+    check_layers = (0, LAYERS // 2, LAYERS - 1) if args.check else ()
     with torch.cuda.stream(stream):
-        plan, op_bytes, op_kind = build_decode_set(sm, torch, dev, ncol=ncol, head_rows=args.head_rows)
+        ds = build_decode_set(sm, torch, dev, ncol=ncol, head_rows=args.head_rows, keep_hosts=check_layers)
+        plan, op_bytes, op_kind = ds.plan, ds.op_bytes, ds.op_kind
         ms = time_steps(plan, torch, stream, args.steps, args.warmup, args.mode)
         op_ms = plan.time_ops(stream, iters=max(3, min(args.steps, 10)))
+        torch.cuda.synchronize()
     total_bytes = float(op_bytes.sum())
     vq = np.array([k == "vq" for k in op_kind])
     vq_bytes, vq_ms = float(op_bytes[vq].sum()), float(op_ms[vq].sum())
@@ -281,6 +322,14 @@ def bench_decode_set(args, sm, torch, dev):
                      "head_q8_0": {"us": round(head_ms * 1e3, 2),
                                    "gbps": round(float(op_bytes[~vq].sum()) / (head_ms * 1e-3) / 1e9, 1)}},
     }
+    if check_layers:
+        t = time.time()
+        res = check_decode_set(ds, check_layers)
+        log(f"  output check ({time.time() - t:.1f} s): " + ", ".join(f"{k} {v:.2e}" for k, v in res.items()))
+        out["check"] = {"rel_l2_max": max(res.values()), "per_group": {k: float(f"{v:.3e}") for k, v in res.items()},
+                        "layers": list(check_layers), "head_rows": args.head_rows, "columns": ncol,
+                        "method": "outputs of the timed plan vs the oracle's decode x f64 (all rows of the layers "
+                                  "listed, every head row)"}
     return out
 
 
@@ -573,6 +622,8 @@ def main():
     ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-check", dest="check", action="store_false",
+                    help="skip the oracle check of the timed outputs")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB on the device (for counter calibration)")
     args = ap.parse_args()

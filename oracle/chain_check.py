@@ -9,8 +9,9 @@ reference's transforms (rms_norm model.rs:236-245, gelu model.rs:253-258,
 bf16 rounding to nearest even as the activations are stored), and each
 matvec is compared with the oracle's bit-exact decode of the container
 (lib.rs:197-211) times that input in f64 — the reference's own gate method
-(tools/vq/gpu/decode-gpu.c:469-484). The Q8_0 head is compared on sampled
-rows with the closed-form dequant (ggml block layout, 34 B per 32 weights).
+(tools/vq/gpu/decode-gpu.c:469-484). The Q8_0 head is compared on every row
+with the closed-form dequant (ggml block layout, 34 B per 32 weights) and the
+runtime's f32 dot (model.rs:209-234).
 """
 import numpy as np
 
@@ -57,8 +58,8 @@ def _f32(t):
     return t.detach().cpu().numpy().astype(F32)
 
 
-def check_decode_chain(dc, host_layers, head_blocks, layers, head_sample=4096, seed=1, xouts=None):
-    """Check layers `layers` of a DecodeChain and a sample of its head rows.
+def check_decode_chain(dc, host_layers, head_blocks, layers, xouts=None):
+    """Check layers `layers` of a DecodeChain and every row of its head.
 
     host_layers[l][name] are the containers' host bytes (DECODE_MATS names).
     xouts, when given, is the list of per-op staged-x tensors (x_out), and
@@ -101,17 +102,41 @@ def check_decode_chain(dc, host_layers, head_blocks, layers, head_sample=4096, s
     hL = _f32(dc.h[dc.L])
     hn = _u16(dc.hn)
     out["hn_mismatch"] = int(np.sum(hn != norm_bf16(hL, eps)))
-    rng = np.random.default_rng(seed)
-    rows = np.sort(rng.choice(dc.head_rows, size=min(head_sample, dc.head_rows), replace=False))
-    hid = dc.hidden
-    blk = hid // 32 * 34
-    sub = np.ascontiguousarray(np.asarray(head_blocks).reshape(dc.head_rows, blk)[rows]).reshape(-1)
-    Wh = ref.q8_0_dequant(sub, len(rows), hid)
-    want = Wh.astype(np.float64) @ bf16_f32(hn).astype(np.float64)
-    out["head"] = rel_l2(_f32(dc.logits)[rows], want)
+    want = ref.q8_0_matvec(np.asarray(head_blocks), dc.head_rows, dc.hidden, bf16_f32(hn))
+    out["head"] = rel_l2(_f32(dc.logits), want)
     return out
 
 
 def worst_matvec(res):
     return max(res[k] for k in ("q+k+v+g", "o", "gate+up", "down", "head"))
 
+
+
+def check_decode_set(ds, layer_mats, layers):
+    """The decode-set plan's outputs (bench.py's DecodeSet): every row and
+    column of the kept layers' matvecs against the oracle's decode times x in
+    f64, and every head row against the oracle's closed-form Q8_0 dequant
+    and the runtime's f32 dot (model.rs:209-234). Returns the
+    largest relative L2 error per launch group (q+k+v+g, o, gate+up, down,
+    head), over all columns."""
+    res = {}
+    group_names = {}
+    for i, (name, _, _, grp) in enumerate(layer_mats):
+        group_names.setdefault(grp, []).append(name)
+    for l in layers:
+        for i, y in ds.ys[l]:
+            name, rows, cols, grp = layer_mats[i]
+            W = ref.decode(ds.hosts[l][i]).astype(np.float64)
+            X = ds.xs[cols][1].astype(np.float64)
+            want = X @ W.T                       # [ncol, rows]
+            got = _f32(y)[:, :rows]
+            key = "+".join(group_names[grp])
+            res[key] = max(res.get(key, 0.0), rel_l2(got, want))
+    x = ds.xs[layer_mats[0][2]][1]
+    got = _f32(ds.logits)
+    worst = 0.0
+    for n in range(ds.ncol):
+        want = ref.q8_0_matvec(ds.head, ds.head_rows, x.shape[1], x[n])
+        worst = max(worst, rel_l2(got[n], want))
+    res["head"] = worst
+    return res

@@ -1,0 +1,115 @@
+"""GPU parity at the benchmark's full sizes (the configurations the bench
+times), against the oracle:
+
+  - the 36-layer N=1 decode matvec set at the reference model's real shapes
+    plus the 151,936 x 2560 Q8_0 tied head, every row of every layer and of
+    the head (the plan the bench replays);
+  - the same set with 8 activation columns (speculative verify), every row
+    and column, and the 8-column head equal, column by column and bit for
+    bit, to one-column launches;
+  - the prefill GEMM at 512 tokens for both FFN shapes, 10240 x 2560 and
+    2560 x 10240;
+  - the dependent decode chain (one persistent launch) over 36 real-shape
+    layers, with the head.
+
+Each matvec is compared with the oracle's bit-exact decode times x in f64
+(the reference's gate method, tools/vq/gpu/decode-gpu.c:469-484)."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+TIGHT = 1e-5
+
+
+def _decode_set(sm, dev, ncol):
+    import torch
+    import bench
+    bench.log = lambda *a: print(*a, flush=True)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        ds = bench.build_decode_set(sm, torch, dev, ncol=ncol, keep_hosts=range(bench.LAYERS))
+        ds.plan.run(stream)
+    torch.cuda.synchronize()
+    return bench, ds
+
+
+def test_decode_set_full_size(sm, dev):
+    import chain_check as cc
+    bench, ds = _decode_set(sm, dev, 1)
+    res = cc.check_decode_set(ds, bench.LAYER_MATS, range(bench.LAYERS))
+    print("N=1 decode set, 36 layers + 151936-row head:", res)
+    for k, v in res.items():
+        assert v <= TIGHT, (k, v)
+
+
+def test_verify8_set_full_size(sm, dev):
+    import torch
+    import chain_check as cc
+    bench, ds = _decode_set(sm, dev, 8)
+    res = cc.check_decode_set(ds, bench.LAYER_MATS, range(bench.LAYERS))
+    print("N=8 verify set, 36 layers + 151936-row head:", res)
+    for k, v in res.items():
+        assert v <= TIGHT, (k, v)
+    # the 8-column head gives each column exactly the one-column result
+    hb = torch.from_numpy(ds.head).to(dev)
+    x = ds.xs[bench.HIDDEN][0]
+    for n in range(8):
+        y1 = torch.zeros(1, ds.head_rows, device=dev)
+        sm.kquant_gemv("q8_0", hb, ds.head_rows, bench.HIDDEN, x[n:n + 1], y1)
+        torch.cuda.synchronize()
+        assert torch.equal(y1[0], ds.logits[n]), f"column {n} differs from a one-column launch"
+
+
+@pytest.mark.parametrize("rows,cols", [(10240, 2560), (2560, 10240)])
+def test_prefill_512_full_size(sm, ref, dev, rows, cols):
+    """The prompt GEMM at 512 tokens: two stages folded into one f16 weight
+    before the MFMA, so within 1e-3 (measured about 2e-4)."""
+    import torch
+    ntok = 512
+    data = sm.synth_container(0x9F00 + cols, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    xb = sm.synth_bf16(0x9F10 + cols, ntok * cols).reshape(ntok, cols)
+    X = sm.bf16_to_f32(xb).astype(np.float64)
+    m = sm.DeviceContainer(data, dev)
+    x = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+    y = torch.zeros(ntok, rows, device=dev)
+    m.prefill(x, y)
+    torch.cuda.synchronize()
+    want = X @ W.T
+    got = y.cpu().numpy().astype(np.float64)
+    err = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    worst_tok = max(float(np.linalg.norm(got[t] - want[t]) / np.linalg.norm(want[t])) for t in (0, 1, 63, 64, 511))
+    print(f"prefill {rows}x{cols}x{ntok}: relL2 {err:.2e}, worst checked token {worst_tok:.2e}")
+    assert err <= 1e-3 and worst_tok <= 1e-3
+
+
+def test_decode_chain_full_size(sm, dev):
+    """The dependent chain at the real shapes: layers 0, 17 and 35 checked op
+    by op from the inputs the GPU read, and every head row."""
+    import torch
+    import chain_check as cc
+    import bench
+    import concurrent.futures
+    with concurrent.futures.ThreadPoolExecutor(16) as ex:
+        hosts = list(ex.map(lambda l: bench.gen_layer(sm, l), range(bench.LAYERS)))
+    head = sm.synth_q8_0(0x4EAD, bench.VOCAB, bench.HIDDEN)
+    layers = [{n: sm.DeviceContainer(h, dev) for (n, _, _, _), h in zip(bench.LAYER_MATS, hl)} for hl in hosts]
+    h0 = torch.from_numpy(sm.bf16_to_f32(sm.synth_bf16(0xE0, bench.HIDDEN))).to(dev)
+    dc = sm.DecodeChain(layers, torch.from_numpy(head).to(dev), bench.VOCAB, h0)
+    dc.launch()
+    torch.cuda.synchronize()
+    dc.chain.status()
+    hl = [{n: h for (n, _, _, _), h in zip(bench.LAYER_MATS, hs)} for hs in hosts]
+    res = cc.check_decode_chain(dc, hl, head, (0, 17, 35))
+    print("decode chain, 36 layers:", res)
+    for k in ("q+k+v+g", "o", "gate+up", "down", "head"):
+        assert res[k] <= TIGHT, (k, res)
+    assert res["q16_mismatch"] == 0 and res["act_mismatch"] <= 4 and res["hn_mismatch"] <= 2, res
