@@ -175,6 +175,19 @@ int sparkmv_q8_0_dequant(const void * blocks, int rows, int cols, float * out, v
 int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
                        const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy,
                        int accumulate, void * stream);
+/* The same prefill without any allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). A short
+ * matrix's split-K partial sums go to a fixed device array of 32 MiB that the
+ * library holds on every GPU it runs on until the process ends, instead of
+ * the pool sparkmv_vq_prefill draws from; a call whose split slices would
+ * exceed it fails with a message saying how many bytes it needs. Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race. The first call on a
+ * device looks the array's address up once. */
+int sparkmv_vq_prefill_noalloc(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                               const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy,
+                               int accumulate, void * stream);
 
 /* ---- decode-set plan: a recorded chain of matvec launches ----
  * The per-token matvec chain of the forward (tools/vq/gpu/vq-model-gpu.cu:776-835

@@ -387,29 +387,47 @@ int sparkmv_q8_0_dequant(const void * blocks, int rows, int cols, float * out, v
     return kq_dequant_launch(8, blocks, rows, cols, out, (hipStream_t) stream);
 }
 
-int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
-                       const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy, int accumulate,
-                       void * stream) {
+static int vq_prefill_impl(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                           const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy, int accumulate,
+                           void * stream, int noalloc) {
     if (!stages || !x || !y) { set_error("null pointer passed to prefill"); return -1; }
     if (x_dtype != SPARKMV_X_BF16 && x_dtype != SPARKMV_X_F32) { set_error("unknown x dtype %d", x_dtype); return -1; }
+    if (nstages < 1 || nstages > kMaxStages) { set_error("stage count %d is outside 1..%d", nstages, kMaxStages); return -1; }
+    if (ntok < 1) { set_error("prefill needs at least one token, not %d", ntok); return -1; }
     if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
     if (ldx < cols || ldy < rows) { set_error("ldx/ldy below the matrix extent"); return -1; }
-    for (int i = 0; i < nstages && i < kMaxStages; i++)
+    for (int i = 0; i < nstages; i++)
         if (!stages[i]) { set_error("stage %d payload is null", i); return -1; }
     const Layout L = make_layout(dim, nc, rows, cols, v3);
     const int xf32 = x_dtype == SPARKMV_X_F32;
+    void * ws = nullptr;
+    if (noalloc && prefill_scratch(&ws)) return -1;
     if (prefill_mfma_ready(L, nstages < 2 ? nstages : 2, x, xf32, ldx, 0, ntok)) {
         /* the matrix cores, two stages per launch; later pairs accumulate */
         for (int s0 = 0; s0 < nstages; s0 += 2) {
             const int n = nstages - s0 < 2 ? nstages - s0 : 2;
             if (prefill_mfma_launch(stages + s0, n, L, x, xf32, ldx, 0, ntok, y, ldy, accumulate || s0 > 0,
-                                    (hipStream_t) stream))
+                                    (hipStream_t) stream, ws))
                 return -1;
         }
         return 0;
     }
     return prefill_simple_launch(stages, nstages, L, x, xf32, (size_t) ldx, 1, ntok, y, ldy, accumulate ? 1 : 0,
                                  (hipStream_t) stream);
+}
+
+int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                       const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy, int accumulate,
+                       void * stream) {
+    return vq_prefill_impl(stages, nstages, dim, nc, rows, cols, v3, x, x_dtype, ldx, ntok, y, ldy, accumulate,
+                           stream, 0);
+}
+
+int sparkmv_vq_prefill_noalloc(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
+                               const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy, int accumulate,
+                               void * stream) {
+    return vq_prefill_impl(stages, nstages, dim, nc, rows, cols, v3, x, x_dtype, ldx, ntok, y, ldy, accumulate,
+                           stream, 1);
 }
 
 }  // extern "C"

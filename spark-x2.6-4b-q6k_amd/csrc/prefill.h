@@ -19,7 +19,18 @@ int prefill_simple_launch(const void * const * stages, int nst, const Layout & L
  * matrices split K through a stream-ordered workspace and a fixed-order
  * reduction. */
 int prefill_mfma_ready(const Layout & L, int nst, const void * x, int xf32, int ldx, int xt, int ntok);
+/* fixed_ws: NULL takes split slices from the library's pool; otherwise the
+ * device address of the no-allocation scratch (prefill_scratch), whose size
+ * bounds the split slices. */
 int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
-                        int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s);
+                        int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s,
+                        void * fixed_ws = nullptr);
+
+/* Bytes of the no-allocation prefill's scratch (split-K partial sums), one
+ * array per GPU: the 2560 x 10240 FFN down matrix at 512 tokens needs 26 MB. */
+constexpr size_t kPrefillScratchBytes = 32u << 20;
+/* The scratch array's device address on the current device (looked up once
+ * per device); 0, or -1 with the message set. */
+int prefill_scratch(void ** ptr);
 
 }  // namespace sparkmv

@@ -759,6 +759,30 @@ static int prefill_cw_splits(int rows, int ntok, int nk) {
     return best;
 }
 
+/* The no-allocation form's split slices: one file-scope device array of
+ * kPrefillScratchBytes, which every GPU the library runs on holds until the
+ * process ends. Host code never passes the array's name to a kernel (on the
+ * host it is a stand-in, not a device address): the address comes from
+ * hipGetSymbolAddress, asked once per device with that device current. */
+static __device__ __align__(256) float scratch[kPrefillScratchBytes / sizeof(float)];
+
+int prefill_scratch(void ** ptr) {
+    static void * addr[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail_hip("get device", e);
+    if (dev < 0 || dev >= 64) { set_error("device %d is outside the scratch table", dev); return -1; }
+    if (!addr[dev]) {
+        void * p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return fail_hip("prefill scratch address", e);
+        if (!p) { set_error("prefill scratch has no device address"); return -1; }
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return 0;
+}
+
 /* the split slices come from a pool owned by the library (stream ordered,
  * kept between calls), one per device */
 static int cw_workspace(size_t bytes, hipStream_t s, void ** out) {
@@ -806,7 +830,8 @@ static int prefill_cw_t(const CwArgs & P, int nsplit, hipStream_t s) {
 }
 
 static int prefill_cw_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32,
-                             int ldx, int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s) {
+                             int ldx, int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s,
+                             void * fixed_ws) {
     CwArgs P;
     memset(&P, 0, sizeof P);
     P.st[0] = (const uint8_t *) stages[0];
@@ -823,7 +848,19 @@ static int prefill_cw_launch(const void * const * stages, int nst, const Layout 
     void * ws = nullptr;
     if (nsplit > 1) {
         P.ysplit = (size_t) ntok * L.rows;
-        if (cw_workspace(P.ysplit * nsplit * sizeof(float), s, &ws)) return -1;
+        const size_t need = P.ysplit * nsplit * sizeof(float);
+        if (fixed_ws) {
+            /* every slice is written whole by its split before the reduction
+             * reads it, so the scratch needs no clearing */
+            if (need > kPrefillScratchBytes) {
+                set_error("this prefill splits K %d ways and needs %zu bytes of scratch; the no-allocation "
+                          "prefill holds %zu", nsplit, need, (size_t) kPrefillScratchBytes);
+                return -1;
+            }
+            ws = fixed_ws;
+        } else if (cw_workspace(need, s, &ws)) {
+            return -1;
+        }
         P.y = (float *) ws;
         P.ldy = L.rows;
         P.accumulate = 0;
@@ -850,21 +887,23 @@ static int prefill_cw_launch(const void * const * stages, int nst, const Layout 
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) rc = fail_hip("split reduction launch", e);
         }
-        hipError_t e = hipFreeAsync(ws, s);
-        if (!rc && e != hipSuccess) rc = fail_hip("split workspace release", e);
+        if (!fixed_ws) {
+            hipError_t e = hipFreeAsync(ws, s);
+            if (!rc && e != hipSuccess) rc = fail_hip("split workspace release", e);
+        }
     }
     return rc;
 }
 
 int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32, int ldx,
-                        int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s) {
+                        int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s, void * fixed_ws) {
     if (!prefill_mfma_ready(L, nst, x, xf32, ldx, xt, ntok)) {
         set_error("the MFMA prefill kernel does not take this geometry, stage count or x layout");
         return -1;
     }
     if (ntok <= 0) { set_error("prefill needs at least one token"); return -1; }
     if (prefill_cw_ready(L, nst, x, xf32, ldx, xt, ntok, y, ldy))
-        return prefill_cw_launch(stages, nst, L, x, xf32, ldx, xt, ntok, y, ldy, accumulate, s);
+        return prefill_cw_launch(stages, nst, L, x, xf32, ldx, xt, ntok, y, ldy, accumulate, s, fixed_ws);
     MfmaArgs P;
     memset(&P, 0, sizeof P);
     P.st[0] = (const uint8_t *) stages[0];

@@ -121,6 +121,7 @@ SIGNATURES = {
     "sparkmv_q6k_dequant": (_I, [_P, _I, _I, _P, _P]),
     "sparkmv_q8_0_dequant": (_I, [_P, _I, _I, _P, _P]),
     "sparkmv_vq_prefill": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
+    "sparkmv_vq_prefill_noalloc": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
     "sparkmv_plan_create": (_P, []),
     "sparkmv_plan_destroy": (None, [_P]),
     "sparkmv_plan_size": (_I, [_P]),
