@@ -26,12 +26,23 @@
  *     prefill, and an explicit hipStream_t (passed as void *, NULL = default).
  *     Same return and error convention.
  *
- * Variant numbers for the VQ GEMV (vqg_gemv_ready / _t / _launch_t):
- *   0 auto (fastest ready kernel)    1 generic wave-per-row kernel
- *   2 wave-per-row, codebook in LDS  3 DQV3 dim-4 MFMA block kernel
- * In the reference, `vqg_gemv_t` variant 0 named its shared-memory kernel;
- * every kernel here keeps the codebook on chip, so 0 means auto everywhere.
- * Launch widths (`threads`) must be multiples of 64 (wave64).
+ * Variant numbers. The vqg_* GEMV entry points number variants as the
+ * reference does (decode-gpu.cu:788-797, :808-833, :865-906), so its
+ * runtime and tuner choose what they would choose on CUDA:
+ *   vqg_gemv_ready  3 when the DQV3 block preconditions hold, 2 for dim 4,
+ *                   1 always, 0 when the codebook fits the shared-codebook
+ *                   kernel (160 KB of LDS);
+ *   vqg_gemv_t / vqg_gemv: 0 the shared-codebook kernel (256 wide), 1 the
+ *                   generic wave kernel, 2 the dim-4 path (the MFMA block
+ *                   kernel where it takes the geometry), 3 the block path;
+ *   vqg_gemv_launch / _launch_t: 0 the reference's pick (3 when ready,
+ *                   else 2 for dim 4, else 1), 1-3 as above.
+ * Launch widths are warp multiples (32) up to 1024, as there; a width
+ * rounds up to whole 64-lane waves, which changes only how many rows share
+ * a workgroup, never a result.
+ * The sparkmv_* GEMV entry points number their kernels directly: 0 the
+ * fastest that takes the call, 1 the generic wave kernel, 2 the wave kernel
+ * with the codebook in LDS, 3 the MFMA block kernel (sparkmv_vq_gemv_ready).
  */
 #ifndef SPARKMV_H
 #define SPARKMV_H
@@ -128,6 +139,8 @@ size_t sparkmv_stage_bytes(int v3, int rows, int cols, int dim, int nc);
  * nstages <= 4 pointers); x has ncols <= 16 columns; accumulate 1 adds into y,
  * 0 overwrites it. Replaces the per-stage loop of tools/vq/gpu/vq-model-gpu.cu:651-660
  * (gemv) with the bf16 / N-column forms the reference lacks. variant as above. */
+/* Whether a sparkmv_* GEMV variant (numbering above) takes this geometry. */
+int sparkmv_vq_gemv_ready(int dim, int nc, int rows, int cols, int v3, int variant);
 int sparkmv_vq_gemv(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
                     const void * x, int x_dtype, int ldx, int ncols, float * y, int ldy,
                     int accumulate, int variant, void * stream);

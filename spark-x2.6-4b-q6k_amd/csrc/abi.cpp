@@ -91,11 +91,60 @@ static int timed(F launch, int iters, double * ms) {
     return rc;
 }
 
+/* The reference's DQV3 block-kernel preconditions (decode-gpu.cu:62-64): a
+ * 12-bit main stream, whole 32-index groups, 4-byte aligned row streams. */
+static int v3_blk_ok(const Layout & L) {
+    return L.v3 && L.nbit >= 12 && L.nidx_row % 32 == 0 && L.mrow % 4 == 0 && L.stream_off % 4 == 0;
+}
+
+/* LDS a workgroup may hold (the variant-0 codebook kernel's bound, as the
+ * reference's smem_max() bounds its shared-memory kernel) */
+static const size_t kLdsLimit = 160 * 1024;
+
+/* A reference variant number (decode-gpu.cu:788-797, :808-833, :865-906) as
+ * the kernel that runs it here (VqCall's numbering: 1 the generic wave
+ * kernel, 2 the wave kernel with the codebook in LDS, 3 the MFMA block
+ * kernel, 0 the fastest that takes the call). `timed` is vqg_gemv_t /
+ * vqg_gemv, whose variant 0 is the shared-codebook kernel; the launch forms
+ * read 0 as the reference's pick (3 when the block kernel's preconditions
+ * hold, else 2 for dim 4, else 1). Variant 2 is the dim-4 path (the
+ * fastest dim-4 kernel that takes the geometry); 3 is the block path, which
+ * here is the MFMA kernel for dim 4 and the wave kernel for other dims. */
+static int map_variant(const Layout & L, int variant, int timed) {
+    if (variant == 0 && timed) return 2;
+    if (variant == 0) variant = v3_blk_ok(L) ? 3 : (L.dim == 4 ? 2 : 1);
+    switch (variant) {
+        case 1: return 1;
+        case 2: return L.dim == 4 ? 0 : 1;
+        case 3: return L.dim == 4 ? 0 : ((size_t) L.nc * L.dim * 2 <= kLdsLimit ? 2 : 1);
+        default: return -1;
+    }
+}
+
 static int one_stage_gemv(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x,
-                          float * y, int variant, int threads) {
+                          float * y, int variant, int threads, int timed = 0) {
     if (!width_ok(v3, nc) || !geometry_ok(dim, nc, rows, cols)) return -1;
     if (variant < 0 || variant > 3) { set_error("unknown gemv variant %d", variant); return -1; }
     if (!payload) { set_error("payload is null"); return -1; }
+    const Layout L = make_layout(dim, nc, rows, cols, v3);
+    if (variant == 3 && !v3_blk_ok(L)) { set_error("the DQV3 block kernel does not take this geometry"); return -1; }
+    if (variant == 0 && timed && (size_t) nc * dim * 2 > kLdsLimit) {
+        set_error("a codebook of %d x %d does not fit the shared-codebook kernel", nc, dim);
+        return -1;
+    }
+    /* the reference takes warp multiples (32) up to 1024; a wave here is 64
+     * lanes, so a width rounds up to whole waves (it only sets how many
+     * row-waves share a workgroup, never the arithmetic); the shared-
+     * codebook kernel runs 256 wide, as the reference's does */
+    if (variant == 0 && timed) threads = 256;
+    else if (threads) {
+        if (threads < 32 || threads > 1024 || threads % 32) {
+            set_error("gemv launch width %d is not a warp multiple up to 1024", threads);
+            return -1;
+        }
+        threads = (threads + 63) & ~63;
+    }
+    variant = map_variant(L, variant, timed);
     VqMatDesc m;
     memset(&m, 0, sizeof m);
     m.stages[0] = payload;
@@ -138,7 +187,25 @@ int vqg_driver_version(void) {
     return v;
 }
 
+/* The reference's readiness rules (decode-gpu.cu:788-797): 3 when the block
+ * kernel's preconditions hold, 2 for dim 4, 1 always, 0 when the codebook
+ * fits the shared-codebook kernel. A geometry the launch refuses (cols not a
+ * multiple of dim, a DQV3 codebook past 13 bits, empty) is ready for no
+ * variant. */
 int vqg_gemv_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
+    if (dim <= 0 || nc <= 0 || rows <= 0 || cols <= 0 || cols % dim) return 0;
+    if (v3 && bits_for(nc) > 13) return 0;
+    const Layout L = make_layout(dim, nc, rows, cols, v3);
+    switch (variant) {
+        case 3: return v3_blk_ok(L);
+        case 2: return dim == 4;
+        case 1: return 1;
+        case 0: return (size_t) nc * dim * 2 <= kLdsLimit;
+        default: return 0;
+    }
+}
+
+int sparkmv_vq_gemv_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
     return vq_variant_ready(dim, nc, rows, cols, v3, variant);
 }
 
@@ -146,12 +213,13 @@ int vqg_gemv_t(const void * payload, int dim, int nc, int rows, int cols, int v3
                int variant, int threads, int iters, double * ms) {
     if (!width_ok(v3, nc)) return -1;
     if (rows <= 0 || cols <= 0) { set_error("gemv needs a non-empty matrix"); return -1; }
-    return timed([&] { return one_stage_gemv(payload, dim, nc, rows, cols, v3, x, y, variant, threads); }, iters, ms);
+    return timed([&] { return one_stage_gemv(payload, dim, nc, rows, cols, v3, x, y, variant, threads, 1); }, iters,
+                 ms);
 }
 
 int vqg_gemv(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x, float * y,
              int variant, int iters, double * ms) {
-    return vqg_gemv_t(payload, dim, nc, rows, cols, v3, x, y, variant, 0, iters, ms);
+    return vqg_gemv_t(payload, dim, nc, rows, cols, v3, x, y, variant, 256, iters, ms);
 }
 
 int vqg_gemv_launch_t(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x, float * y,
@@ -163,7 +231,7 @@ int vqg_gemv_launch_t(const void * payload, int dim, int nc, int rows, int cols,
 
 int vqg_gemv_launch(const void * payload, int dim, int nc, int rows, int cols, int v3, const float * x, float * y,
                     int variant) {
-    return vqg_gemv_launch_t(payload, dim, nc, rows, cols, v3, x, y, variant, 0);
+    return vqg_gemv_launch_t(payload, dim, nc, rows, cols, v3, x, y, variant, 256);
 }
 
 int vqg_dequant(const void * payload, int dim, int nc, int rows, int cols, int v3, float * out, int iters,

@@ -738,7 +738,7 @@ int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
     switch (variant) {
         case 0: return 1;
         case 1: return 1;
-        case 2: return (size_t) nc * dim * 2 <= 65536;
+        case 2: return (size_t) nc * dim * 2 <= (size_t) kLdsMax;
         case 3: return fast_geometry_ok(dim, nc, rows, cols, v3);
         default: return 0;
     }
@@ -1050,9 +1050,18 @@ static int launch_wave(const VqCall & c, int variant) {
      * changes how many row-waves share a workgroup, never the arithmetic. */
     const int threads = c.threads && c.threads < 256 ? c.threads : 256;
     const int nw = threads / 64;
+    const size_t lds = variant == 2 ? (size_t) c.nc * c.dim * 2 : 0;
+    if (lds > 65536) {
+        static size_t opted = 0;
+        if (lds > opted) {
+            hipError_t e = hipFuncSetAttribute((const void *) vq_wave_kernel<1>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+            if (e != hipSuccess) return fail_hip("LDS opt-in for the codebook wave kernel", e);
+            opted = lds;
+        }
+    }
     for (int m = 0; m < c.nmat; m++) {
         const Layout L = make_layout(c.dim, c.nc, c.mats[m].rows, c.cols, c.v3);
-        const size_t lds = variant == 2 ? (size_t) c.nc * c.dim * 2 : 0;
         int grid = c.grid > 0 ? c.grid : (L.rows + nw - 1) / nw;
         for (int s = 0; s < c.nst; s++) {
             const int acc = s > 0 || c.accumulate;
@@ -1112,7 +1121,7 @@ int vq_launch(const VqCall & c) {
         }
     }
     int variant = c.variant;
-    if (variant == 0) variant = all_fast ? 3 : ((size_t) c.nc * c.dim * 2 <= 65536 ? 2 : 1);
+    if (variant == 0) variant = all_fast ? 3 : ((size_t) c.nc * c.dim * 2 <= (size_t) kLdsMax ? 2 : 1);
     if (variant == 3) {
         if (!all_fast) {
             set_error("the VQ block kernel does not take this geometry, alignment or LDS footprint");
@@ -1129,7 +1138,7 @@ int vq_launch(const VqCall & c) {
         }
         return 0;
     }
-    if (variant == 2 && (size_t) c.nc * c.dim * 2 > 65536) {
+    if (variant == 2 && (size_t) c.nc * c.dim * 2 > (size_t) kLdsMax) {
         set_error("a codebook of %d x %d does not fit the LDS variant", c.nc, c.dim);
         return -1;
     }

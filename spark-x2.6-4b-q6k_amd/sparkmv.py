@@ -113,6 +113,7 @@ SIGNATURES = {
     "vqg_gemv_f32": (_I, [_P, _P, _P, _I, _I, _I, _D]),
     "sparkmv_container_open": (_I, [_P, _S, ctypes.POINTER(ContainerInfo)]),
     "sparkmv_stage_bytes": (_S, [_I] * 5),
+    "sparkmv_vq_gemv_ready": (_I, [_I] * 6),
     "sparkmv_vq_gemv": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _I, _P]),
     "sparkmv_vq_gemv_multi": (_I, [ctypes.POINTER(VqMatrix), _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P]),
     "sparkmv_vq_dequant": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _P]),

@@ -42,18 +42,30 @@ def test_binding_covers_every_declared_symbol(sm):
 
 
 def test_readiness_rules(sm):
+    """vqg_gemv_ready is the reference's truth table (decode-gpu.cu:788-797):
+    3 when the DQV3 block kernel's preconditions hold (v3, a 12-bit main
+    stream, whole 32-index groups, 4-byte aligned streams; :62-64), 2 for
+    dim 4, 1 always, 0 when the codebook fits the shared-codebook kernel
+    (160 KB of LDS here). Geometries every launch refuses (a DQV3 codebook
+    past 13 bits, cols not a multiple of dim) are ready for no variant."""
     L = sm.lib()
-    assert L.vqg_gemv_ready(4, 4096, 10240, 2560, 1, 3) == 1
-    assert L.vqg_gemv_ready(4, 8192, 16, 2560, 1, 3) == 1
-    assert L.vqg_gemv_ready(4, 1024, 64, 2560, 1, 3) == 0      # 10-bit stream: not the block kernel
-    assert L.vqg_gemv_ready(8, 4096, 64, 2560, 1, 3) == 0      # dim 8
-    assert L.vqg_gemv_ready(4, 4096, 64, 2500, 1, 3) == 0      # 625 indices per row, not whole 32-index steps
-    assert L.vqg_gemv_ready(4, 4096, 64, 2560, 0, 3) == 0      # DQVQ
-    assert L.vqg_gemv_ready(4, 16384, 64, 2560, 1, 1) == 0     # DQV3 is at most 13 bits
-    assert L.vqg_gemv_ready(4, 16384, 64, 2560, 0, 1) == 1     # DQVQ has no such limit
-    for v in (0, 1, 2):
-        assert L.vqg_gemv_ready(4, 4096, 37, 12, 1, v) == 1
-    assert L.vqg_gemv_ready(4, 4096, 1, 10, 1, 0) == 0         # cols not a multiple of dim
+    table = [   # (dim, nc, rows, cols, v3) -> ready for variants 0, 1, 2, 3
+        ((4, 4096, 10240, 2560, 1), (1, 1, 1, 1)),
+        ((4, 8192, 16, 2560, 1), (1, 1, 1, 1)),      # 13-bit: 12-bit stream + plane
+        ((4, 1024, 64, 2560, 1), (1, 1, 1, 0)),      # 10-bit stream
+        ((8, 4096, 64, 2560, 1), (1, 1, 0, 1)),      # dim 8: block path yes, dim-4 path no
+        ((4, 4096, 64, 2560, 0), (1, 1, 1, 0)),      # DQVQ
+        ((4, 4096, 64, 2500, 1), (1, 1, 1, 0)),      # 625 indices per row: not whole 32-index groups
+        ((4, 4096, 37, 12, 1), (1, 1, 1, 0)),
+        ((2, 65536, 8, 256, 0), (0, 1, 0, 0)),       # 256 KB codebook: not the shared-codebook kernel
+        ((4, 16384, 64, 2560, 0), (1, 1, 1, 0)),     # DQVQ has no 13-bit limit; 128 KB codebook fits
+        ((4, 16384, 64, 2560, 1), (0, 0, 0, 0)),     # DQV3 is at most 13 bits
+        ((4, 4096, 1, 10, 1), (0, 0, 0, 0)),         # cols not a multiple of dim
+    ]
+    for geom, want in table:
+        got = tuple(L.vqg_gemv_ready(*geom, v) for v in range(4))
+        assert got == want, (geom, got, want)
+    assert L.vqg_gemv_ready(4, 4096, 64, 2560, 1, 4) == 0
 
 
 def test_prefill_readiness_rules(sm):

@@ -57,7 +57,7 @@ def test_gemv_all_variants(sm, ref, dev, geom, f32):
         xt, xf = _x(sm, 5 + ncol, ncol, cols, f32)
         want = xf.astype(np.float64) @ W.T          # [ncol, rows]
         for variant in (0, 1, 2, 3):
-            if not sm.lib().vqg_gemv_ready(dim, nc, rows, cols, v3, variant):
+            if not sm.lib().sparkmv_vq_gemv_ready(dim, nc, rows, cols, v3, variant):
                 continue
             y = torch.full((ncol, rows), float("nan"), device=dev)
             dc.gemv(xt, y, ncols=ncol, accumulate=False, variant=variant)
@@ -172,6 +172,56 @@ def test_reference_abi_per_stage(sm, ref, dev):
         assert ms.value > 0
 
 
+@pytest.mark.parametrize("threads", [32, 96, 160, 1024])
+def test_reference_abi_warp_widths(sm, ref, dev, threads):
+    """The reference takes any multiple of 32 up to 1024 as the launch width
+    of variants 1-3 (decode-gpu.cu:815-818); here a width rounds up to whole
+    64-lane waves and never changes the result."""
+    import torch
+    rows, cols = 72, 512
+    data = sm.synth_container(33, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    x = np.cos(np.arange(cols, dtype=np.float32) * 0.003).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev)
+    L = sm.lib()
+    for variant in (1, 2, 3):
+        y = torch.zeros(rows, device=dev)
+        for p in dc.stage_ptrs:
+            sm.check(L.vqg_gemv_launch_t(p, 4, 4096, rows, cols, 1, xd.data_ptr(), y.data_ptr(), variant, threads),
+                     "launch")
+        torch.cuda.synchronize()
+        assert rel_l2(y.cpu().numpy(), W @ x.astype(np.float64)) <= TIGHT, (variant, threads)
+
+
+@pytest.mark.parametrize("dim,nc,v3", [(8, 4096, 1), (8, 8192, 0), (4, 16384, 0)])
+def test_reference_variants_beyond_dim4(sm, ref, dev, dim, nc, v3):
+    """Every variant the reference's readiness rules call ready runs and
+    matches the oracle: the block path (3) for a dim-8 DQV3 stream, the
+    shared-codebook kernel (0, via vqg_gemv_t) with a 128 KB codebook, and
+    the dim-4 path (2) on a DQVQ stream."""
+    import torch
+    rows, cols = 40, 1024
+    data = sm.synth_container(34 + dim, rows, cols, dim=dim, nc=nc, nstages=1, v3=v3)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    x = np.sin(np.arange(cols, dtype=np.float32) * 0.002).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev)
+    L = sm.lib()
+    ran = []
+    for variant in (0, 1, 2, 3):
+        if not L.vqg_gemv_ready(dim, nc, rows, cols, v3, variant):
+            continue
+        y = torch.zeros(rows, device=dev)
+        ms = ctypes.c_double()
+        sm.check(L.vqg_gemv_t(dc.stage_ptrs[0], dim, nc, rows, cols, v3, xd.data_ptr(), y.data_ptr(), variant, 128, 1,
+                              ctypes.byref(ms)), f"variant {variant}")
+        torch.cuda.synchronize()
+        assert rel_l2(y.cpu().numpy(), W @ x.astype(np.float64)) <= TIGHT, variant
+        ran.append(variant)
+    assert 0 in ran and 1 in ran
+
+
 def test_reference_abi_errors(sm, dev):
     import torch
     L = sm.lib()
@@ -183,9 +233,10 @@ def test_reference_abi_errors(sm, dev):
     assert "13 index bits" in sm.last_error()
     assert L.vqg_gemv_launch(p, 4, 4096, 0, 128, 1, x.data_ptr(), y.data_ptr(), 0) == -1
     assert L.vqg_gemv_launch(p, 4, 4096, 32, 128, 1, x.data_ptr(), y.data_ptr(), 9) == -1
-    assert L.vqg_gemv_launch_t(p, 4, 4096, 32, 128, 1, x.data_ptr(), y.data_ptr(), 3, 96) == -1
-    assert "multiple of 64" in sm.last_error()
+    assert L.vqg_gemv_launch_t(p, 4, 4096, 32, 128, 1, x.data_ptr(), y.data_ptr(), 3, 100) == -1
+    assert "warp multiple" in sm.last_error()
     assert L.vqg_gemv_launch(p, 4, 1024, 32, 128, 1, x.data_ptr(), y.data_ptr(), 3) == -1
+    assert "block kernel" in sm.last_error()
     assert L.vqg_row_dequant(p, 4, 4096, 32, 128, 1, 32, y.data_ptr()) == -1
     torch.cuda.synchronize()
 
