@@ -229,6 +229,18 @@ int sparkmv_plan_launch(void * plan, void * stream);
  * (hipExtLaunchKernel), so each figure is kernel time without launch gaps;
  * op_ms receives sparkmv_plan_size(plan) values. */
 int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms);
+/* Apply a trusted tuning profile (VQPROF 1) to the plan's VQ ops, as
+ * tools/vq/gpu/vq-model-gpu.cu:300-324 applies one at load: each op takes its
+ * geometry's gemv entry (every matrix of the op tuned alike) after the entry
+ * is re-checked as runnable here (vqg_gemv_ready, a warp-multiple width); a
+ * stale or non-ready entry keeps the heuristic. A profile measured for another
+ * artifact fingerprint or device changes nothing (returns 0). Returns the
+ * number of ops changed; the error text then counts the refused entries.
+ * Drops a captured graph. */
+int sparkmv_plan_apply_profile(void * plan, const void * profile, uint64_t artifact, const char * gpu);
+/* The kernel op i runs (sparkmv_* numbering; -1 for a k-quant op) and its
+ * launch width (0 = the kernel's own). */
+int sparkmv_plan_op_kernel(void * plan, int i, int * variant, int * threads);
 
 /* ---- decode chain: the per-token matvec chain as ONE persistent launch ----
  * Replaces the launch-by-launch chain of tools/vq/gpu/vq-model-gpu.cu:776-835
@@ -382,6 +394,12 @@ int sparkmv_model_verify(void * model, const uint32_t * tokens, int ntok, int po
 int sparkmv_model_rollback(void * model, int pos);
 /* The cached length: one past the last position a step wrote, or as rolled back. */
 int sparkmv_model_len(void * model);
+/* Apply a trusted tuning profile to the model's VQ matvecs per geometry,
+ * with the same checks as sparkmv_plan_apply_profile (vq-model-gpu.cu:300-324).
+ * Returns the number of geometries tuned; drops a captured graph. */
+int sparkmv_model_apply_profile(void * model, const void * profile, uint64_t artifact, const char * gpu);
+/* The kernel the model runs for a rows x cols VQ matvec (0, 0 = heuristic). */
+int sparkmv_model_matvec_kernel(void * model, int rows, int cols, int * variant, int * threads);
 /* The device rows of layer's K and V cache ([max_ctx][kv_dim] f32 each). */
 int sparkmv_model_kv(void * model, int layer, float ** k, float ** v);
 

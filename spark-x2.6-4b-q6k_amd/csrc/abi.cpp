@@ -205,6 +205,26 @@ int vqg_gemv_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
     }
 }
 
+}  // extern "C"
+
+namespace sparkmv {
+
+int profile_gemv_pick(const void * profile, int dim, int nc, int rows, int cols, int v3, int * variant, int * threads) {
+    sparkmv_profile_entry e;
+    memset(&e, 0, sizeof e);
+    if (sparkmv_profile_find(profile, 0, dim, nc, rows, cols, v3, &e) != 0) return 0;
+    if (e.variant < 0 || e.variant > 3 || !vqg_gemv_ready(dim, nc, rows, cols, v3, e.variant) || e.threads < 32 ||
+        e.threads > 1024 || e.threads % 32)
+        return -1;
+    *variant = map_variant(make_layout(dim, nc, rows, cols, v3), e.variant, 0);
+    *threads = (e.threads + 63) & ~63;
+    return 1;
+}
+
+}  // namespace sparkmv
+
+extern "C" {
+
 int sparkmv_vq_gemv_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
     return vq_variant_ready(dim, nc, rows, cols, v3, variant);
 }

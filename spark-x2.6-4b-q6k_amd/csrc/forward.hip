@@ -39,6 +39,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <map>
 #include <vector>
 
 #include "../../include/sparkmv.h"
@@ -503,6 +504,8 @@ struct Model {
     hipGraphExec_t exec = nullptr;
     /* cached positions (model.rs:453, :361-381) */
     int len = 0;
+    /* tuned kernels per (rows, cols) of a VQ matvec: variant, threads */
+    std::map<std::pair<int, int>, std::pair<int, int>> picks;
     /* verify-block buffers, allocated at the first block: 8 columns of each
      * activation, gate rows at the qkv stride, partials per token */
     void * vmem = nullptr;
@@ -536,6 +539,8 @@ int gemv(const Model & m, const void * const * st, int rows, int cols, const voi
     c.mats = &d; c.nmat = 1;
     c.x = x; c.ldx = cols; c.xf32 = m.c.x_dtype == SPARKMV_X_F32; c.ncol = ncol; c.ldy = ldy ? ldy : rows;
     c.accumulate = acc; c.stream = s;
+    const auto it = m.picks.find({rows, cols});
+    if (it != m.picks.end()) { c.variant = it->second.first; c.threads = it->second.second; }
     return vq_launch(c);
 }
 
@@ -552,6 +557,12 @@ int gemv2(const Model & m, const void * const * st0, int rows0, float * y0, cons
     c.mats = d; c.nmat = 2;
     c.x = x; c.ldx = cols; c.xf32 = m.c.x_dtype == SPARKMV_X_F32; c.ncol = ncol; c.ldy = ldy ? ldy : rows0;
     c.accumulate = 0; c.stream = s;
+    /* two matrices in one launch take a tuned kernel when both are tuned alike */
+    const auto a = m.picks.find({rows0, cols}), b = m.picks.find({rows1, cols});
+    if (a != m.picks.end() && b != m.picks.end() && a->second == b->second) {
+        c.variant = a->second.first;
+        c.threads = a->second.second;
+    }
     return vq_launch(c);
 }
 
@@ -962,6 +973,55 @@ int sparkmv_model_rollback(void * model, int pos) {
 int sparkmv_model_len(void * model) {
     Model * m = (Model *) model;
     return m ? m->len : -1;
+}
+
+/* Apply a trusted tuning profile to the model's VQ matvecs, per geometry,
+ * as the reference's loader does (tools/vq/gpu/vq-model-gpu.cu:300-324): a
+ * geometry with a runnable gemv entry takes its kernel and width; an entry
+ * that is not runnable here leaves the heuristic; an untrusted profile
+ * changes nothing. Returns the number of geometries tuned, or -1. Drops a
+ * captured graph (capture again to replay the tuned kernels). */
+int sparkmv_model_apply_profile(void * model, const void * profile, uint64_t artifact, const char * gpu) {
+    Model * m = (Model *) model;
+    if (!m || !profile || !gpu) { set_error("model, profile or gpu name is null"); return -1; }
+    const int t = sparkmv_profile_trusted(profile, artifact, gpu);
+    if (t < 0) return -1;
+    if (t == 0) {
+        set_error("profile: measured for another artifact or device; the heuristic stays");
+        return 0;
+    }
+    const auto & c = m->c;
+    const int qd = c.heads * c.head_dim, kvd = c.kv_heads * c.head_dim;
+    const int geoms[][2] = {{qd + 2 * kvd, c.hidden}, {c.heads, c.hidden}, {c.hidden, qd},
+                            {c.intermediate, c.hidden}, {c.hidden, c.intermediate}, {c.vocab, c.hidden}};
+    int applied = 0, refused = 0;
+    m->picks.clear();
+    for (const auto & g : geoms) {
+        if (m->picks.count({g[0], g[1]})) continue;
+        int v = 0, th = 0;
+        const int r = profile_gemv_pick(profile, c.dim, c.nc, g[0], g[1], c.v3, &v, &th);
+        if (r < 0) refused++;
+        if (r == 1) {
+            m->picks[{g[0], g[1]}] = {v, th};
+            applied++;
+        }
+    }
+    if (m->exec) { hipGraphExecDestroy(m->exec); m->exec = nullptr; }
+    if (m->graph) { hipGraphDestroy(m->graph); m->graph = nullptr; }
+    set_error("profile: %d geometries take their tuned kernel, %d entries are not runnable here (heuristic kept)",
+              applied, refused);
+    return applied;
+}
+
+/* The kernel the model runs for a (rows, cols) VQ matvec: variant and width
+ * as sparkmv_plan_op_kernel reports them (0, 0 = the heuristic). */
+int sparkmv_model_matvec_kernel(void * model, int rows, int cols, int * variant, int * threads) {
+    Model * m = (Model *) model;
+    if (!m) { set_error("model is null"); return -1; }
+    const auto it = m->picks.find({rows, cols});
+    if (variant) *variant = it == m->picks.end() ? 0 : it->second.first;
+    if (threads) *threads = it == m->picks.end() ? 0 : it->second.second;
+    return 0;
 }
 
 /* The layer's KV cache rows (device pointers), for tests and inspection. */

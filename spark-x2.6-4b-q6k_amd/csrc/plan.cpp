@@ -159,6 +159,58 @@ int sparkmv_plan_launch(void * plan, void * stream) {
     return e == hipSuccess ? 0 : fail_hip("graph launch", e);
 }
 
+/* Apply a trusted tuning profile to the plan's VQ ops, as the reference's
+ * runtime applies one at load (tools/vq/gpu/vq-model-gpu.cu:300-324): an op
+ * takes its geometry's gemv entry when every matrix of the op has a runnable
+ * entry and they agree; an entry that is not runnable here leaves the op on
+ * the heuristic. An untrusted profile (another artifact or device) changes
+ * nothing. Returns the number of ops changed (the message then says how many
+ * entries were refused), or -1 on a null argument. */
+int sparkmv_plan_apply_profile(void * plan, const void * profile, uint64_t artifact, const char * gpu) {
+    Plan * p = (Plan *) plan;
+    if (!p || !profile || !gpu) { set_error("plan, profile or gpu name is null"); return -1; }
+    const int t = sparkmv_profile_trusted(profile, artifact, gpu);
+    if (t < 0) return -1;
+    if (t == 0) {
+        set_error("profile: measured for another artifact or device; the heuristic stays");
+        return 0;
+    }
+    int applied = 0, refused = 0;
+    for (auto & op : p->ops) {
+        if (op.kind != 0) continue;
+        int v = -1, th = -1, ok = 1;
+        for (const auto & m : op.mats) {
+            int mv = 0, mt = 0;
+            const int r = profile_gemv_pick(profile, op.vq.dim, op.vq.nc, m.rows, op.vq.cols, op.vq.v3, &mv, &mt);
+            if (r < 0) refused++;
+            if (r != 1 || (v >= 0 && (mv != v || mt != th))) { ok = 0; continue; }
+            v = mv;
+            th = mt;
+        }
+        if (ok && v >= 0) {
+            op.vq.variant = v;
+            op.vq.threads = th;
+            applied++;
+        }
+    }
+    drop_graph(p);
+    set_error("profile: %d ops take their tuned kernel, %d entries are not runnable here (heuristic kept)", applied,
+              refused);
+    return applied;
+}
+
+/* The kernel an op runs: its variant (0 the fastest that takes the call, 1
+ * the generic wave kernel, 2 the LDS-codebook wave kernel, 3 the MFMA block
+ * kernel; -1 for a k-quant op) and launch width (0 = the kernel's own). */
+int sparkmv_plan_op_kernel(void * plan, int i, int * variant, int * threads) {
+    Plan * p = (Plan *) plan;
+    if (!p || i < 0 || i >= (int) p->ops.size()) { set_error("no plan op %d", i); return -1; }
+    const PlanOp & op = p->ops[(size_t) i];
+    if (variant) *variant = op.kind == 0 ? op.vq.variant : -1;
+    if (threads) *threads = op.kind == 0 ? op.vq.threads : 0;
+    return 0;
+}
+
 /* Average device time of every op over `iters` eager runs: each op's
  * kernels carry a start and a stop event in their own dispatches, so an op's
  * time is its kernels' duration without the launch gap between ops. op_ms

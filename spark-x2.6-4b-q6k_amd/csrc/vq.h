@@ -30,6 +30,14 @@ struct VqCall {
     int grid;      /* workgroups; 0 = the default */
 };
 
+/* The kernel a profile's gemv entry (tools/vq/gpu/vq-profile.h, the
+ * reference's variant numbering) asks for on one geometry, re-checked for
+ * runnability as tools/vq/gpu/vq-model-gpu.cu:300-324 does: 1 with *variant
+ * (VqCall numbering) and *threads set; 0 when the profile has no entry; -1
+ * when its entry is not runnable here (unknown or not-ready variant, or a
+ * width that is not a warp multiple up to 1024), so the heuristic stays. */
+int profile_gemv_pick(const void * profile, int dim, int nc, int rows, int cols, int v3, int * variant, int * threads);
+
 /* Whether a kernel variant runs this geometry (same numbering as VqCall). */
 int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant);
 /* Validate and launch; returns 0, or -1 with the message set. */

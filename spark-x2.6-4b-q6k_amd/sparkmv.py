@@ -132,6 +132,8 @@ SIGNATURES = {
     "sparkmv_plan_capture": (_I, [_P, _P]),
     "sparkmv_plan_launch": (_I, [_P, _P]),
     "sparkmv_plan_time_ops": (_I, [_P, _P, _I, _D]),
+    "sparkmv_plan_apply_profile": (_I, [_P, _P, _U64, ctypes.c_char_p]),
+    "sparkmv_plan_op_kernel": (_I, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "sparkmv_chain_create": (_P, []),
     "sparkmv_chain_destroy": (None, [_P]),
     "sparkmv_chain_size": (_I, [_P]),
@@ -172,6 +174,8 @@ SIGNATURES = {
     "sparkmv_model_rollback": (_I, [_P, _I]),
     "sparkmv_model_len": (_I, [_P]),
     "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
+    "sparkmv_model_apply_profile": (_I, [_P, _P, _U64, ctypes.c_char_p]),
+    "sparkmv_model_matvec_kernel": (_I, [_P, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "sparkmv_profile_fingerprint": (_I, [ctypes.c_char_p, ctypes.POINTER(_U64)]),
     "sparkmv_profile_load": (_P, [ctypes.c_char_p]),
     "sparkmv_profile_close": (None, [_P]),
@@ -575,6 +579,16 @@ class Model:
     def __len__(self):
         return lib().sparkmv_model_len(self.h)
 
+    def apply_profile(self, profile, artifact, gpu):
+        n = lib().sparkmv_model_apply_profile(self.h, profile.h, artifact, gpu.encode())
+        check(0 if n >= 0 else -1, "model apply profile")
+        return n
+
+    def matvec_kernel(self, rows, cols):
+        v, t = ctypes.c_int(), ctypes.c_int()
+        check(lib().sparkmv_model_matvec_kernel(self.h, rows, cols, ctypes.byref(v), ctypes.byref(t)), "model kernel")
+        return v.value, t.value
+
     def kv(self, layer):
         """(k, v) device pointers of the layer's cache, [max_ctx][kv_dim] f32 each."""
         k, v = ctypes.c_void_p(), ctypes.c_void_p()
@@ -630,36 +644,136 @@ def profile_write(path, artifact, gpu, driver, entries):
           "profile write")
 
 
-def tune_gemv(mats, iters=20, widths=(64, 128, 256)):
-    """Measure every ready GEMV variant and launch width of each
-    (DeviceContainer) geometry on the current device, stage by stage through
-    the reference ABI (vqg_gemv_t, f32 x), and return one profile entry per
-    geometry: the fastest (tools/vq-tune's gemv sweep)."""
+TUNE_GATE = 1e-4   # tools/vq-tune/src/main.rs:107-108 (GEMV_GATE, PREFILL_GATE)
+
+
+def _tune_activations(n):
+    """tools/vq-tune/src/main.rs:89-91: sin(0.001 i) in f64, rounded to f32."""
+    return np.sin(np.arange(n, dtype=np.float64) * 0.001).astype(np.float32)
+
+
+def _tune_rel_l2(a, b):
+    """tools/vq-tune/src/kernels.rs:241-253: ||a - b|| / ||b||, 0/0 = 0."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    d, n = float(np.sum((a - b) ** 2)), float(np.sum(b * b))
+    if n == 0.0:
+        return 0.0 if d == 0.0 else float("inf")
+    return (d / n) ** 0.5
+
+
+def tune(mats, iters=20, tokens=512, prefill=True):
+    """tools/vq-tune's sweep (main.rs:110-225) on the current device, per
+    distinct geometry of the DeviceContainers, every stage through the
+    reference ABI with the tuner's activations:
+
+      gemv: a reference output from variant 3, else 2, else 1, at 256 threads;
+        then every ready variant (3, 2, 1, 0) at each width (0 at 256, the
+        others at 128, 256 and 512). A candidate whose output differs from
+        the reference's by more than 1e-4 relative L2 is rejected; the fastest
+        survivor (GB/s of container) is the entry.
+      prefill (`tokens` tokens, xT [cols][tokens] f32): the reference is tile
+        128 x 64 of variant 1 when ready, else the legacy variant 3; the
+        candidates are every ready tile of variants 1 and 2 (only 3 when no
+        tile is ready), gated the same way; the fastest (tokens/s) wins.
+
+    Returns (entries, rejected): ProfileEntry records (kind 0 gemv, 1 prefill)
+    and (kind, geometry, candidate, relL2) for every gated-out candidate."""
     torch = _torch()
-    out, seen = [], set()
+    L = lib()
+    entries, rejected, seen = [], [], set()
     for m in mats:
         h = m.host
-        key = (h.dim, h.nc, h.rows, h.cols, h.v3)
-        if key in seen:
+        g = (h.dim, h.nc, h.rows, h.cols, h.v3)
+        if g in seen:
             continue
-        seen.add(key)
-        x = torch.randn(h.cols, device="cuda")
+        seen.add(g)
+        nbytes = float(h.data.nbytes) if hasattr(h, "data") else float(h.stage_bytes * h.nstages)
+        x = torch.from_numpy(_tune_activations(h.cols)).to("cuda")
         y = torch.zeros(h.rows, device="cuda")
-        best = None
-        for variant in (1, 2, 3):
-            if not lib().vqg_gemv_ready(h.dim, h.nc, h.rows, h.cols, h.v3, variant):
-                continue
-            for th in (widths if variant != 3 else (0,)):
+
+        def gemv(variant, threads, n):
+            y.zero_()
+            total = 0.0
+            for p in m.stage_ptrs:
                 ms = ctypes.c_double()
-                check(lib().vqg_gemv_t(m.stage_ptrs[0], h.dim, h.nc, h.rows, h.cols, h.v3, x.data_ptr(), y.data_ptr(),
-                                       variant, th, iters, ctypes.byref(ms)), "vqg_gemv_t")
-                gbs = h.stage_bytes / (ms.value * 1e-3) / 1e9
+                check(L.vqg_gemv_t(p, *g, x.data_ptr(), y.data_ptr(), variant, threads, n, ctypes.byref(ms)),
+                      "vqg_gemv_t")
+                total += ms.value
+            return total, (y.cpu().numpy().copy() if n == 1 else None)
+
+        ready = lambda v: L.vqg_gemv_ready(*g, v) != 0  # noqa: E731
+        ref_v = 3 if ready(3) else (2 if ready(2) else 1)
+        _, ref_out = gemv(ref_v, 256, 1)
+        best = None
+        for variant in (3, 2, 1, 0):
+            if not ready(variant):
+                continue
+            for th in ((256,) if variant == 0 else (128, 256, 512)):
+                _, out = gemv(variant, th, 1)
+                rel = _tune_rel_l2(out, ref_out)
+                if rel > TUNE_GATE:
+                    rejected.append((0, g, (variant, th), rel))
+                    continue
+                ms, _ = gemv(variant, th, iters)
+                gbs = nbytes / (ms * 1e-3) / 1e9
                 if best is None or gbs > best[2]:
                     best = (variant, th, gbs)
-        e = ProfileEntry(kind=0, dim=h.dim, nc=h.nc, rows=h.rows, cols=h.cols, v3=h.v3, variant=best[0],
-                         threads=best[1], rate=best[2])
-        out.append(e)
-    return out
+        if best is None:
+            raise SparkmvError(f"no runnable gemv variant for {g}")
+        entries.append(ProfileEntry(kind=0, dim=h.dim, nc=h.nc, rows=h.rows, cols=h.cols, v3=h.v3,
+                                    variant=best[0], threads=best[1], rate=best[2]))
+        if not prefill:
+            continue
+        xt = torch.from_numpy(_tune_activations(h.cols * tokens).reshape(h.cols, tokens)).to("cuda")
+        yb = torch.zeros(tokens, h.rows, device="cuda")
+
+        def pre(variant, bn, bk, n):
+            yb.zero_()
+            total = 0.0
+            for p in m.stage_ptrs:
+                ms = ctypes.c_double()
+                check(L.vqg_prefill_tile(p, *g, xt.data_ptr(), tokens, yb.data_ptr(), n, ctypes.byref(ms), bn, bk,
+                                         variant), "vqg_prefill_tile")
+                total += ms.value
+            return total, (yb.cpu().numpy().copy() if n == 1 else None)
+
+        tile_ready = lambda bn, bk, v: L.vqg_prefill_cfg_ready(*g, bn, bk, v) != 0  # noqa: E731
+        ref_t = (1, 128, 64) if tile_ready(128, 64, 1) else (3, 0, 0)
+        _, ref_out = pre(*ref_t, 1)
+        cands = []
+        if ref_t[0] == 3:
+            cands.append((3, 0, 0))
+        else:
+            for i in range(L.vqg_prefill_cfg_count()):
+                bn, bk = ctypes.c_int(), ctypes.c_int()
+                check(L.vqg_prefill_cfg(i, ctypes.byref(bn), ctypes.byref(bk)), "vqg_prefill_cfg")
+                for variant in (1, 2):
+                    if tile_ready(bn.value, bk.value, variant):
+                        cands.append((variant, bn.value, bk.value))
+        best = None
+        for cand in cands:
+            _, out = pre(*cand, 1)
+            rel = _tune_rel_l2(out, ref_out)
+            if rel > TUNE_GATE:
+                rejected.append((1, g, cand, rel))
+                continue
+            ms, _ = pre(*cand, iters)
+            tps = tokens / (ms * 1e-3)
+            if best is None or tps > best[3]:
+                best = (*cand, tps)
+        if best is None:
+            raise SparkmvError(f"no runnable prefill path for {g}")
+        entries.append(ProfileEntry(kind=1, dim=h.dim, nc=h.nc, rows=h.rows, cols=h.cols, v3=h.v3,
+                                    variant=best[0], bn=best[1], bk=best[2], rate=best[3]))
+    return entries, rejected
+
+
+def device_name():
+    """vqg_device_name: the name a profile's trust check compares."""
+    buf = ctypes.create_string_buffer(256)
+    check(lib().vqg_device_name(buf, 256), "device name")
+    return buf.value.decode()
 
 
 class Plan:
@@ -714,6 +828,18 @@ class Plan:
 
     def launch(self, stream=None):
         check(lib().sparkmv_plan_launch(self.h, _stream_ptr(stream)), "plan launch")
+
+    def apply_profile(self, profile, artifact, gpu):
+        """Apply a trusted Profile (sparkmv_plan_apply_profile): returns the
+        number of ops changed; last_error() then counts refused entries."""
+        n = lib().sparkmv_plan_apply_profile(self.h, profile.h, artifact, gpu.encode())
+        check(0 if n >= 0 else -1, "plan apply profile")
+        return n
+
+    def op_kernel(self, i):
+        v, t = ctypes.c_int(), ctypes.c_int()
+        check(lib().sparkmv_plan_op_kernel(self.h, i, ctypes.byref(v), ctypes.byref(t)), "plan op kernel")
+        return v.value, t.value
 
     def time_ops(self, stream=None, iters=5):
         n = len(self)

@@ -60,12 +60,12 @@ def test_manifest_container_through_the_gemv(sm, ref, dev, tmp_path):
 
 
 def test_tuned_profile_round_trip(sm, ref, dev, tmp_path):
-    """tools/vq-tune's gemv sweep on this device: every ready variant and
-    width of each geometry of a small manifest directory timed through
-    vqg_gemv_t, the fastest written as a VQPROF 1 profile with the
-    directory's fingerprint and the device name; the profile is then trusted
-    only for that directory and device, and the variant it names gives the
-    GEMV at the bar."""
+    """tools/vq-tune's sweep on this device (gemv variants and widths, prefill
+    tiles, each gated at 1e-4 against the reference candidate) over a small
+    manifest directory, written as a VQPROF 1 profile with the directory's
+    fingerprint and the device name; the profile is trusted only for that
+    directory and device, and a plan that applies it computes the GEMV at
+    the bar with the tuned kernels."""
     import torch
     conts = {"blk.0.mlp.up_proj.weight": sm.synth_container(41, 512, 2560),
              "blk.0.mlp.down_proj.weight": sm.synth_container(42, 256, 1024)}
@@ -76,21 +76,30 @@ def test_tuned_profile_round_trip(sm, ref, dev, tmp_path):
         lines.append(f"{name} {h.rows} {h.cols} {h.nstages} {c.nbytes} 1.0")
     (tmp_path / "manifest.txt").write_text("\n".join(lines) + "\n")
     mats = [sm.DeviceContainer(c, dev) for c in conts.values()]
-    entries = sm.tune_gemv(mats, iters=3)
-    assert len(entries) == 2
+    entries, rejected = sm.tune(mats, iters=3, tokens=128)
+    assert sorted(e.kind for e in entries) == [0, 0, 1, 1]
+    assert not rejected, rejected
     fp = sm.profile_fingerprint(tmp_path)
-    gpu = torch.cuda.get_device_name(0)
+    gpu = sm.device_name()
     path = tmp_path / "vq-tune.profile"
     sm.profile_write(path, fp, gpu, "hip", entries)
     pf = sm.Profile(path)
-    assert pf.trusted(fp, gpu) and not pf.trusted(fp ^ 1, gpu)
-    for m, c in zip(mats, conts.values()):
+    assert pf.trusted(fp, gpu) and not pf.trusted(fp ^ 1, gpu) and not pf.trusted(fp, gpu + "x")
+    plan = sm.Plan()
+    ys, xs, Ws = [], [], []
+    for i, (m, c) in enumerate(zip(mats, conts.values())):
         e = pf.find(0, m.host.dim, m.host.nc, m.rows, m.cols, m.host.v3)
-        print(f"{m.rows}x{m.cols}: variant {e.variant}, threads {e.threads}, {e.rate:.0f} GB/s")
-        assert e is not None and e.variant in (1, 2, 3)
-        W = ref.decode(c).astype(np.float64)
-        xb = sm.synth_bf16(43, m.cols)
+        p = pf.find(1, m.host.dim, m.host.nc, m.rows, m.cols, m.host.v3)
+        print(f"{m.rows}x{m.cols}: gemv variant {e.variant} threads {e.threads} {e.rate:.0f} GB/s; "
+              f"prefill variant {p.variant} tile {p.bn}x{p.bk} {p.rate:.0f} tok/s")
+        assert e.variant in (0, 1, 2, 3) and p.variant in (1, 2, 3)
+        xb = sm.synth_bf16(43 + i, m.cols)
+        x = torch.from_numpy(xb.view(np.int16).copy()).to(dev).reshape(1, m.cols)
         y = torch.full((1, m.rows), float("nan"), device=dev)
-        m.gemv(torch.from_numpy(xb.view(np.int16).copy()).to(dev).reshape(1, m.cols), y, variant=e.variant)
-        torch.cuda.synchronize()
+        plan.add_vq([m], x, [y])
+        ys.append(y); xs.append(xb); Ws.append(ref.decode(c).astype(np.float64))
+    assert plan.apply_profile(pf, fp, gpu) == 2
+    plan.run()
+    torch.cuda.synchronize()
+    for y, xb, W in zip(ys, xs, Ws):
         assert rel_l2(y.cpu().numpy()[0], W @ sm.bf16_to_f32(xb).astype(np.float64)) <= TIGHT
