@@ -333,6 +333,73 @@ def bench_decode_set(args, sm, torch, dev):
     return out
 
 
+def bench_decode_chain(args, sm, torch, dev):
+    """decode-chain: the 36-layer N=1 matvec chain with every op depending on
+    the one before it, as in the forward (q+k+v+g from rms_norm(h), o from q,
+    gate+up from rms_norm(h + o), down from gelu(gate) * up into the residual),
+    as ONE persistent launch (sparkmv_chain_*), then the Q8_0 head; the
+    dataflow of sparkmv.DecodeChain."""
+    t0 = time.time()
+    with concurrent.futures.ThreadPoolExecutor(min(16, os.cpu_count() or 4)) as ex:
+        hosts = list(ex.map(lambda l: gen_layer(sm, l), range(LAYERS)))
+        head = sm.synth_q8_0(0x4EAD, args.head_rows, HIDDEN)
+    layers = [{n: sm.DeviceContainer(h, dev) for (n, _, _, _), h in zip(LAYER_MATS, hl)} for hl in hosts]
+    nbytes = sum(h.nbytes for hl in hosts for h in hl) + head.nbytes
+    kept = (0, LAYERS // 2, LAYERS - 1)
+    hosts = {l: {n: h for (n, _, _, _), h in zip(LAYER_MATS, hosts[l])} for l in kept}
+    log(f"generated and uploaded in {time.time() - t0:.1f} s")
+    h0 = torch.from_numpy(sm.bf16_to_f32(sm.synth_bf16(0xE0, HIDDEN))).to(dev)
+    dc = sm.DecodeChain(layers, torch.from_numpy(head).to(dev), args.head_rows, h0)
+    dc.chain.tune(args.chain_waves, args.chain_look, args.chain_units)
+    stream = torch.cuda.Stream(device=dev)
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            dc.launch(stream)
+        torch.cuda.synchronize()
+        dc.chain.status()
+        a, b = ev(), ev()
+        a.record(stream)
+        for _ in range(args.steps):
+            dc.launch(stream)
+        b.record(stream)
+        torch.cuda.synchronize()
+        dc.chain.status()
+        ms = a.elapsed_time(b) / args.steps
+        c0, c1 = ev(), ev()
+        c0.record(stream)
+        for _ in range(args.steps):
+            dc.chain.launch(stream)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        dc.chain.status()
+        chain_ms = c0.elapsed_time(c1) / args.steps
+    log(f"  decode chain: {ms * 1e3:.1f} us/token ({chain_ms * 1e3:.1f} us for the chain launch), "
+        f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s of weights")
+    out = {"metric": "decode matvec us/token, dependent chain (36-layer trunk as one persistent launch + Q8_0 head)",
+           "value": round(ms * 1e3, 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f16xf16->f32 (bf16 x), f64 norm sums",
+           "data": "synthetic (seeded, random-init weights of the real shapes)",
+           "config": {"workload": "decode chain: 144 dependent VQ matvecs with rms_norm/gelu staging, one launch, "
+                                  "then the Q8_0 head", "layers": LAYERS, "hidden": HIDDEN, "ffn": FFN,
+                      "head": f"Q8_0 {args.head_rows}x{HIDDEN}", "waves": args.chain_waves,
+                      "look": args.chain_look, "min_units": args.chain_units},
+           "chain_launch_us": round(chain_ms * 1e3, 2), "weight_bytes": int(nbytes),
+           "achieved_gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4)}
+    if args.check:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import chain_check as cc
+        t = time.time()
+        res = cc.check_decode_chain(dc, hosts, head, kept)
+        log(f"  output check ({time.time() - t:.1f} s): {res}")
+        out["check"] = {"rel_l2_max": cc.worst_matvec(res), "detail": res, "layers": list(kept),
+                        "method": "each op of the timed chain vs the oracle from the inputs the GPU read; every "
+                                  "head row"}
+    return out
+
+
 FW_WINDOW = 512   # sliding_window; 9 of the 36 layers are full attention (every fourth)
 
 
@@ -618,10 +685,13 @@ def main():
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--workload", default="decode-set",
                     choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512", "forward",
-                             "verify-block", "decode-set-q6k"])
+                             "verify-block", "decode-set-q6k", "decode-chain"])
     ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--chain-waves", type=int, default=16, help="decode-chain: waves per workgroup")
+    ap.add_argument("--chain-look", type=int, default=2, help="decode-chain: index steps in flight per wave")
+    ap.add_argument("--chain-units", type=int, default=16, help="decode-chain: units per workgroup aimed for")
     ap.add_argument("--no-check", dest="check", action="store_false",
                     help="skip the oracle check of the timed outputs")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -652,6 +722,8 @@ def main():
         out = bench_prefill(args, sm, torch, dev)
     elif args.workload == "decode-set-q6k":
         out = bench_decode_set_q6k(args, sm, torch, dev)
+    elif args.workload == "decode-chain":
+        out = bench_decode_chain(args, sm, torch, dev)
     elif args.workload in ("forward", "verify-block"):
         out = bench_forward(args, sm, torch, dev)
     else:

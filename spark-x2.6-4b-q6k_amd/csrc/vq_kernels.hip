@@ -432,11 +432,14 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         f4 acc[NST];
 #pragma unroll
         for (int s = 0; s < NST; s++) acc[s] = f4{0.f, 0.f, 0.f, 0.f};
+        /* XG: the largest bf16 |x| this lane converts in the unit, per half */
+        u16x2 xmx = {0, 0};
+        u16x2 * const xm = XG ? &xmx : nullptr;
         if (active) {
             if (MSC > 0) {
 #pragma unroll
                 for (int u = 0; u < D; u++) {
-                    mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc);
+                    mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc, 1.0f, xm);
                     if (u + kLook < D) ld(w[u + kLook], u + kLook);
                 }
             } else {
@@ -444,7 +447,8 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
 #pragma unroll
                     for (int u = 0; u < D; u++) {
                         if (ms0 + u < MS)
-                            mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc);
+                            mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc,
+                                                      1.0f, xm);
                         if (MS > D) ld(w[u], ms0 + u + D);
                     }
                 }
@@ -453,34 +457,48 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         /* the factor 2^uk that the unit's sums carry back */
         int uk = xk;
         if constexpr (XG != 0) {
-            /* x read per step, converted per step: an |x| past f16's range
-             * shows as a non-finite sum. Then, when the wave's largest finite
-             * |x| over the unit is 2^15 or more, it sets uk and the unit runs
-             * again, one step at a time, with x * 2^-uk (an infinity or NaN in
-             * x stays one). Small x is not rescaled here: below 2^-14 it keeps
-             * f16's subnormal spacing, 2^-24. */
+            /* x read per step, converted per step, so the range is checked
+             * per unit and per B column (the four lanes of lane & 15: one
+             * part of one activation column), after the fact:
+             *  - an |x| past f16's range shows as a non-finite sum; the
+             *    column's largest finite |x| is then read again;
+             *  - small x shows in the largest |x| the steps converted: a
+             *    nonzero maximum below 2^-4 would leave the values below
+             *    2^-14 on f16's subnormal grid.
+             * A column outside [2^-4, 2^15) gets uk that brings its largest
+             * finite |x| to [2^14, 2^15), and the unit runs again, one step
+             * at a time, with x * 2^-uk (exact; an infinity or NaN in x stays
+             * one). The sums are scaled back by 2^uk before any other
+             * column's or chunk's are added to them. */
             if (active) {
                 bool bad = false;
 #pragma unroll
                 for (int s = 0; s < NST; s++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) bad = bad || !__builtin_isfinite(acc[s][i]);
-                if (__builtin_amdgcn_ballot_w64(bad)) {
-                    typedef uint32_t u4x __attribute__((ext_vector_type(4)));
-                    uint32_t m = 0;
+                /* as f32 bits; a non-finite maximum is never small */
+                uint32_t m = xr_col_max((uint32_t) max(xmx[0], xmx[1]) << 16);
+                const bool small = m != 0u && m < kXrLow;
+                if (__builtin_amdgcn_ballot_w64(bad || small)) {
+                    if (__builtin_amdgcn_ballot_w64(bad)) {
+                        typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+                        m = 0;
 #pragma unroll 1
-                    for (int u = 0; u < MS; u++) {
+                        for (int u = 0; u < MS; u++) {
 #pragma unroll
-                        for (int k = 0; k < 4; k++) {
-                            const u4x v = ((const u4x *) (xgp + 256 * u))[k];
+                            for (int k = 0; k < 4; k++) {
+                                const u4x v = ((const u4x *) (xgp + 256 * u))[k];
 #pragma unroll
-                            for (int h = 0; h < 4; h++)
-                                m = max(m, max(xr_fin((v[h] << 16) & 0x7fffffffu), xr_fin(v[h] & 0x7fff0000u)));
+                                for (int h = 0; h < 4; h++)
+                                    m = max(m, max(xr_fin((v[h] << 16) & 0x7fffffffu), xr_fin(v[h] & 0x7fff0000u)));
+                            }
                         }
+                        m = xr_col_max(m);   /* the column's largest finite |x| in the unit */
                     }
-                    m = xr_wave_max(m);   /* the largest finite |x| of the unit */
-                    if (m >= kXrOver) {
-                        uk = xr_shift_of(m);
+                    /* 2^-uk must be a normal f32: bf16 x below 2^-126 is
+                     * brought up only as far as 2^126 takes it */
+                    uk = max(xr_shift_of(m), -126);
+                    if (__builtin_amdgcn_ballot_w64(uk != 0)) {
                         const float sc = __uint_as_float((uint32_t) (127 - uk) << 23);
 #pragma unroll
                         for (int s = 0; s < NST; s++) acc[s] = f4{0.f, 0.f, 0.f, 0.f};

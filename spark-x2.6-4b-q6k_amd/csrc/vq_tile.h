@@ -78,9 +78,17 @@ __device__ __forceinline__ uint32_t step_addr(const Words<NST, EXT, XG> & W, int
     return (uint32_t) s * cbb + a;
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+/* XG, SCX = 0: *xm (when given) keeps, per 16-bit half, the largest bf16
+ * magnitude |x| of the lane's values so far (bf16 magnitudes order as
+ * integers; an infinity or NaN is larger than any finite value), from which
+ * the caller finds units of small x. SCX: x is multiplied by sc (a power of
+ * two) before it is converted. */
 template <int NST, int XF32, int EXT, int XG = 0, int SCX = 0>
 __device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8_t * lds, uint32_t cbb,
-                                      const uint8_t * xb, const uint8_t * xbl, f4 * acc, float sc = 1.0f) {
+                                      const uint8_t * xb, const uint8_t * xbl, f4 * acc, float sc = 1.0f,
+                                      u16x2 * xm = nullptr) {
     h4 cw[8][NST], b[8], bl[8];
 #pragma unroll
     for (int s = 0; s < NST; s++) {
@@ -105,6 +113,10 @@ __device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8
             b[t][1] = (_Float16) (SCX ? f1 * sc : f1);
             b[t][2] = (_Float16) (SCX ? f2 * sc : f2);
             b[t][3] = (_Float16) (SCX ? f3 * sc : f3);
+            if (!SCX && xm) {
+                *xm = __builtin_elementwise_max(*xm, __builtin_bit_cast(u16x2, u0 & 0x7fff7fffu));
+                *xm = __builtin_elementwise_max(*xm, __builtin_bit_cast(u16x2, u1 & 0x7fff7fffu));
+            }
         } else {
             b[t] = *(const h4 *) (xb + 8 * t);
             if (XF32) bl[t] = *(const h4 *) (xbl + 8 * t);

@@ -111,6 +111,13 @@ __device__ __forceinline__ uint32_t xr_wave_max(uint32_t m) {
     return m;
 }
 
+/* The largest m over the four lanes that share lane & 15: in the MFMA
+ * layouts here, the lanes of one B column (and of one output column). */
+__device__ __forceinline__ uint32_t xr_col_max(uint32_t m) {
+    m = max(m, (uint32_t) __shfl_xor((int) m, 16, 64));
+    return max(m, (uint32_t) __shfl_xor((int) m, 32, 64));
+}
+
 /* The rescale exponent k for the largest finite |x|, as f32 bits M: 0 when
  * M is zero or in range, else the k that brings M to exponent 14. */
 __device__ __forceinline__ int xr_shift_of(uint32_t M) {

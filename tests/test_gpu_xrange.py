@@ -74,13 +74,13 @@ def per_col_err(got, xf, W):
 
 # rows, cols, columns, f32 x, shifts; the paths: one column staged in one
 # pass; f32 x (ring kernel, hi + lo f16); several columns staged in LDS;
-# several columns read from global memory per step (which checks overflow
-# per unit and leaves small x to f16's subnormals, so only shifts up).
+# several columns read from global memory per step (which checks the range
+# per unit and per column after the fact, and runs a unit again scaled).
 VQ_CASES = [
     (256, 2560, 1, False, (20, -30, 100)),
     (64, 256, 1, True, (20, -30)),
     (33, 2560, 8, False, (20, -30)),
-    (64, 4096, 8, False, (20, 12)),
+    (64, 4096, 8, False, (20, 12, -30, -100)),
 ]
 
 
@@ -127,6 +127,33 @@ def test_vq_gemv_spikes_and_mixed_columns(sm, ref, dev, rows, cols, ncol, f32):
         err = per_col_err(got, xm, W)
         print(f"vq mixed columns {rows}x{cols} N={ncol}: relL2 {err:.2e}")
         assert err <= TIGHT
+
+
+def test_vq_gemv_small_columns_from_global(sm, ref, dev):
+    """x read from global memory (8 columns of 4096): columns of very small
+    values beside ordinary ones. Column 1 holds N(0,1) * 2^-20 with ALL its
+    values kept, down to bf16's smallest normals, and column 2 N(0,1) * 2^-40
+    (below f16's smallest subnormal). Converted to f16 as they are, such
+    columns would lose their values below 2^-14 (2^-24 apart at best); each
+    column is brought into range by a power of two of its own, so every
+    column meets the bar and the ordinary columns are unchanged."""
+    rows, cols, ncol = 64, 4096, 8
+    data = sm.synth_container(rows + 29, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    xf = base_x(sm, 93, ncol, cols)
+    y_plain = run_vq(sm, dev, dc, xf, rows, False)
+    full = sm.bf16_to_f32(sm.synth_bf16(94, 2 * cols)).reshape(2, cols)
+    xs = xf.copy()
+    xs[1] = np.ldexp(full[0], -20)
+    xs[2] = np.ldexp(full[1], -40)
+    got = run_vq(sm, dev, dc, xs, rows, False)
+    want = xs.astype(np.float64) @ W.T
+    errs = [rel_l2(got[n], want[n]) for n in range(ncol)]
+    print("small columns from global memory, relL2 per column:", [f"{e:.1e}" for e in errs])
+    assert max(errs) <= TIGHT
+    keep = [n for n in range(ncol) if n not in (1, 2)]
+    assert np.array_equal(got[keep], y_plain[keep])
 
 
 @pytest.mark.parametrize("rows,cols,ncol", [(256, 2560, 1), (64, 4096, 8)], ids=["one-column", "x-from-global"])
