@@ -626,16 +626,24 @@ def bench_prefill(args, sm, torch, dev):
         def step():
             for m, x, y, _, _ in mats:
                 m.prefill(x, y, stream=stream)
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(args.steps):
-            step()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
+
+        def timed():
+            for _ in range(args.warmup):
+                step()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                step()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / args.steps
+        # the default: the two stages folded into one f16 weight; then the
+        # same step with each stage's exact codewords accumulated apart
+        assert sm.prefill_fold()
+        ms = timed()
+        with sm.prefill_mode(False):
+            ms_apart = timed()
         # the same step through the reference's ABI: xT [cols][ntok] f32, one
         # launch per stage, tiled variant 2 with the runtime's 128 x 64 tile
         # (vq-model-gpu.cu:296-299, :838-851); the null stream, as it uses
@@ -663,15 +671,20 @@ def bench_prefill(args, sm, torch, dev):
     log(f"  reference ABI (xT f32, one launch per stage): {ms_ref * 1e3:.1f} us/step, "
         f"{flops / (ms_ref * 1e-3) / 1e12:.1f} TFLOP/s")
     nbytes = sum(m.host.data.nbytes + 2 * ntok * c + 4 * ntok * r for m, _, _, r, c in mats)
-    log(f"  prefill {ntok} tokens, up + down: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s")
+    log(f"  prefill {ntok} tokens, up + down: {ms * 1e3:.1f} us/step, {tflops:.1f} TFLOP/s (stages folded); "
+        f"{ms_apart * 1e3:.1f} us/step, {flops / (ms_apart * 1e-3) / 1e12:.1f} TFLOP/s (stages apart)")
     return {"metric": "prefill GEMM us/step (N=512, FFN up + down)", "value": round(ms * 1e3, 2), "unit": "us/step",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16xf16->f32 (bf16 x)",
             "data": "synthetic (seeded, random-init weights of the real shapes)",
-            "config": {"workload": "prefill GEMM, 512 bf16 tokens x (10240x2560 and 2560x10240 VQ)", "tokens": ntok},
+            "config": {"workload": "prefill GEMM, 512 bf16 tokens x (10240x2560 and 2560x10240 VQ)", "tokens": ntok,
+                       "stages": "folded (g0 c0 + g1 c1 rounded to one f16 weight)"},
             "roofline": {"bound": "mfma", "kernel": "prefill_cw_kernel", "achieved": round(tflops, 1),
                          "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / PEAK_F16_TFLOPS, 4),
                          "traffic": None, "flops_per_step": flops, "bytes_per_step": int(nbytes)},
+            "stages_apart": {"us_per_step": round(ms_apart * 1e3, 2),
+                             "tflops": round(flops / (ms_apart * 1e-3) / 1e12, 1),
+                             "mode": "sparkmv_prefill_fold(0): each stage's exact codewords, gains in f32"},
             "reference_abi": {"us_per_step": round(ms_ref * 1e3, 2),
                               "tflops": round(flops / (ms_ref * 1e-3) / 1e12, 1),
                               "route": "vqg_prefill_launch_tile variant 2, xT [cols][512] f32, one launch per stage"}}

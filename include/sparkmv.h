@@ -183,8 +183,9 @@ int sparkmv_q8_0_dequant(const void * blocks, int rows, int cols, float * out, v
  * y is [ntok][ldy] f32, y (+)= W x_t for each token t. Replaces the
  * transpose + vqg_prefill_launch_tile route of tools/vq/gpu/vq-model-gpu.cu:838-851, :899-900.
  * DQV3 dim-4 matrices with 16-byte aligned x rows run on the matrix cores
- * (weights decoded to f16 tiles, f32 accumulation, like the reference's
- * f16 tiled kernel); any other call runs the one-thread-per-output kernel. */
+ * (f16 codewords from an LDS codebook, x as f16, f32 accumulation, like the
+ * reference's f16 tiled kernel; two stages as sparkmv_prefill_fold says);
+ * any other call runs the one-thread-per-output kernel. */
 int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
                        const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy,
                        int accumulate, void * stream);
@@ -201,6 +202,17 @@ int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc
 int sparkmv_vq_prefill_noalloc(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
                                const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy,
                                int accumulate, void * stream);
+/* How the matrix-core prefill treats two stages, process-wide. 1 (the
+ * default): the stages fold into one f16 weight g0 c0 + g1 c1 before the
+ * MFMA, one more rounding per weight (about 2e-4 relative L2 at the FFN
+ * shapes, inside the prefill's 1e-3 gate). 0: each stage's exact f16
+ * codewords multiply x in their own f32 accumulators and the row gains
+ * apply at the end, the reference's per-stage arithmetic
+ * (decode-gpu.cu:359-501, one launch per stage there), about 16 % slower on
+ * the FFN pair. Matrices whose codebooks do not fit LDS (8192 entries, two
+ * stages) always use decoded f16 weight tiles. Returns the previous setting;
+ * on < 0 only reads it. Calls that overlap a change see either setting. */
+int sparkmv_prefill_fold(int on);
 
 /* ---- decode-set plan: a recorded chain of matvec launches ----
  * The per-token matvec chain of the forward (tools/vq/gpu/vq-model-gpu.cu:776-835
@@ -386,9 +398,29 @@ int sparkmv_model_replay(void * model, uint32_t token, int pos, void * stream);
  * pos .. pos + ntok - 1, each attending causally to the positions up to its
  * own; every matvec runs once over the block's columns and the head gives
  * logits [ntok][vocab] (a Q8_0 head column equals its one-column result bit
- * for bit). Fills those cache rows. The first block allocates the model's
- * block buffers. */
+ * for bit). Fills those cache rows. Without a reservation the first block
+ * allocates the model's block buffers. */
 int sparkmv_model_verify(void * model, const uint32_t * tokens, int ntok, int pos, float * logits, void * stream);
+/* A prompt chunk (vq-model-gpu.cu:858-943 forward_batch; with logits also
+ * :946-953 tail_logits): ntok <= 512 consecutive tokens at positions
+ * pos .. pos + ntok - 1, each attending causally to the positions up to its
+ * own; fills those cache rows. Matvecs over up to 16 tokens run the batched
+ * GEMV (each column the decode arithmetic); longer chunks run the prefill
+ * GEMM, whose x enters the matrix cores as f16, as in the reference's prompt
+ * path. logits, when non-null, receives the last token's vocab logits; NULL
+ * skips the head, as forward_batch does between chunks. The host token array
+ * is read before the call returns (it waits for the stream's earlier work).
+ * Refused past max_ctx or the vocabulary. A chunk longer than the
+ * reservation (re)allocates the block buffers after a device
+ * synchronization; split-K prefills draw their partial sums from the
+ * library's stream-ordered pool (allocated on first use, kept after). */
+int sparkmv_model_forward_batch(void * model, const uint32_t * tokens, int ntok, int pos, float * logits,
+                                void * stream);
+/* Allocate the block buffers for verify blocks and prompt chunks of up to
+ * ntok tokens (1..512; at least 8 are reserved) now, so that those calls
+ * allocate nothing. A larger reservation than the current one synchronizes
+ * the device and replaces the buffers. */
+int sparkmv_model_reserve(void * model, int ntok);
 /* Keep the first pos cached positions (model.rs:361-381 rollback): refused
  * past the cached length; later steps overwrite the rows it drops. */
 int sparkmv_model_rollback(void * model, int pos);

@@ -518,4 +518,9 @@ int sparkmv_vq_prefill_noalloc(const void * const * stages, int nstages, int dim
                            stream, 1);
 }
 
+int sparkmv_prefill_fold(int on) {
+    if (on < 0) return prefill_fold_on();
+    return prefill_fold_set(on);
+}
+
 }  // extern "C"

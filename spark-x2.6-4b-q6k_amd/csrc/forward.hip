@@ -33,6 +33,7 @@
  * attention launch reserves LDS for its longest window.
  */
 #include "kq.h"
+#include "prefill.h"
 #include "vq.h"
 
 #include <hip/hip_runtime.h>
@@ -479,6 +480,88 @@ __global__ void fw_gelu_mul_kernel(const float * g, const float * u, float * act
     }
 }
 
+/* ---- a prompt chunk: up to kPromptMax consecutive tokens at pos0 .. ----
+ * (vq-model-gpu.cu:858-943 forward_batch). The steps are the verify
+ * block's; the tokens come from device memory, and attention runs without
+ * per-chunk partials (whose buffer grows with tokens x context). */
+constexpr int kPromptMax = 512;
+
+/* Embedding rows of a Q8_0 head: column t = row tok[t] (device). */
+__global__ void fw_q8_0_rows_dev_kernel(const uint8_t * blocks, int cols, const int * tok, float * out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    if (i >= cols) return;
+    const uint8_t * b = blocks + ((size_t) tok[t] * (cols >> 5) + (i >> 5)) * 34;
+    _Float16 d;
+    __builtin_memcpy(&d, b, 2);
+    out[(size_t) t * cols + i] = (float) d * (float) (int8_t) b[2 + (i & 31)];
+}
+
+/* Attention of token t = blockIdx.y (query rotated in qkv, every key of its
+ * window in the cache) for the query heads of kv head blockIdx.x, one wave
+ * per query head: the window in chunks of kAttnChunk positions with a
+ * running maximum m, sum l and output o (each chunk's terms scaled to the
+ * new maximum, the old ones by e^(m_old - m_new)), then o / l times the
+ * head's sigmoid gate. The same softmax as the CPU's (model.rs:520-557),
+ * summed chunk by chunk in position order. */
+template <int VPL>
+__global__ __launch_bounds__(256) void fw_attn_prompt_kernel(const float * qkv, int ldq, int kvd, const float * kc,
+                                                              const float * vc, const float * gate, int ldg, int pos0,
+                                                              int window, int heads, int kv_heads, float scale,
+                                                              float * out, uint16_t * out16) {
+    constexpr int hd = 64 * VPL, C = kAttnChunk;
+    typedef float fv __attribute__((ext_vector_type(VPL)));
+    const int t = blockIdx.y, pos = pos0 + t;
+    const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
+    const int n = pos + 1 - start;
+    const int kvh = blockIdx.x, G = heads / kv_heads;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = kvh * G + wave;
+    const fv q = *(const fv *) (qkv + (size_t) t * ldq + (size_t) h * hd + lane * VPL);
+    const float * kb = kc + (size_t) start * kvd + (size_t) kvh * hd + lane * VPL;
+    const float * vb = vc + (size_t) start * kvd + (size_t) kvh * hd + lane * VPL;
+    float m = -INFINITY, l = 0.0f;
+    fv o = (fv) 0.0f;
+    for (int j0 = 0; j0 < n; j0 += C) {
+        const int jn = min(C, n - j0);
+        fv kr[C], vr[C];
+#pragma unroll
+        for (int j = 0; j < C; j++) kr[j] = *(const fv *) (kb + (size_t) (j0 + min(j, jn - 1)) * kvd);
+#pragma unroll
+        for (int j = 0; j < C; j++) vr[j] = *(const fv *) (vb + (size_t) (j0 + min(j, jn - 1)) * kvd);
+        float sc[C];
+        float mc = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+            float sv = 0.0f;
+#pragma unroll
+            for (int v = 0; v < VPL; v++) sv += q[v] * kr[j][v];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) sv += __shfl_xor(sv, off, 64);
+            sc[j] = sv * scale;
+            if (j < jn) mc = fmaxf(mc, sc[j]);
+        }
+        const float mn = fmaxf(m, mc);
+        const float a = expf(m - mn);          /* 0 on the first chunk (m = -inf) */
+        l *= a;
+        o *= a;
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+            const float e = j < jn ? expf(sc[j] - mn) : 0.0f;
+            l += e;
+            o += e * vr[j];
+        }
+        m = mn;
+    }
+    const float g = 1.0f / (1.0f + expf(-gate[(size_t) t * ldg + h]));
+    const fv r = o * (1.0f / l) * g;
+    const size_t ob = (size_t) t * heads * hd + (size_t) h * hd + lane * VPL;
+#pragma unroll
+    for (int v = 0; v < VPL; v++) {
+        out[ob + v] = r[v];
+        if (out16) out16[ob + v] = fw_bf16(r[v]);
+    }
+}
+
 /* ------------------------------------------------------------------ host -- */
 
 namespace {
@@ -506,11 +589,15 @@ struct Model {
     int len = 0;
     /* tuned kernels per (rows, cols) of a VQ matvec: variant, threads */
     std::map<std::pair<int, int>, std::pair<int, int>> picks;
-    /* verify-block buffers, allocated at the first block: 8 columns of each
-     * activation, gate rows at the qkv stride, partials per token */
+    /* block buffers (verify blocks and prompt chunks), one allocation at
+     * sparkmv_model_reserve or the first block: vcap columns of each
+     * activation, gate rows at the qkv stride, the tokens, and attention
+     * partials for verify blocks of up to 8 tokens */
     void * vmem = nullptr;
+    int vcap = 0;
     float * vh, * vxn, * vqkv, * vg, * vattn, * vmg, * vmu, * vact, * vpart;
     uint16_t * vxn16, * vattn16, * vact16;
+    int * vtok;
 };
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t) 255; }
@@ -796,25 +883,50 @@ int chain(Model * m, float * logits, hipStream_t s) {
     return kq_gemv_launch(8, m->head_blocks, c.vocab, c.hidden, xin, b16 ? 0 : 1, c.hidden, 1, logits, c.vocab, 0, s);
 }
 
-int alloc_verify(Model * m) {
+/* The block buffers for up to cap tokens (at least 8). A smaller or equal
+ * reservation keeps what is there; a larger one replaces it (the caller
+ * synchronizes first: work in flight may still use the old buffers). */
+int alloc_block(Model * m, int cap) {
+    cap = cap < 8 ? 8 : cap;
+    if (m->vmem && cap <= m->vcap) return 0;
     const sparkmv_model_cfg & c = m->c;
-    const size_t qd = (size_t) c.heads * c.head_dim, kvd = (size_t) c.kv_heads * c.head_dim, N = 8;
+    const size_t qd = (size_t) c.heads * c.head_dim, kvd = (size_t) c.kv_heads * c.head_dim, N = (size_t) cap;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
     const size_t o_h = take(N * c.hidden * 4), o_xn = take(N * c.hidden * 4), o_qkv = take(N * (qd + 2 * kvd) * 4);
     const size_t o_g = take(N * (qd + 2 * kvd) * 4), o_attn = take(N * qd * 4), o_mg = take(N * c.intermediate * 4);
     const size_t o_mu = take(N * c.intermediate * 4), o_act = take(N * c.intermediate * 4);
     const size_t o_xn16 = take(N * c.hidden * 2), o_attn16 = take(N * qd * 2), o_act16 = take(N * c.intermediate * 2);
-    const size_t o_part = take(N * c.heads * (size_t) m->nch_max * (c.head_dim + 2) * 4);
-    hipError_t e = hipMalloc(&m->vmem, off);
-    if (e != hipSuccess) { m->vmem = nullptr; return fail_hip("verify-block buffers", e); }
+    const size_t o_part = take((size_t) 8 * c.heads * (size_t) m->nch_max * (c.head_dim + 2) * 4);
+    const size_t o_tok = take(N * sizeof(int));
+    void * mem = nullptr;
+    hipError_t e = hipMalloc(&mem, off);
+    if (e != hipSuccess) return fail_hip("block buffers", e);
+    if (m->vmem) (void) hipFree(m->vmem);
+    m->vmem = mem;
+    m->vcap = cap;
     uint8_t * b = (uint8_t *) m->vmem;
     m->vh = (float *) (b + o_h); m->vxn = (float *) (b + o_xn); m->vqkv = (float *) (b + o_qkv);
     m->vg = (float *) (b + o_g); m->vattn = (float *) (b + o_attn); m->vmg = (float *) (b + o_mg);
     m->vmu = (float *) (b + o_mu); m->vact = (float *) (b + o_act); m->vpart = (float *) (b + o_part);
     m->vxn16 = (uint16_t *) (b + o_xn16); m->vattn16 = (uint16_t *) (b + o_attn16);
     m->vact16 = (uint16_t *) (b + o_act16);
+    m->vtok = (int *) (b + o_tok);
     return 0;
+}
+
+/* y[t * ldy + r] (+)= W x_t for N tokens of x ([N][cols], the model's x
+ * dtype): up to kMaxCols tokens through the batched GEMV (each column the
+ * decode arithmetic), more through the prefill GEMM (the reference's prompt
+ * path, vq-model-gpu.cu:838-851: x enters the matrix cores as f16). */
+int mat_n(const Model & m, const void * const * st, int rows, int cols, const void * x, float * y, int acc,
+          hipStream_t s, int N, int ldy) {
+    if (N <= kMaxCols) return gemv(m, st, rows, cols, x, y, acc, s, N, ldy);
+    const Layout L = make_layout(m.c.dim, m.c.nc, rows, cols, m.c.v3);
+    const int xf32 = m.c.x_dtype == SPARKMV_X_F32;
+    if (m.c.nstages <= 2 && prefill_mfma_ready(L, m.c.nstages, x, xf32, cols, 0, N))
+        return prefill_mfma_launch(st, m.c.nstages, L, x, xf32, cols, 0, N, y, ldy, acc, s);
+    return prefill_simple_launch(st, m.c.nstages, L, x, xf32, (size_t) cols, 1, N, y, ldy, acc, s);
 }
 
 /* A verify block: the forward of ntok consecutive tokens at pos .. pos + ntok - 1
@@ -894,6 +1006,84 @@ int block(Model * m, const uint32_t * tokens, int N, int pos, float * logits, hi
     return kq_gemv_launch(8, m->head_blocks, c.vocab, c.hidden, xin, b16 ? 0 : 1, c.hidden, N, logits, c.vocab, 0, s);
 }
 
+/* A prompt chunk (vq-model-gpu.cu:858-943 forward_batch): N tokens at
+ * pos .. pos + N - 1 through every layer, the tokens already in m->vtok.
+ * With logits, the final norm and the head of the last token
+ * (vq-model-gpu.cu:946-953 tail_logits). */
+int prompt(Model * m, int N, int pos, float * logits, hipStream_t s) {
+    const sparkmv_model_cfg & c = m->c;
+    const bool b16 = c.x_dtype == SPARKMV_X_BF16;
+    const int qd = c.heads * c.head_dim, kvd = c.kv_heads * c.head_dim, hd = c.head_dim, ldq = qd + 2 * kvd;
+    if (m->head_kind == 0) {
+        hipLaunchKernelGGL(fw_fill_kernel, dim3((N * c.hidden + 255) / 256), dim3(256), 0, s, m->vh, N * c.hidden, 0.0f);
+        if (check_launch("fill launch")) return -1;
+        const Layout L = make_layout(c.dim, c.nc, c.vocab, c.hidden, c.v3);
+        for (int st = 0; st < c.nstages; st++)
+            if (vq_row_dequant_dev_launch(m->head_stages[st], L, m->vtok, m->vh, s, N, (size_t) c.hidden)) return -1;
+    } else {
+        hipLaunchKernelGGL(fw_q8_0_rows_dev_kernel, dim3((c.hidden + 255) / 256, N), dim3(256), 0, s,
+                           (const uint8_t *) m->head_blocks, c.hidden, (const int *) m->vtok, m->vh);
+        if (check_launch("embedding launch")) return -1;
+    }
+    const float scale = 1.0f / sqrtf((float) hd);
+    const void * xin = b16 ? (const void *) m->vxn16 : (const void *) m->vxn;
+    for (int li = 0; li < c.layers; li++) {
+        const sparkmv_model_layer & L = m->layers[li];
+        const bool full = L.full != 0;
+        float * kc = m->kv + (size_t) li * 2 * c.max_ctx * kvd;
+        float * vc = kc + (size_t) c.max_ctx * kvd;
+        if (rmsnorm(*m, m->vh, L.in_norm, s, N, m->vxn, m->vxn16)) return -1;
+        if (N <= kMaxCols) {
+            if (gemv2(*m, L.qkv, ldq, m->vqkv, L.attn_gate, c.heads, m->vg, c.hidden, xin, s, N, ldq)) return -1;
+        } else {
+            if (mat_n(*m, L.qkv, ldq, c.hidden, xin, m->vqkv, 0, s, N, ldq)) return -1;
+            if (mat_n(*m, L.attn_gate, c.heads, c.hidden, xin, m->vg, 0, s, N, ldq)) return -1;
+        }
+        const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
+        const int pdim = rope_dim(hd, full ? c.rope_full_partial : c.rope_slide_partial);
+        const int items = (c.heads + c.kv_heads) * (pdim / 2) > kvd ? (c.heads + c.kv_heads) * (pdim / 2) : kvd;
+        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3((items + 255) / 256, N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd,
+                           c.heads, c.kv_heads, hd, pdim, (float) theta, pos, kc, vc);
+        if (check_launch("rope launch")) return -1;
+        const int window = full ? 0 : c.sliding_window;
+        const dim3 ag((unsigned) c.kv_heads, (unsigned) N), ab((unsigned) (64 * (c.heads / c.kv_heads)));
+        uint16_t * a16 = b16 ? m->vattn16 : nullptr;
+        if (hd == 64)
+            hipLaunchKernelGGL(fw_attn_prompt_kernel<1>, ag, ab, 0, s, m->vqkv, ldq, kvd, kc, vc, m->vg, ldq, pos,
+                               window, c.heads, c.kv_heads, scale, m->vattn, a16);
+        else if (hd == 128)
+            hipLaunchKernelGGL(fw_attn_prompt_kernel<2>, ag, ab, 0, s, m->vqkv, ldq, kvd, kc, vc, m->vg, ldq, pos,
+                               window, c.heads, c.kv_heads, scale, m->vattn, a16);
+        else
+            hipLaunchKernelGGL(fw_attn_prompt_kernel<4>, ag, ab, 0, s, m->vqkv, ldq, kvd, kc, vc, m->vg, ldq, pos,
+                               window, c.heads, c.kv_heads, scale, m->vattn, a16);
+        if (check_launch("attention launch")) return -1;
+        if (mat_n(*m, L.out, c.hidden, qd, b16 ? (const void *) m->vattn16 : (const void *) m->vattn, m->vh, 1, s, N,
+                  c.hidden))
+            return -1;
+        if (rmsnorm(*m, m->vh, L.post_norm, s, N, m->vxn, m->vxn16)) return -1;
+        if (N <= kMaxCols) {
+            if (gemv2(*m, L.gate, c.intermediate, m->vmg, L.up, c.intermediate, m->vmu, c.hidden, xin, s, N,
+                      c.intermediate))
+                return -1;
+        } else {
+            if (mat_n(*m, L.gate, c.intermediate, c.hidden, xin, m->vmg, 0, s, N, c.intermediate)) return -1;
+            if (mat_n(*m, L.up, c.intermediate, c.hidden, xin, m->vmu, 0, s, N, c.intermediate)) return -1;
+        }
+        hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * c.intermediate + 255) / 256), dim3(256), 0, s, m->vmg, m->vmu,
+                           m->vact, b16 ? m->vact16 : nullptr, N * c.intermediate);
+        if (check_launch("gelu launch")) return -1;
+        if (mat_n(*m, L.down, c.hidden, c.intermediate, b16 ? (const void *) m->vact16 : (const void *) m->vact, m->vh,
+                  1, s, N, c.hidden))
+            return -1;
+    }
+    if (!logits) return 0;
+    /* the last token's row: final norm and the head, as one decode step's */
+    if (rmsnorm(*m, m->vh + (size_t) (N - 1) * c.hidden, m->final_norm, s, 1, m->vxn, m->vxn16)) return -1;
+    if (m->head_kind == 0) return gemv(*m, m->head_stages, c.vocab, c.hidden, xin, logits, 0, s);
+    return kq_gemv_launch(8, m->head_blocks, c.vocab, c.hidden, xin, b16 ? 0 : 1, c.hidden, 1, logits, c.vocab, 0, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -920,13 +1110,13 @@ int sparkmv_model_capture(void * model, float * logits, void * stream) {
     const int rc = chain(m, logits, s);
     hipGraph_t g = nullptr;
     e = hipStreamEndCapture(s, &g);
-    if (rc) { if (g) hipGraphDestroy(g); return -1; }
+    if (rc) { if (g) (void) hipGraphDestroy(g); return -1; }
     if (e != hipSuccess) return fail_hip("end capture", e);
     hipGraphExec_t x = nullptr;
     e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
-    if (e != hipSuccess) { hipGraphDestroy(g); return fail_hip("graph instantiate", e); }
-    if (m->exec) hipGraphExecDestroy(m->exec);
-    if (m->graph) hipGraphDestroy(m->graph);
+    if (e != hipSuccess) { (void) hipGraphDestroy(g); return fail_hip("graph instantiate", e); }
+    if (m->exec) (void) hipGraphExecDestroy(m->exec);
+    if (m->graph) (void) hipGraphDestroy(m->graph);
     m->graph = g;
     m->exec = x;
     return 0;
@@ -956,8 +1146,52 @@ int sparkmv_model_verify(void * model, const uint32_t * tokens, int ntok, int po
     for (int t = 0; t < ntok; t++)
         if ((long) tokens[t] >= m->c.vocab) { set_error("token %u is outside the vocabulary", tokens[t]); return -1; }
     if (ready(m)) return -1;
-    if (!m->vmem && alloc_verify(m)) return -1;
+    if (!m->vmem && alloc_block(m, 8)) return -1;
     if (block(m, tokens, ntok, pos, logits, (hipStream_t) stream)) return -1;
+    m->len = pos + ntok;
+    return 0;
+}
+
+int sparkmv_model_reserve(void * model, int ntok) {
+    Model * m = (Model *) model;
+    if (!m) { set_error("model is null"); return -1; }
+    if (ntok < 1 || ntok > kPromptMax) { set_error("a reservation covers 1..%d tokens, not %d", kPromptMax, ntok); return -1; }
+    if (m->vmem && ntok > m->vcap) {
+        /* the old buffers may still be in use by queued work */
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return fail_hip("synchronize before a larger reservation", e);
+    }
+    return alloc_block(m, ntok);
+}
+
+int sparkmv_model_forward_batch(void * model, const uint32_t * tokens, int ntok, int pos, float * logits,
+                                void * stream) {
+    Model * m = (Model *) model;
+    if (!m || !tokens) { set_error("model or tokens is null"); return -1; }
+    if (ntok < 1 || ntok > kPromptMax) { set_error("a prompt chunk holds 1..%d tokens, not %d", kPromptMax, ntok); return -1; }
+    if (pos < 0 || pos + ntok > m->c.max_ctx) {
+        set_error("positions %d..%d exceed the %d-token cache", pos, pos + ntok - 1, m->c.max_ctx);
+        return -1;
+    }
+    for (int t = 0; t < ntok; t++)
+        if ((long) tokens[t] >= m->c.vocab) { set_error("token %u is outside the vocabulary", tokens[t]); return -1; }
+    if (ready(m)) return -1;
+    if (!m->vmem || ntok > m->vcap) {
+        if (m->vmem) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) return fail_hip("synchronize before larger block buffers", e);
+        }
+        if (alloc_block(m, ntok)) return -1;
+    }
+    hipStream_t s = (hipStream_t) stream;
+    /* the tokens go to device memory on the stream; the host array is read
+     * before the call returns */
+    static_assert(sizeof(uint32_t) == sizeof(int), "token width");
+    hipError_t e = hipMemcpyAsync(m->vtok, tokens, (size_t) ntok * sizeof(int), hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return fail_hip("token upload", e);
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail_hip("token upload", e);
+    if (prompt(m, ntok, pos, logits, s)) return -1;
     m->len = pos + ntok;
     return 0;
 }
@@ -1006,8 +1240,8 @@ int sparkmv_model_apply_profile(void * model, const void * profile, uint64_t art
             applied++;
         }
     }
-    if (m->exec) { hipGraphExecDestroy(m->exec); m->exec = nullptr; }
-    if (m->graph) { hipGraphDestroy(m->graph); m->graph = nullptr; }
+    if (m->exec) { (void) hipGraphExecDestroy(m->exec); m->exec = nullptr; }
+    if (m->graph) { (void) hipGraphDestroy(m->graph); m->graph = nullptr; }
     set_error("profile: %d geometries take their tuned kernel, %d entries are not runnable here (heuristic kept)",
               applied, refused);
     return applied;

@@ -26,6 +26,12 @@ int prefill_mfma_launch(const void * const * stages, int nst, const Layout & L, 
                         int xt, int ntok, float * y, int ldy, int accumulate, hipStream_t s,
                         void * fixed_ws = nullptr);
 
+/* Whether two-stage prefills fold their stages into one f16 weight (the
+ * default; off: each stage's exact codewords accumulate apart).
+ * Process-wide. */
+int prefill_fold_on();
+int prefill_fold_set(int on);   /* returns the previous setting */
+
 /* Bytes of the no-allocation prefill's scratch (split-K partial sums), one
  * array per GPU: the 2560 x 10240 FFN down matrix at 512 tokens needs 26 MB. */
 constexpr size_t kPrefillScratchBytes = 32u << 20;

@@ -23,6 +23,8 @@
 
 #include <string.h>
 
+#include <atomic>
+
 namespace sparkmv {
 
 __device__ __forceinline__ float pf_f16(uint16_t h) {
@@ -651,7 +653,7 @@ __global__ __launch_bounds__(kCThreads) void prefill_cw_kernel(const CwArgs P) {
                 v[i] = t;
             }
             float * yp = yb + (size_t) tok * P.ldy + row;
-            if (row + 4 <= P.rows) {
+            if (row + 4 <= P.rows && !((uintptr_t) yp & 15u)) {
                 if (P.accumulate) v += *(const pf_f4 *) yp;
                 *(pf_f4 *) yp = v;
             } else {
@@ -738,7 +740,8 @@ static int prefill_cw_ready(const Layout & L, int nst, const void * x, int xf32,
                             const float * y, int ldy) {
     if (!prefill_mfma_ready(L, nst, x, xf32, ldx, xt, ntok)) return 0;
     if (xt && ntok % 4) return 0;
-    if (((uintptr_t) y & 15u) || ldy % 4) return 0;
+    (void) y;
+    (void) ldy;
     return prefill_cw_lds(nst, L.nc) <= 160 * 1024;
 }
 
@@ -758,6 +761,12 @@ static int prefill_cw_splits(int rows, int ntok, int nk) {
     }
     return best;
 }
+
+static std::atomic<int> g_prefill_fold{1};
+
+int prefill_fold_on() { return g_prefill_fold.load(std::memory_order_relaxed); }
+
+int prefill_fold_set(int on) { return g_prefill_fold.exchange(on ? 1 : 0); }
 
 /* The no-allocation form's split slices: one file-scope device array of
  * kPrefillScratchBytes, which every GPU the library runs on holds until the
@@ -809,12 +818,8 @@ static int cw_workspace(size_t bytes, hipStream_t s, void ** out) {
     return e == hipSuccess ? 0 : fail_hip("split workspace", e);
 }
 
-template <int NST, int EXT, int XF32, int XT>
-static int prefill_cw_t(const CwArgs & P, int nsplit, hipStream_t s) {
-    /* two stages fold into one f16 weight (one MFMA per block, measured
-     * about 10 % faster on the FFN pair than accumulating the stages apart);
-     * one stage keeps its exact codewords */
-    constexpr int FOLD = NST == 2 ? 1 : 0;
+template <int NST, int EXT, int XF32, int XT, int FOLD>
+static int prefill_cw_tf(const CwArgs & P, int nsplit, hipStream_t s) {
     static size_t opted = 0;
     const size_t lds = prefill_cw_lds(NST, P.nc);
     const void * fn = (const void *) prefill_cw_kernel<NST, EXT, XF32, XT, FOLD>;
@@ -827,6 +832,20 @@ static int prefill_cw_t(const CwArgs & P, int nsplit, hipStream_t s) {
     launch_kernel(prefill_cw_kernel<NST, EXT, XF32, XT, FOLD>, grid, dim3(kCThreads), (uint32_t) lds, s, P);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("codeword prefill launch", e);
+}
+
+/* Two stages fold by default into one f16 weight (one MFMA per block, 16 %
+ * faster on the FFN pair than running them apart, and one more rounding of
+ * each weight). With the fold switched off each stage's exact codewords
+ * accumulate in their own registers and the gains apply in f32 at the end,
+ * the reference's per-stage arithmetic (decode-gpu.cu:359-501). One stage
+ * always keeps its exact codewords. */
+template <int NST, int EXT, int XF32, int XT>
+static int prefill_cw_t(const CwArgs & P, int nsplit, hipStream_t s) {
+    if constexpr (NST == 2) {
+        if (prefill_fold_on()) return prefill_cw_tf<2, EXT, XF32, XT, 1>(P, nsplit, s);
+    }
+    return prefill_cw_tf<NST, EXT, XF32, XT, 0>(P, nsplit, s);
 }
 
 static int prefill_cw_launch(const void * const * stages, int nst, const Layout & L, const void * x, int xf32,
@@ -843,7 +862,9 @@ static int prefill_cw_launch(const void * const * stages, int nst, const Layout 
     P.stream_off = (uint32_t) L.stream_off;
     P.mrow = (uint32_t) L.mrow;
     P.prow = (uint32_t) L.prow;
-    const int nk = L.cols / kPK, nsplit = prefill_cw_splits(L.rows, ntok, nk);
+    /* the split reduction stores four rows at once: y in 16-byte aligned rows */
+    const int y_vec = !((uintptr_t) y & 15u) && ldy % 4 == 0;
+    const int nk = L.cols / kPK, nsplit = y_vec ? prefill_cw_splits(L.rows, ntok, nk) : 1;
     P.nkc = nk / nsplit;
     void * ws = nullptr;
     if (nsplit > 1) {

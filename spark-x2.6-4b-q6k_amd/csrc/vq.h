@@ -48,8 +48,10 @@ int vq_launch(const VqCall & c);
 int vq_dequant_launch(const void * payload, const Layout & L, float * out, int accumulate, hipStream_t s);
 /* Decode one row of one stage into out (cols f32), accumulating. */
 int vq_row_dequant_launch(const void * payload, const Layout & L, int row, float * out, hipStream_t s);
-/* the same with the row read from device memory at run time */
-int vq_row_dequant_dev_launch(const void * payload, const Layout & L, const int * drow, float * out, hipStream_t s);
+/* the same with the rows read from device memory at run time: row
+ * drow[i] into out + i * ldo, for i < nrows */
+int vq_row_dequant_dev_launch(const void * payload, const Layout & L, const int * drow, float * out, hipStream_t s,
+                              int nrows = 1, size_t ldo = 0);
 /* y[r] += dot(W row r, x): the plain f32 bandwidth yardstick. */
 int f32_gemv_launch(const float * w, const float * x, float * y, int rows, int cols, hipStream_t s);
 

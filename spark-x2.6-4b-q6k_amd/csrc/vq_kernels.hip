@@ -713,9 +713,12 @@ __global__ void vq_dequant_kernel(const uint8_t * p, const Layout L, float * out
 
 /* drow, when given, holds the row in device memory (a captured graph reads
  * the token it is replayed for); rows past the matrix decode nothing. */
-__global__ void vq_row_dequant_kernel(const uint8_t * p, const Layout L, int row, const int * drow, float * out) {
+/* Row `row` (or drow[blockIdx.y], read on the device) into out + blockIdx.y * ldo. */
+__global__ void vq_row_dequant_kernel(const uint8_t * p, const Layout L, int row, const int * drow, float * out,
+                                      size_t ldo) {
     const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (drow) row = *drow;
+    if (drow) row = drow[blockIdx.y];
+    out += blockIdx.y * ldo;
     if (i >= L.nidx_row || row < 0 || row >= L.rows) return;
     const uint16_t * cb = (const uint16_t *) (p + L.cb_off);
     const float g = f16_to_f32(((const uint16_t *) (p + L.gain_off))[row]);
@@ -1176,15 +1179,17 @@ int vq_dequant_launch(const void * payload, const Layout & L, float * out, int a
 int vq_row_dequant_launch(const void * payload, const Layout & L, int row, float * out, hipStream_t s) {
     const int threads = 256;
     hipLaunchKernelGGL(vq_row_dequant_kernel, dim3((unsigned) ((L.nidx_row + threads - 1) / threads)), dim3(threads),
-                       0, s, (const uint8_t *) payload, L, row, (const int *) nullptr, out);
+                       0, s, (const uint8_t *) payload, L, row, (const int *) nullptr, out, (size_t) 0);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("row dequant launch", e);
 }
 
-int vq_row_dequant_dev_launch(const void * payload, const Layout & L, const int * drow, float * out, hipStream_t s) {
+int vq_row_dequant_dev_launch(const void * payload, const Layout & L, const int * drow, float * out, hipStream_t s,
+                              int nrows, size_t ldo) {
     const int threads = 256;
-    hipLaunchKernelGGL(vq_row_dequant_kernel, dim3((unsigned) ((L.nidx_row + threads - 1) / threads)), dim3(threads),
-                       0, s, (const uint8_t *) payload, L, 0, drow, out);
+    if (nrows < 1) { set_error("row dequant needs at least one row"); return -1; }
+    hipLaunchKernelGGL(vq_row_dequant_kernel, dim3((unsigned) ((L.nidx_row + threads - 1) / threads), (unsigned) nrows),
+                       dim3(threads), 0, s, (const uint8_t *) payload, L, 0, drow, out, ldo);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail_hip("row dequant launch", e);
 }

@@ -123,6 +123,7 @@ SIGNATURES = {
     "sparkmv_q8_0_dequant": (_I, [_P, _I, _I, _P, _P]),
     "sparkmv_vq_prefill": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
     "sparkmv_vq_prefill_noalloc": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
+    "sparkmv_prefill_fold": (_I, [_I]),
     "sparkmv_plan_create": (_P, []),
     "sparkmv_plan_destroy": (None, [_P]),
     "sparkmv_plan_size": (_I, [_P]),
@@ -171,6 +172,8 @@ SIGNATURES = {
     "sparkmv_model_capture": (_I, [_P, _P, _P]),
     "sparkmv_model_replay": (_I, [_P, ctypes.c_uint32, _I, _P]),
     "sparkmv_model_verify": (_I, [_P, ctypes.POINTER(ctypes.c_uint32), _I, _I, _P, _P]),
+    "sparkmv_model_forward_batch": (_I, [_P, ctypes.POINTER(ctypes.c_uint32), _I, _I, _P, _P]),
+    "sparkmv_model_reserve": (_I, [_P, _I]),
     "sparkmv_model_rollback": (_I, [_P, _I]),
     "sparkmv_model_len": (_I, [_P]),
     "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
@@ -498,6 +501,31 @@ def gemv_multi(mats, x, ys, ncols=1, accumulate=False, variant=0, stream=None):
                                       _stream_ptr(stream)), "vq gemv multi")
 
 
+def prefill_fold(on=None):
+    """The two-stage prefill's mode, process-wide: True (default) folds the
+    stages into one f16 weight, False runs each stage's exact codewords
+    apart. With no argument, returns the current setting; else sets it and
+    returns the previous one."""
+    prev = lib().sparkmv_prefill_fold(-1 if on is None else int(bool(on)))
+    return bool(prev)
+
+
+class prefill_mode:
+    """Context manager: the two-stage prefill folded (True) or with its
+    stages apart (False) inside the block, the previous mode after it."""
+
+    def __init__(self, fold):
+        self.fold = bool(fold)
+
+    def __enter__(self):
+        self.prev = prefill_fold(self.fold)
+        return self
+
+    def __exit__(self, *exc):
+        prefill_fold(self.prev)
+        return False
+
+
 def kquant_gemv(kind, blocks, rows, cols, x, y, ncols=1, accumulate=False, stream=None):
     """kind 'q6_k' or 'q8_0'; blocks a device uint8 tensor of ggml blocks."""
     torch = _torch()
@@ -571,6 +599,19 @@ class Model:
         arr = (ctypes.c_uint32 * len(tokens))(*[int(t) for t in tokens])
         check(lib().sparkmv_model_verify(self.h, arr, len(tokens), int(pos), logits.data_ptr(), _stream_ptr(stream)),
               "model verify")
+
+    def forward_batch(self, tokens, pos, logits=None, stream=None):
+        """A prompt chunk of up to 512 tokens at pos .. (vq-model-gpu.cu:858-953
+        forward_batch + tail_logits): fills their cache rows; logits (device
+        f32 [vocab]), when given, gets the last token's."""
+        arr = (ctypes.c_uint32 * len(tokens))(*[int(t) for t in tokens])
+        check(lib().sparkmv_model_forward_batch(self.h, arr, len(tokens), int(pos),
+                                                logits.data_ptr() if logits is not None else None,
+                                                _stream_ptr(stream)), "model forward batch")
+
+    def reserve(self, ntok):
+        """Allocate the block buffers for up to ntok tokens now."""
+        check(lib().sparkmv_model_reserve(self.h, int(ntok)), "model reserve")
 
     def rollback(self, pos):
         """Keep the first pos cached positions (model.rs:361-381)."""

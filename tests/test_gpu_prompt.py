@@ -1,0 +1,167 @@
+"""Long contexts and the prompt path of the GPU forward, against the oracle's
+restatement of tools/vq-runtime/src/model.rs:441-591 (oracle/forward.py).
+
+The small model of test_gpu_forward.py with a 256-position cache and a
+40-position sliding window, run over 210 tokens:
+
+  - the decode step (sparkmv_model_forward) at every position, checked at
+    positions on both sides of 16 (the attention chunk), of 40 (the window
+    edge, after which a sliding layer's chunks start mid-window) and of 192
+    (twelve chunks: past it the full layer's combine runs its four-chunk
+    loop), with every KV row; then one verify block of 8 at position 210;
+  - the prompt path (sparkmv_model_forward_batch, vq-model-gpu.cu:858-953):
+    chunks of 100 (the prefill GEMM), 10 (the batched GEMV) and 100 tokens
+    without logits, then decode steps on the cache the chunks wrote.
+
+Bars: decode steps and chunks of at most 16 tokens keep the decode
+arithmetic, 1e-5 with f32 activations. Longer chunks run the prefill GEMM,
+where x enters the matrix cores as f16, as in the reference's own prompt
+path: f32 activations then meet 5e-3 (each matvec input rounded to f16's
+11 bits), bf16 activations the decode tests' 2e-2.
+"""
+import numpy as np
+import pytest
+
+import forward as fw
+from test_gpu_forward import CFG, build, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+LONG = dict(CFG, max_ctx=256, sliding_window=40)
+NTOK = 210
+CHECK_POS = [0, 1, 15, 16, 17, 39, 40, 41, 56, 57, 191, 192, 193, 208, 209]
+
+
+def tokens(n, seed=5):
+    return [int(t) for t in np.random.default_rng(seed).integers(0, LONG["vocab"], n)]
+
+
+def kv_rows(model, dev, li, n, kvd):
+    """The first n rows of layer li's K and V cache, copied device to device."""
+    import ctypes
+    import torch
+    hip = ctypes.CDLL("libamdhip64.so")
+    out = []
+    for ptr in model.kv(li):
+        buf = torch.empty((n, kvd), dtype=torch.float32, device=dev)
+        assert hip.hipMemcpy(ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(ptr), ctypes.c_size_t(n * kvd * 4),
+                             ctypes.c_int(3)) == 0
+        out.append(buf.cpu().numpy())
+    return out
+
+
+def check_kv(model, oracle, dev, n, bar, label):
+    kvd = LONG["kv_heads"] * LONG["head_dim"]
+    worst = 0.0
+    for li in range(LONG["layers"]):
+        for got, want in zip(kv_rows(model, dev, li, n, kvd), (oracle.kv_k[li], oracle.kv_v[li])):
+            worst = max(worst, rel_l2(got, want[:n]))
+    print(f"{label}: KV rows 0..{n - 1} worst relL2 {worst:.2e}")
+    assert worst <= bar
+
+
+@pytest.mark.parametrize("head_kind", ["q8_0", "vq"])
+def test_long_context_decode_and_verify(sm, ref, dev, head_kind):
+    import torch
+    model, oracle = build(sm, ref, dev, head_kind, sm.X_F32, LONG)
+    toks = tokens(NTOK + 8)
+    logits = torch.full((LONG["vocab"],), float("nan"), device=dev)
+    worst = 0.0
+    for pos in range(NTOK):
+        model.forward(toks[pos], pos, logits)
+        want = oracle.forward(toks[pos], pos)
+        if pos in CHECK_POS:
+            torch.cuda.synchronize()
+            err = rel_l2(logits.cpu().numpy(), want)
+            worst = max(worst, err)
+            print(f"head {head_kind} pos {pos}: logits relL2 {err:.2e}")
+            assert err <= 1e-5, pos
+    torch.cuda.synchronize()
+    check_kv(model, oracle, dev, NTOK, 1e-5, f"head {head_kind} decode")
+    block = toks[NTOK:NTOK + 8]
+    out = torch.full((8, LONG["vocab"]), float("nan"), device=dev)
+    model.verify(block, NTOK, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i, t in enumerate(block):
+        err = rel_l2(got[i], oracle.forward(t, NTOK + i))
+        print(f"head {head_kind} verify row {i} (pos {NTOK + i}): relL2 {err:.2e}")
+        assert err <= 1e-5
+    print(f"head {head_kind}: worst decode relL2 {worst:.2e}")
+
+
+@pytest.mark.parametrize("head_kind,xd", [("q8_0", "f32"), ("vq", "f32"), ("q8_0", "bf16")])
+def test_forward_batch_against_oracle(sm, ref, dev, head_kind, xd):
+    import torch
+    x_dtype = sm.X_F32 if xd == "f32" else sm.X_BF16
+    bar = 5e-3 if xd == "f32" else 2e-2
+    model, oracle = build(sm, ref, dev, head_kind, x_dtype, LONG)
+    model.reserve(128)
+    toks = tokens(NTOK + 2, seed=9)
+    logits = torch.full((LONG["vocab"],), float("nan"), device=dev)
+    want = None
+    for p in range(100):
+        want = oracle.forward(toks[p], p)
+    model.forward_batch(toks[:100], 0, logits)
+    torch.cuda.synchronize()
+    err = rel_l2(logits.cpu().numpy(), want)
+    print(f"head {head_kind} x {xd}: chunk 0..99 (prefill GEMM), last logits relL2 {err:.2e}")
+    assert err <= bar
+    for p in range(100, 110):
+        want = oracle.forward(toks[p], p)
+    model.forward_batch(toks[100:110], 100, logits)
+    torch.cuda.synchronize()
+    err = rel_l2(logits.cpu().numpy(), want)
+    print(f"head {head_kind} x {xd}: chunk 100..109 (batched GEMV), last logits relL2 {err:.2e}")
+    assert err <= bar
+    for p in range(110, NTOK):
+        oracle.forward(toks[p], p)
+    model.forward_batch(toks[110:NTOK], 110)      # no logits, as between prompt chunks
+    assert len(model) == NTOK
+    for p in (NTOK, NTOK + 1):
+        model.forward(toks[p], p, logits)
+        torch.cuda.synchronize()
+        err = rel_l2(logits.cpu().numpy(), oracle.forward(toks[p], p))
+        print(f"head {head_kind} x {xd}: decode at {p} after the chunks, relL2 {err:.2e}")
+        assert err <= bar
+    if xd == "f32":
+        check_kv(model, oracle, dev, NTOK + 2, bar, f"head {head_kind} prompt")
+
+
+def test_forward_batch_short_chunk_is_exact(sm, ref, dev):
+    """A chunk of 12 tokens (at most 16: every matvec on the batched GEMV)
+    keeps the decode arithmetic: 1e-5 with f32 activations for the last
+    logits and every KV row, the attention of each token over the chunk's
+    own earlier positions included."""
+    import torch
+    model, oracle = build(sm, ref, dev, "q8_0", sm.X_F32, LONG)
+    toks = tokens(12, seed=13)
+    want = None
+    for p, t in enumerate(toks):
+        want = oracle.forward(t, p)
+    logits = torch.full((LONG["vocab"],), float("nan"), device=dev)
+    model.forward_batch(toks, 0, logits)
+    torch.cuda.synchronize()
+    err = rel_l2(logits.cpu().numpy(), want)
+    print(f"12-token chunk: last logits relL2 {err:.2e}")
+    assert err <= 1e-5
+    check_kv(model, oracle, dev, 12, 1e-5, "12-token chunk")
+
+
+def test_forward_batch_refusals(sm, ref, dev):
+    import torch
+    model, _ = build(sm, ref, dev, "q8_0", sm.X_F32, LONG)
+    logits = torch.zeros(LONG["vocab"], device=dev)
+    with pytest.raises(sm.SparkmvError):
+        model.forward_batch([1] * 513, 0, logits)
+    assert "1..512 tokens" in sm.last_error()
+    with pytest.raises(sm.SparkmvError):
+        model.forward_batch([1] * 20, LONG["max_ctx"] - 10, logits)
+    assert "exceed" in sm.last_error()
+    with pytest.raises(sm.SparkmvError):
+        model.forward_batch([1, LONG["vocab"]], 0, logits)
+    assert "outside the vocabulary" in sm.last_error()
+    for bad in (0, 513):
+        with pytest.raises(sm.SparkmvError):
+            model.reserve(bad)
+    assert len(model) == 0

@@ -323,27 +323,70 @@ def test_prefill_mfma_against_oracle(sm, ref, dev, rows, cols, ntok, nc, f32):
     inside a four-row store), f32 x, the long 10240-column rows of down_proj
     (256 x 10240 x 64 tokens splits K sixteen ways: one row tile, one token
     tile), and an 8192-entry two-stage codebook, whose LDS only the weight-
-    tile kernel holds (64 x 512 and 10200 x 256). Two stages enter the MFMA
-    as one f16 weight (one rounding of the exact decode), so the bar is the
-    1e-3 relative L2 of the GEMM gate, not the GEMV's f32-exact 1e-5."""
+    tile kernel holds (64 x 512 and 10200 x 256).
+
+    Both two-stage modes run. With the stages apart (sparkmv_prefill_fold
+    0), a 4096-entry codebook and bf16 x, each stage's exact codewords meet x
+    (exact in f16) with f32 accumulation: the GEMV's 1e-5. The default folds
+    each weight g0 c0 + g1 c1 to f16 (so does the weight-tile kernel, in
+    both modes), and f32 x rounds to f16 as the reference's prefill rounds
+    it: those meet the GEMM gate, 1e-3."""
     import torch
     data = sm.synth_container(rows * 3 + ntok, rows, cols, 4, nc, 2, 1)
     W = ref.decode(data).astype(np.float64)
     dc = sm.DeviceContainer(data)
     xt, xf = _x(sm, ntok + 5, ntok, cols, f32)
-    y = torch.full((ntok, rows), float("nan"), device=dev)
-    dc.prefill(xt, y)
-    torch.cuda.synchronize()
-    got = y.cpu().numpy()
     want = xf.astype(np.float64) @ W.T
-    err = rel_l2(got, want)
-    print(f"prefill {rows}x{cols} ntok {ntok} nc {nc} f32 {f32}: relL2 {err:.2e}")
-    assert err <= BAR
-    # accumulate adds into y
-    y2 = torch.from_numpy(got.copy()).to(dev)
-    dc.prefill(xt, y2, accumulate=True)
-    torch.cuda.synchronize()
-    assert rel_l2(y2.cpu().numpy(), 2 * want) <= BAR
+    for fold in (True, False):
+        with sm.prefill_mode(fold):
+            y = torch.full((ntok, rows), float("nan"), device=dev)
+            dc.prefill(xt, y)
+            torch.cuda.synchronize()
+            got = y.cpu().numpy()
+            err = rel_l2(got, want)
+            bar = BAR if fold or f32 or nc > 4096 else TIGHT
+            print(f"prefill {rows}x{cols} ntok {ntok} nc {nc} f32 {f32} fold {fold}: relL2 {err:.2e} (bar {bar:.0e})")
+            assert err <= bar
+            # accumulate adds into y
+            y2 = torch.from_numpy(got.copy()).to(dev)
+            dc.prefill(xt, y2, accumulate=True)
+            torch.cuda.synchronize()
+            assert rel_l2(y2.cpu().numpy(), 2 * want) <= bar
+    assert sm.prefill_fold() is True
+
+
+@pytest.mark.parametrize("rows,cols,ntok", [(1024, 2560, 256), (512, 10240, 130)])
+def test_prefill_fold_error_bound(sm, ref, dev, rows, cols, ntok):
+    """The two-stage switch (sparkmv_prefill_fold): stages apart meet the
+    GEMV's 1e-5 against the oracle's exact decode; folded into one f16
+    weight (the default) they add that weight's rounding, bounded by the
+    GEMM gate 1e-3 against both the oracle and the exact path, and not zero
+    (the switch took effect). The setting is process-wide and restored."""
+    import torch
+    data = sm.synth_container(0x7F00 + cols, rows, cols, 4, 4096, 2, 1)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    xt, xf = _x(sm, 0x7F10 + cols, ntok, cols, False)
+    want = xf.astype(np.float64) @ W.T
+    assert sm.prefill_fold() is True
+    ys = {}
+    for fold in (False, True):
+        prev = sm.prefill_fold(fold)
+        try:
+            y = torch.full((ntok, rows), float("nan"), device=dev)
+            dc.prefill(xt, y)
+            torch.cuda.synchronize()
+            ys[fold] = y.cpu().numpy()
+        finally:
+            sm.prefill_fold(prev)
+    assert sm.prefill_fold() is True
+    e_exact, e_fold = rel_l2(ys[False], want), rel_l2(ys[True], want)
+    e_between = rel_l2(ys[True], ys[False])
+    print(f"prefill {rows}x{cols} ntok {ntok}: stages apart {e_exact:.2e}, folded {e_fold:.2e}, "
+          f"folded vs apart {e_between:.2e}")
+    assert e_exact <= TIGHT
+    assert e_fold <= BAR and e_between <= BAR
+    assert e_between > 0.0
 
 
 def test_prefill_full_size_down_split_k(sm, ref, dev):
