@@ -160,6 +160,22 @@ int sparkmv_vq_gemv_multi(const sparkmv_vq_matrix * mats, int nmat, int nstages,
                           int v3, const void * x, int x_dtype, int ldx, int ncols, int ldy,
                           int accumulate, int variant, void * stream);
 
+/* rms_norm fused into the matvecs that read it: one column, x =
+ * bf16(rms_norm(h) * norm_w) (model.rs:236-245: the sum of squares in f64,
+ * 1 / sqrt(mean + eps) rounded once to f32, (h * inv) * w in f32, then
+ * bf16 as the bf16 activations are stored), staged by every workgroup from
+ * the f32 residual h, then y_m (+)= W_m x for the nmat <= 4 matrices. It
+ * replaces the forward's norm launch followed by its matvec launch
+ * (vq-model-gpu.cu:789-792, :808-813). x_out, when non-null, receives those
+ * bf16 values. No counterpart in the reference ABI. Only shapes the
+ * one-column block kernel stages whole (DQV3 dim 4, an even codebook, 1 or
+ * 2 stages, columns a multiple of 128 up to 8 per thread of the launch,
+ * 16-byte aligned h and norm_w); any other call is refused with a message
+ * and launches nothing. */
+int sparkmv_vq_gemv_norm(const sparkmv_vq_matrix * mats, int nmat, int nstages, int dim, int nc, int cols, int v3,
+                         const float * h, const float * norm_w, float eps, uint16_t * x_out, int accumulate,
+                         void * stream);
+
 /* Bit-exact decode of every stage into out (rows x cols f32, row-major):
  * out (+)= sum_s cb_s[idx] * g_s, stage 0 first (lib.rs:197-211, :309-315). */
 int sparkmv_vq_dequant(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,

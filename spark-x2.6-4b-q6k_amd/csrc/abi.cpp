@@ -425,6 +425,39 @@ int sparkmv_vq_gemv_multi(const sparkmv_vq_matrix * mats, int nmat, int nstages,
     return vq_launch(c);
 }
 
+int sparkmv_vq_gemv_norm(const sparkmv_vq_matrix * mats, int nmat, int nstages, int dim, int nc, int cols, int v3,
+                         const float * h, const float * norm_w, float eps, uint16_t * x_out, int accumulate,
+                         void * stream) {
+    if (!mats || nmat < 1 || nmat > 4) { set_error("matrix count %d is outside 1..4", nmat); return -1; }
+    if (nstages < 1 || nstages > 2) { set_error("the fused norm takes 1 or 2 stages, not %d", nstages); return -1; }
+    if (!h || !norm_w) { set_error("h or the norm weight is null"); return -1; }
+    if (!(eps > 0.0f)) { set_error("eps must be positive"); return -1; }
+    VqMatDesc m[4];
+    memset(m, 0, sizeof m);
+    for (int i = 0; i < nmat; i++) {
+        for (int s = 0; s < nstages; s++) m[i].stages[s] = mats[i].stages[s];
+        m[i].y = mats[i].y;
+        m[i].rows = mats[i].rows;
+        if (!geometry_ok(dim, nc, mats[i].rows, cols)) return -1;
+    }
+    VqCall c;
+    memset(&c, 0, sizeof c);
+    c.dim = dim; c.nc = nc; c.cols = cols; c.v3 = v3; c.nst = nstages;
+    c.mats = m; c.nmat = nmat;
+    c.x = h; c.ldx = cols; c.xf32 = 1; c.ncol = 1; c.ldy = mats[0].rows;
+    c.accumulate = accumulate ? 1 : 0;
+    c.stream = (hipStream_t) stream;
+    const int rc = vq_norm_launch(c, norm_w, eps, x_out);
+    if (rc == 1) {
+        set_error("the fused-norm kernel does not take this call (it needs DQV3 dim 4 with an even codebook, "
+                  "columns a multiple of 128 that one workgroup stages whole, 16-byte aligned h and norm weight, "
+                  "an 8-byte aligned x_out and 4-byte aligned stages): run the norm, then "
+                  "sparkmv_vq_gemv_multi");
+        return -1;
+    }
+    return rc;
+}
+
 int sparkmv_vq_gemv(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
                     const void * x, int x_dtype, int ldx, int ncols, float * y, int ldy, int accumulate, int variant,
                     void * stream) {

@@ -653,8 +653,37 @@ int gemv2(const Model & m, const void * const * st0, int rows0, float * y0, cons
     return vq_launch(c);
 }
 
+/* rms_norm(h) * w into the bf16 activations, then the two matrices over
+ * them: with bf16 activations and untuned kernels, ONE launch whose
+ * workgroups stage the norm of h themselves (vq_norm_launch); otherwise the
+ * norm launch and gemv2. */
 int rmsnorm(const Model & m, const float * x, const float * w, hipStream_t s, int ncol = 1, float * out = nullptr,
-            uint16_t * out16 = nullptr) {
+            uint16_t * out16 = nullptr);
+
+int norm_gemv2(const Model & m, const float * h, const float * w, const void * const * st0, int rows0, float * y0,
+               const void * const * st1, int rows1, float * y1, int cols, hipStream_t s) {
+    const bool b16 = m.c.x_dtype == SPARKMV_X_BF16;
+    if (b16 && m.picks.empty()) {
+        VqMatDesc d[2];
+        memset(d, 0, sizeof d);
+        for (int i = 0; i < m.c.nstages; i++) { d[0].stages[i] = st0[i]; d[1].stages[i] = st1[i]; }
+        d[0].y = y0; d[0].rows = rows0;
+        d[1].y = y1; d[1].rows = rows1;
+        VqCall c;
+        memset(&c, 0, sizeof c);
+        c.dim = m.c.dim; c.nc = m.c.nc; c.cols = cols; c.v3 = m.c.v3; c.nst = m.c.nstages;
+        c.mats = d; c.nmat = 2;
+        c.x = h; c.ldx = cols; c.xf32 = 1; c.ncol = 1; c.ldy = rows0;
+        c.accumulate = 0; c.stream = s;
+        const int rc = vq_norm_launch(c, w, m.c.eps, nullptr);
+        if (rc <= 0) return rc;
+    }
+    if (rmsnorm(m, h, w, s, 1, nullptr, nullptr)) return -1;
+    return gemv2(m, st0, rows0, y0, st1, rows1, y1, cols, b16 ? (const void *) m.xn16 : (const void *) m.xn, s);
+}
+
+int rmsnorm(const Model & m, const float * x, const float * w, hipStream_t s, int ncol, float * out,
+            uint16_t * out16) {
     const bool b16 = m.c.x_dtype == SPARKMV_X_BF16;
     const int per = (m.c.hidden + 255) / 256;
     float * o = out ? out : m.xn;
@@ -836,9 +865,8 @@ int chain(Model * m, float * logits, hipStream_t s) {
         float * kc = m->kv + (size_t) li * 2 * c.max_ctx * kvd;
         float * vc = kc + (size_t) c.max_ctx * kvd;
 
-        if (rmsnorm(*m, m->h, L.in_norm, s)) return -1;
-        const void * xin = b16 ? (const void *) m->xn16 : (const void *) m->xn;
-        if (gemv2(*m, L.qkv, qd + 2 * kvd, m->qkv, L.attn_gate, c.heads, m->g, c.hidden, xin, s)) return -1;
+        if (norm_gemv2(*m, m->h, L.in_norm, L.qkv, qd + 2 * kvd, m->qkv, L.attn_gate, c.heads, m->g, c.hidden, s))
+            return -1;
 
         /* rope, the KV store and attention (model.rs:484-557), launched for
          * the longest window this layer can see */
@@ -866,8 +894,8 @@ int chain(Model * m, float * logits, hipStream_t s) {
             return -1;
 
         /* MLP (model.rs:566-581) */
-        if (rmsnorm(*m, m->h, L.post_norm, s)) return -1;
-        if (gemv2(*m, L.gate, c.intermediate, m->mg, L.up, c.intermediate, m->mu, c.hidden, xin, s)) return -1;
+        if (norm_gemv2(*m, m->h, L.post_norm, L.gate, c.intermediate, m->mg, L.up, c.intermediate, m->mu, c.hidden, s))
+            return -1;
         hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((c.intermediate + 255) / 256), dim3(256), 0, s, m->mg, m->mu,
                            m->act, b16 ? m->act16 : nullptr, c.intermediate);
         if (check_launch("gelu launch")) return -1;

@@ -42,6 +42,13 @@ int profile_gemv_pick(const void * profile, int dim, int nc, int rows, int cols,
 int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant);
 /* Validate and launch; returns 0, or -1 with the message set. */
 int vq_launch(const VqCall & c);
+/* The same launch with x = bf16(rms_norm(h) * norm_w) staged by the kernel
+ * itself from the f32 residual h = c.x (c.xf32 is ignored; x_out, when
+ * non-null, receives those bf16 values). Only for calls the one-column
+ * straight-line kernel takes: returns 1 without launching otherwise (the
+ * caller then runs the norm and vq_launch), 0 after the launch, -1 on a
+ * launch error. */
+int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t * x_out);
 
 /* Decode one stage into out (row-major rows x cols f32); accumulate 0 writes
  * the stage's values as if adding into zeros. */

@@ -80,6 +80,13 @@ struct FastArgs {
     int threads;         /* the launch width, so the kernel does not wait for the hidden argument */
     int kofs;            /* first macro step of this launch in every row (a K-split launch) */
     FastMat mat[4];      /* a launch of more matrices is split into launches of 4 */
+    /* XN kernels: x is the f32 residual h; the staged x is
+     * bf16(rms_norm(h) * nw) with eps, and workgroup 0 also writes those
+     * bf16 values to xout when it is non-null (after mat, so that the other
+     * kernels' arguments keep their offsets) */
+    const float * nw;
+    float eps;
+    uint16_t * xout;
 };
 
 constexpr int kFastMats = 4;
@@ -88,7 +95,14 @@ constexpr int kFastXg = 1;
 
 constexpr int kRedStride = 16 * 17;   /* floats per wave of the LDS reduction area */
 
-template <int NST, int XF32, int EXT, int MSC, int MC>
+/* f32 -> bf16 bits, round to nearest even (a NaN stays a NaN) */
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <int NST, int XF32, int EXT, int MSC, int MC, int XN = 0>
 __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const FastArgs A) {
     /* MSC > 0: a unit is exactly MSC macro steps, known at compile time, so
      * the whole unit runs as straight-line code and each step waits only for
@@ -96,7 +110,12 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * wave's loads at its head). MSC == 0: any unit length, a ring of D steps.
      * MC: the kernel for several activation columns, with x staged in LDS
      * (1) or, XG (2), read from global memory (the L2) with each step's index
-     * words, so no x is staged and any column count fits LDS. */
+     * words, so no x is staged and any column count fits LDS.
+     * XN (one column, straight-line units): x is the f32 residual h and the
+     * workgroup stages bf16(rms_norm(h) * nw) (model.rs:236-245: sum of
+     * squares in f64, 1 / sqrt rounded once to f32, (h * inv) * w in f32),
+     * so the norm needs no launch of its own. */
+    static_assert(!XN || (MC == 0 && MSC > 0 && !XF32), "the fused norm stages one bf16 column");
     constexpr int XG = MC == 2 ? 1 : 0;
     constexpr int D = MSC > 0 ? MSC : 8;
     /* straight-line units keep at most kLook macro steps of index words in
@@ -244,6 +263,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * 10 loads per thread cover from seven waves up */
     constexpr int K = 10;
     const int bd = A.threads, tid = threadIdx.x;
+    float xinv = 0.0f;        /* XN: 1 / rms of h */
     uint32_t xm = 0;          /* the largest |x| this thread staged, as f32 bits */
     xr_u16x2 xm2 = {0, 0};    /* the same for bf16 x, by pairs */
     if constexpr (MC) {
@@ -302,6 +322,81 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         point(first);
         ld_gains(first);
         ld_head();
+    } else if constexpr (XN) {
+        /* One column staged from the f32 residual h: bf16(rms_norm(h) * nw).
+         * h and nw are requested first (as many 16-byte chunks per thread
+         * as the columns need), then the codebooks; the norm (squares in
+         * f64, a butterfly per wave, the waves' sums from LDS in wave order)
+         * and the staging of x run while the codebooks are in flight. */
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));   /* codebooks are 4-byte aligned */
+        constexpr int KXN = 2;                     /* 16-byte chunks of h and nw (4 columns) per thread, at most */
+        constexpr int KS = 5;                      /* 16-byte codebook chunks per thread and stage */
+        const int xq4 = A.cols >> 2;
+        f4 hv[KXN], wv[KXN];
+#pragma unroll
+        for (int k = 0; k < KXN; k++) {
+            hv[k] = f4{0.f, 0.f, 0.f, 0.f};
+            wv[k] = f4{0.f, 0.f, 0.f, 0.f};
+            if (k * bd < xq4) {   /* uniform: chunks past the columns are not requested */
+                const int i = min(k * bd + tid, xq4 - 1);
+                hv[k] = ((const f4 *) A.x)[i];
+                wv[k] = ((const f4 *) A.nw)[i];
+            }
+        }
+        u4v cv[NST][KS];
+#pragma unroll
+        for (int s = 0; s < NST; s++)
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+                cv[s][k] = ((const u4a *) (stp[s] + 24))[min(k * bd + tid, n16 - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        point(first);
+        ld_gains(first);
+        ld_head();
+        __builtin_amdgcn_sched_barrier(0);
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < KXN; k++)
+            if (k * bd + tid < xq4)
+#pragma unroll
+                for (int j = 0; j < 4; j++) ss += (double) hv[k][j] * (double) hv[k][j];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        double * part = (double *) red;
+        if (lane == 0) part[wave] = ss;
+        __syncthreads();
+        double tot = 0.0;
+        for (int i = 0; i < (bd >> 6); i++) tot += part[i];
+        xinv = (float) (1.0 / sqrt(tot / (double) A.cols + (double) A.eps));
+#pragma unroll
+        for (int k = 0; k < KXN; k++) {
+            if (k * bd >= xq4) continue;
+            /* four columns: bf16 of (h * inv) * w, staged as f16 (exact) */
+            const int e = 4 * min(k * bd + tid, xq4 - 1);
+            uint32_t b[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) b[j] = bf16_rne((hv[k][j] * xinv) * wv[k][j]);
+            const uint32_t p0 = b[0] | (b[1] << 16), p1 = b[2] | (b[3] << 16);
+            xr_acc_bf16x2(xm2, p0);
+            xr_acc_bf16x2(xm2, p1);
+            h4 v4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v4[j] = (_Float16) __uint_as_float(b[j] << 16);
+            *(h4 *) (lx + 264 * (e >> 7) + 2 * (e & 127)) = v4;
+            if (A.xout && blockIdx.x == 0) {
+                typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+                *(u2v *) (A.xout + e) = u2v{p0, p1};
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < NST; s++)
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+                ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
     } else if constexpr (MSC > 0) {
         /* One 16-byte aligned activation column of at most 16 * blockDim
          * columns and an even codebook of at most KS chunks per thread and
@@ -406,6 +501,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
             auto xval = [&](int e) {
                 const int n = e / A.cols, kk = e - n * A.cols;
                 const size_t xi = (size_t) n * A.ldx + kk;
+                if (XN) return __uint_as_float(bf16_rne((((const float *) A.x)[kk] * xinv) * A.nw[kk]) << 16);
                 return XF32 ? ((const float *) A.x)[xi] : bf16_to_f32(((const uint16_t *) A.x)[xi]);
             };
             uint32_t fm = 0;   /* the largest finite |x| of this thread's elements */
@@ -767,16 +863,16 @@ int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant) {
 
 static int aligned4(const void * p) { return ((uintptr_t) p & 3u) == 0; }
 
-template <int NST, int XF32, int EXT, int MSC, int MC = 0>
+template <int NST, int XF32, int EXT, int MSC, int MC = 0, int XN = 0>
 static int launch_fast_t(const FastArgs & A, int grid, int threads, size_t lds, hipStream_t s) {
     static size_t opted = 0;
-    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, MSC, MC>;
+    const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, MSC, MC, XN>;
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the VQ block kernel", e);
         opted = lds;
     }
-    launch_kernel(vq_mfma_kernel<NST, XF32, EXT, MSC, MC>, dim3(grid), dim3(threads), (uint32_t) lds, s, A);
+    launch_kernel(vq_mfma_kernel<NST, XF32, EXT, MSC, MC, XN>, dim3(grid), dim3(threads), (uint32_t) lds, s, A);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip("VQ block kernel launch", e);
     return 0;
@@ -918,6 +1014,23 @@ static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
  * run the straight-line kernel for bf16 x; any other length, and f32 x, the
  * ring kernel. Thirteen-bit indices hold plane bytes too, so their
  * straight-line units stop at 8 steps (10 would spill). */
+/* The one-column straight-line kernels that stage rms_norm(h) themselves. */
+template <int NST, int EXT, int XN>
+static int launch_ms_norm(const FastArgs & A, int MS, int grid, int threads, size_t lds, hipStream_t s) {
+    switch (MS) {
+        case 1: return launch_fast_t<NST, 0, EXT, 1, 0, XN>(A, grid, threads, lds, s);
+        case 2: return launch_fast_t<NST, 0, EXT, 2, 0, XN>(A, grid, threads, lds, s);
+        case 4: return launch_fast_t<NST, 0, EXT, 4, 0, XN>(A, grid, threads, lds, s);
+        case 5: return launch_fast_t<NST, 0, EXT, 5, 0, XN>(A, grid, threads, lds, s);
+        case 8: return launch_fast_t<NST, 0, EXT, 8, 0, XN>(A, grid, threads, lds, s);
+        case 10:
+            if constexpr (!EXT) return launch_fast_t<NST, 0, EXT, 10, 0, XN>(A, grid, threads, lds, s);
+            break;
+        default: break;
+    }
+    return 1;
+}
+
 template <int NST, int XF32, int EXT>
 static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, size_t lds, hipStream_t s) {
     if constexpr (!XF32) {
@@ -965,7 +1078,17 @@ static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, 
 
 /* One launch of the block kernel over macro steps [k0, k0 + mk) of every row
  * (the whole row unless x has to be split to fit LDS). */
-static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, int k0, int mk) {
+struct FastNorm {
+    const float * w;
+    float eps;
+    uint16_t * xout;
+};
+
+/* nrm: stage bf16(rms_norm(x) * w) from the f32 residual x (one column, the
+ * whole row in one launch, a one-column straight-line shape); returns 1
+ * without launching when the call's shape has no such kernel. */
+static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, int k0, int mk,
+                            const FastNorm * nrm = nullptr) {
     const Layout L0 = make_layout(c.dim, c.nc, c.mats[0].rows, c.cols, 1);
     const int ext = L0.nbit > 12;
     VqCall part = c;
@@ -978,7 +1101,12 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     }
     FastArgs A;
     memset(&A, 0, sizeof A);
-    A.x = (const uint8_t *) c.x + (size_t) 128 * k0 * (c.xf32 ? 4 : 2);
+    A.x = (const uint8_t *) c.x + (size_t) 128 * k0 * (c.xf32 || nrm ? 4 : 2);
+    if (nrm) {
+        A.nw = nrm->w;
+        A.eps = nrm->eps;
+        A.xout = nrm->xout;
+    }
     A.nmat = c.nmat;
     A.cols = part.cols;
     A.nc = c.nc;
@@ -1022,6 +1150,16 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
      * several-column call runs the generic kernel, which the shape search
      * kept within 10 waves */
     const int mc = sh.xg ? 2 : c.ncol > 1 && straight;
+    if (nrm) {
+        /* the staging holds 2 chunks of 4 columns per thread */
+        if (c.ncol != 1 || c.xf32 || !straight || mc || k0 != 0 || mk * 128 != c.cols || ((uintptr_t) nrm->w & 15u) ||
+            ((uintptr_t) nrm->xout & 7u) || c.cols > 8 * threads)
+            return 1;
+        if (nst == 2) return ext ? launch_ms_norm<2, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
+                                 : launch_ms_norm<2, 0, 1>(A, MS, wg, threads, sh.lds, c.stream);
+        return ext ? launch_ms_norm<1, 1, 1>(A, MS, wg, threads, sh.lds, c.stream)
+                   : launch_ms_norm<1, 0, 1>(A, MS, wg, threads, sh.lds, c.stream);
+    }
     if (nst == 2) {
         if (c.xf32) return ext ? launch_ms<2, 1, 1>(A, MS, mc, wg, threads, sh.lds, c.stream)
                                : launch_ms<2, 1, 0>(A, MS, mc, wg, threads, sh.lds, c.stream);
@@ -1098,6 +1236,26 @@ static int launch_wave(const VqCall & c, int variant) {
         }
     }
     return 0;
+}
+
+int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t * x_out) {
+    /* the fused kernel's conditions: one f32 column, every matrix on the
+     * block kernel, at most two stages and four matrices, one K range */
+    if (!norm_w || c.ncol != 1 || !c.x || ((uintptr_t) c.x & 15u) || c.nst < 1 || c.nst > 2 || c.nmat < 1 ||
+        c.nmat > kFastMats || c.variant || c.threads || c.grid || c.dim != 4 || c.cols % 128)
+        return 1;
+    for (int m = 0; m < c.nmat; m++) {
+        if (!c.mats[m].y || c.mats[m].rows <= 0) return 1;
+        for (int s = 0; s < c.nst; s++)
+            if (!c.mats[m].stages[s] || !aligned4(c.mats[m].stages[s])) return 1;
+        if (!fast_geometry_ok(c.dim, c.nc, c.mats[m].rows, c.cols, c.v3)) return 1;
+    }
+    if (c.v3 && bits_for(c.nc) > 13) return 1;
+    VqCall b = c;
+    b.xf32 = 0;   /* what is staged: one bf16 column */
+    if (fast_splits(b, c.nst) != 1) return 1;
+    const FastNorm nrm{norm_w, eps, x_out};
+    return launch_fast_part(b, 0, c.nst, c.accumulate, 0, c.cols / 128, &nrm);
 }
 
 int vq_launch(const VqCall & c) {

@@ -116,6 +116,8 @@ SIGNATURES = {
     "sparkmv_vq_gemv_ready": (_I, [_I] * 6),
     "sparkmv_vq_gemv": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P, _I, _I, _I, _P]),
     "sparkmv_vq_gemv_multi": (_I, [ctypes.POINTER(VqMatrix), _I, _I, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "sparkmv_vq_gemv_norm": (_I, [ctypes.POINTER(VqMatrix), _I, _I, _I, _I, _I, _I, _P, _P, ctypes.c_float, _P, _I,
+                                  _P]),
     "sparkmv_vq_dequant": (_I, [_PP, _I, _I, _I, _I, _I, _I, _P, _I, _P]),
     "sparkmv_q6k_gemv": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
     "sparkmv_q8_0_gemv": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _I, _I, _P]),
@@ -481,6 +483,22 @@ class DeviceContainer:
         check(lib().sparkmv_vq_prefill(pp, h.nstages, h.dim, h.nc, h.rows, h.cols, h.v3, x.data_ptr(), xd,
                                        x.stride(0), x.shape[0], y.data_ptr(), y.stride(0), int(accumulate),
                                        _stream_ptr(stream)), "vq prefill")
+
+
+def gemv_norm(mats, h, norm_w, ys, eps=1e-6, x_out=None, accumulate=False, stream=None):
+    """One launch over up to 4 DeviceContainers of x = bf16(rms_norm(h) *
+    norm_w), staged by the kernel from the f32 residual h (device f32
+    [cols]); x_out (device int16 [cols]), when given, receives x."""
+    arr = (VqMatrix * len(mats))()
+    for i, (m, y) in enumerate(zip(mats, ys)):
+        for s, p in enumerate(m.stage_ptrs):
+            arr[i].stages[s] = p
+        arr[i].y = y.data_ptr()
+        arr[i].rows = m.rows
+    h0 = mats[0].host
+    check(lib().sparkmv_vq_gemv_norm(arr, len(mats), h0.nstages, h0.dim, h0.nc, h0.cols, h0.v3, h.data_ptr(),
+                                     norm_w.data_ptr(), float(eps), x_out.data_ptr() if x_out is not None else None,
+                                     int(accumulate), _stream_ptr(stream)), "vq gemv norm")
 
 
 def gemv_multi(mats, x, ys, ncols=1, accumulate=False, variant=0, stream=None):
