@@ -451,6 +451,31 @@ int sparkmv_model_matvec_kernel(void * model, int rows, int cols, int * variant,
 /* The device rows of layer's K and V cache ([max_ctx][kv_dim] f32 each). */
 int sparkmv_model_kv(void * model, int layer, float ** k, float ** v);
 
+/* A checkpoint's config.json (tools/vq-runtime/src/config.rs:39-85,
+ * Config::load): hidden_size, num_hidden_layers, num_attention_heads,
+ * num_key_value_heads, head_dim, intermediate_size, vocab_size,
+ * rms_norm_eps and sliding_window are required ("config.json has no numeric
+ * <key>"), and so is layer_types ("config.json has no layer_types"); a
+ * layer is full when its entry is "full_attention", when the entry is not a
+ * string, or when the list is shorter than the layers; rope_parameters
+ * gives rope_theta and partial_rotary_factor per layer type, falling back
+ * to 5e6 / 0.25 (full) and 1e4 / 1.0 (sliding), both kept in f32. Fills the
+ * model fields of cfg (the VQ geometry, max_ctx and x_dtype are left 0) and
+ * full[i] for i < max_layers. */
+int sparkmv_config_load(const char * path, sparkmv_model_cfg * cfg, int * full, int max_layers);
+/* A whole model from config.json and a VQ artifact directory (model.rs:
+ * 121-185 Weights::load over VqDir; vq-model-gpu.cu:230-357, :739-775
+ * load_model): model.embedding.weight (the tied head), model.norm.weight,
+ * and per layer input_layernorm / post_attention_layernorm and the
+ * q_k_v_proj, g_proj, out_proj, gate_proj, up_proj, down_proj matrices,
+ * each checked against the architecture ("<name>: is RxC, the architecture
+ * needs R'xC'"); every matrix must share one VQ geometry. The weights are
+ * uploaded to device memory that the model owns and frees at
+ * sparkmv_model_destroy. With apply_profile, DIR/vq-tune.profile (when
+ * present) is applied if it is trusted for this artifact and device. NULL
+ * on refusal, with the message set. */
+void * sparkmv_model_load(const char * dir, const char * config_path, int max_ctx, int x_dtype, int apply_profile);
+
 /* ---- the per-artifact tuning profile (VQPROF 1) ----
  * tools/vq/gpu/vq-profile.h:10-30 (format, FNV-1a fingerprint, trust rules),
  * written by tools/vq-tune/src/artifact.rs:148-171. Host only. */

@@ -19,7 +19,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib", "libsparkmv.so")
 
 HIP_SOURCES = ["vq_kernels.hip", "kq_kernels.hip", "prefill.hip", "forward.hip", "chain.hip"]
-CXX_SOURCES = ["abi.cpp", "plan.cpp", "host/vq_format.cpp", "host/synth.cpp", "host/artifacts.cpp", "host/profile.cpp"]
+CXX_SOURCES = ["abi.cpp", "plan.cpp", "host/vq_format.cpp", "host/synth.cpp", "host/artifacts.cpp", "host/profile.cpp",
+               "host/model_load.cpp"]
 
 ARCH = "gfx950"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function"]

@@ -33,6 +33,7 @@
  * attention launch reserves LDS for its longest window.
  */
 #include "kq.h"
+#include "model.h"
 #include "prefill.h"
 #include "vq.h"
 
@@ -232,9 +233,13 @@ __global__ __launch_bounds__(256) void fw_attn_part_kernel(const float * qkv, in
     fv o = (fv) 0.0f;
 #pragma unroll
     for (int j = 0; j < C; j++) {
-        const float e = j < jn ? expf(sc[j] - m) : 0.0f;
-        l += e;
-        o += e * vr[j];
+        /* rows past jn are padding that may hold anything (the row at pos
+         * before its store): skipped, not weighted by zero */
+        if (j < jn) {
+            const float e = expf(sc[j] - m);
+            l += e;
+            o += e * vr[j];
+        }
     }
     float * P = part + ((size_t) h * nch_max + chunk) * (hd + 2);
     *(fv *) (P + lane * VPL) = o;
@@ -400,9 +405,13 @@ __global__ __launch_bounds__(256) void fw_attn_part_n_kernel(const float * qkv, 
     fv o = (fv) 0.0f;
 #pragma unroll
     for (int j = 0; j < C; j++) {
-        const float e = j < jn ? expf(sc[j] - m) : 0.0f;
-        l += e;
-        o += e * vr[j];
+        /* rows past jn are padding that may hold anything (the row at pos
+         * before its store): skipped, not weighted by zero */
+        if (j < jn) {
+            const float e = expf(sc[j] - m);
+            l += e;
+            o += e * vr[j];
+        }
     }
     float * P = part + (((size_t) t * heads + h) * nch_max + chunk) * (hd + 2);
     *(fv *) (P + lane * VPL) = o;
@@ -546,9 +555,13 @@ __global__ __launch_bounds__(256) void fw_attn_prompt_kernel(const float * qkv, 
         o *= a;
 #pragma unroll
         for (int j = 0; j < C; j++) {
-            const float e = j < jn ? expf(sc[j] - mn) : 0.0f;
-            l += e;
-            o += e * vr[j];
+            /* rows past jn are padding that may hold anything (the row at pos
+             * before its store): skipped, not weighted by zero */
+            if (j < jn) {
+                const float e = expf(sc[j] - mn);
+                l += e;
+                o += e * vr[j];
+            }
         }
         m = mn;
     }
@@ -589,6 +602,8 @@ struct Model {
     int len = 0;
     /* tuned kernels per (rows, cols) of a VQ matvec: variant, threads */
     std::map<std::pair<int, int>, std::pair<int, int>> picks;
+    /* device memory the model frees at destroy: weights a loader uploaded */
+    std::vector<void *> owned;
     /* block buffers (verify blocks and prompt chunks), one allocation at
      * sparkmv_model_reserve or the first block: vcap columns of each
      * activation, gate rows at the qkv stride, the tokens, and attention
@@ -774,6 +789,7 @@ void sparkmv_model_destroy(void * model) {
     if (m->graph) (void) hipGraphDestroy(m->graph);
     if (m->mem) (void) hipFree(m->mem);
     if (m->vmem) (void) hipFree(m->vmem);
+    for (void * p : m->owned) (void) hipFree(p);
     delete m;
 }
 
@@ -815,6 +831,13 @@ int sparkmv_model_set_head(void * model, int kind, const void * const * stages, 
 }
 
 }  // extern "C"
+
+int sparkmv::model_adopt(void * model, void * dev_ptr) {
+    Model * m = (Model *) model;
+    if (!m || !dev_ptr) { set_error("model or pointer is null"); return -1; }
+    m->owned.push_back(dev_ptr);
+    return 0;
+}
 
 namespace {
 

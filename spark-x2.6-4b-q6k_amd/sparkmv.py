@@ -179,6 +179,8 @@ SIGNATURES = {
     "sparkmv_model_rollback": (_I, [_P, _I]),
     "sparkmv_model_len": (_I, [_P]),
     "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
+    "sparkmv_config_load": (_I, [ctypes.c_char_p, ctypes.POINTER(ModelCfg), ctypes.POINTER(_I), _I]),
+    "sparkmv_model_load": (_P, [ctypes.c_char_p, ctypes.c_char_p, _I, _I, _I]),
     "sparkmv_model_apply_profile": (_I, [_P, _P, _U64, ctypes.c_char_p]),
     "sparkmv_model_matvec_kernel": (_I, [_P, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "sparkmv_profile_fingerprint": (_I, [ctypes.c_char_p, ctypes.POINTER(_U64)]),
@@ -558,6 +560,20 @@ def kquant_dequant(kind, blocks, rows, cols, out, stream=None):
     check(fn(blocks.data_ptr(), rows, cols, out.data_ptr(), _stream_ptr(stream)), kind + " dequant")
 
 
+_CFG_FIELDS = ("hidden", "layers", "heads", "kv_heads", "head_dim", "intermediate", "vocab", "eps", "sliding_window",
+               "rope_full_theta", "rope_full_partial", "rope_slide_theta", "rope_slide_partial")
+
+
+def config_load(path, max_layers=4096):
+    """config.json (tools/vq-runtime/src/config.rs:39-85): a dict of the
+    model fields and the per-layer full-attention flags."""
+    c = ModelCfg()
+    full = (_I * max_layers)()
+    check(lib().sparkmv_config_load(os.fsencode(str(path)), ctypes.byref(c), full, max_layers), "config load")
+    cfg = {k: getattr(c, k) for k in _CFG_FIELDS}
+    return cfg, [bool(full[i]) for i in range(min(c.layers, max_layers))]
+
+
 class Model:
     """The decode forward on the GPU (sparkmv_model_*): one token through
     every layer, tools/vq-runtime/src/model.rs:441-591 (Model::forward).
@@ -591,6 +607,21 @@ class Model:
                   "model head")
         else:
             check(lib().sparkmv_model_set_head(self.h, 8, None, head.data_ptr(), final_norm.data_ptr()), "model head")
+
+    @classmethod
+    def load(cls, directory, config_path, max_ctx, x_dtype=X_BF16, apply_profile=True):
+        """The whole model from a VQ artifact directory and config.json
+        (sparkmv_model_load: model.rs:121-185 over VqDir); the model owns
+        the weights it uploaded."""
+        self = cls.__new__(cls)
+        self.h = lib().sparkmv_model_load(os.fsencode(str(directory)), os.fsencode(str(config_path)), int(max_ctx),
+                                          int(x_dtype), int(bool(apply_profile)))
+        if not self.h:
+            raise SparkmvError("model load: " + last_error())
+        cfg, _ = config_load(config_path)
+        self.cfg = dict(cfg, max_ctx=int(max_ctx), x_dtype=int(x_dtype))
+        self.keep = []
+        return self
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -165,3 +165,55 @@ def test_forward_batch_refusals(sm, ref, dev):
         with pytest.raises(sm.SparkmvError):
             model.reserve(bad)
     assert len(model) == 0
+
+
+def poison_kv(model, dev):
+    """Every K and V byte 0xFF (a NaN in f32): what a cache that reuses freed
+    memory may hold before its rows are written."""
+    import ctypes
+    import torch
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = LONG["max_ctx"] * LONG["kv_heads"] * LONG["head_dim"] * 4
+    for li in range(LONG["layers"]):
+        for ptr in model.kv(li):
+            assert hip.hipMemset(ctypes.c_void_p(ptr), ctypes.c_int(0xFF), ctypes.c_size_t(n)) == 0
+    assert hip.hipDeviceSynchronize() == 0
+    torch.cuda.synchronize(dev)
+
+
+@pytest.mark.parametrize("path", ["decode", "verify", "chunks"])
+def test_unwritten_cache_rows_are_not_read(sm, ref, dev, path):
+    """The attention reads whole 16-row chunks of the cache and skips the
+    rows past the position: with NaN in every row not yet written, each
+    path still meets its bar (decode and verify 1e-5, a 12-token chunk
+    1e-5, a 100-token chunk 5e-3)."""
+    import torch
+    model, oracle = build(sm, ref, dev, "q8_0", sm.X_F32, LONG)
+    poison_kv(model, dev)
+    toks = tokens(120, seed=17)
+    V = LONG["vocab"]
+    if path == "decode":
+        logits = torch.full((V,), float("nan"), device=dev)
+        for pos in range(18):
+            model.forward(toks[pos], pos, logits)
+            torch.cuda.synchronize()
+            err = rel_l2(logits.cpu().numpy(), oracle.forward(toks[pos], pos))
+            assert err <= 1e-5, pos
+    elif path == "verify":
+        out = torch.full((8, V), float("nan"), device=dev)
+        model.verify(toks[:8], 0, out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        for i in range(8):
+            assert rel_l2(got[i], oracle.forward(toks[i], i)) <= 1e-5, i
+    else:
+        logits = torch.full((V,), float("nan"), device=dev)
+        for n0, n1, bar in ((0, 12, 1e-5), (12, 112, 5e-3)):
+            want = None
+            for p in range(n0, n1):
+                want = oracle.forward(toks[p], p)
+            model.forward_batch(toks[n0:n1], n0, logits)
+            torch.cuda.synchronize()
+            err = rel_l2(logits.cpu().numpy(), want)
+            print(f"chunk {n0}..{n1 - 1} over a NaN cache: relL2 {err:.2e}")
+            assert err <= bar
