@@ -471,9 +471,13 @@ int sparkmv_config_load(const char * path, sparkmv_model_cfg * cfg, int * full, 
  * each checked against the architecture ("<name>: is RxC, the architecture
  * needs R'xC'"); every matrix must share one VQ geometry. The weights are
  * uploaded to device memory that the model owns and frees at
- * sparkmv_model_destroy. With apply_profile, DIR/vq-tune.profile (when
- * present) is applied if it is trusted for this artifact and device. NULL
- * on refusal, with the message set. */
+ * sparkmv_model_destroy. With apply_profile, DIR/vq-tune.profile is
+ * applied when it is trusted for this artifact and device; like the
+ * reference's runtime (vq-model-gpu.cu:1097-1120), a profile that is absent,
+ * unreadable, not version 1 or for another artifact or device never fails
+ * the load: the heuristic stays, and after a successful load the message
+ * channel (vqg_decode_error) says which case applied. NULL on refusal, with
+ * the message set. */
 void * sparkmv_model_load(const char * dir, const char * config_path, int max_ctx, int x_dtype, int apply_profile);
 
 /* ---- the per-artifact tuning profile (VQPROF 1) ----

@@ -27,6 +27,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <new>
 #include <string>
 #include <utility>
 #include <vector>
@@ -222,6 +223,8 @@ static bool read_text(const char * path, std::string & out, std::string & err) {
     return true;
 }
 
+constexpr int kMaxConfigLayers = 65536;
+
 /* config.rs:39-85 */
 static bool config_load(const char * path, sparkmv_model_cfg & cfg, std::vector<int> & full, std::string & err) {
     std::string text;
@@ -247,6 +250,14 @@ static bool config_load(const char * path, sparkmv_model_cfg & cfg, std::vector<
     if (!lt || lt->type != Json::Arr) { err = "config.json has no layer_types"; return false; }
     for (double v : {hidden, layers, heads, kvh, hd, inter, vocab, window})
         if (!(v >= 1.0 && v <= 2147483647.0)) { err = "config.json has a size outside 1..2^31-1"; return false; }
+    /* the per-layer flags are held in memory: a layer count past any model
+     * is refused here rather than allocated */
+    if (layers >= (double) (kMaxConfigLayers + 1)) {
+        char b[96];
+        snprintf(b, sizeof b, "config.json has %.0f layers, above %d", layers, kMaxConfigLayers);
+        err = b;
+        return false;
+    }
     memset(&cfg, 0, sizeof cfg);
     cfg.hidden = (int) hidden;
     cfg.layers = (int) layers;
@@ -367,7 +378,9 @@ static void * model_load(const char * dir, const char * config_path, int max_ctx
     Loader L;
     L.manifest = sparkmv_manifest_open(dir);
     if (!L.manifest) { err = vqg_decode_error(); return nullptr; }
-    const int hid = cfg.hidden, qd = cfg.heads * cfg.head_dim, kvd = cfg.kv_heads * cfg.head_dim;
+    const long long qd64 = (long long) cfg.heads * cfg.head_dim, kvd64 = (long long) cfg.kv_heads * cfg.head_dim;
+    if (qd64 + 2 * kvd64 > 2147483647LL) { err = "config.json: the attention widths overflow 32 bits"; return nullptr; }
+    const int hid = cfg.hidden, qd = (int) qd64, kvd = (int) kvd64;
 
     /* the tied embedding decides the geometry; the model is created from it */
     const void * head[4] = {};
@@ -422,22 +435,29 @@ static void * model_load(const char * dir, const char * config_path, int max_ctx
         if (model_adopt(L.model, d)) { err = vqg_decode_error(); return nullptr; }
     L.pending.clear();
 
+    /* The profile never fails a load (vq-model-gpu.cu:1097-1120): one that
+     * is absent, not version 1, for another artifact or device, or that
+     * cannot be checked leaves the heuristic, and the outcome is left in
+     * the message channel. */
+    std::string note = "profile: not requested; heuristics";
     if (apply_profile) {
         const std::string prof_path = std::string(dir) + "/vq-tune.profile";
-        FILE * f = fopen(prof_path.c_str(), "rb");
-        if (f) {
-            fclose(f);
-            void * prof = sparkmv_profile_load(prof_path.c_str());
-            if (!prof) { err = vqg_decode_error(); return nullptr; }
-            uint64_t fp = 0;
-            char gpu[256] = {};
-            rc = sparkmv_profile_fingerprint(dir, &fp);
-            if (!rc) rc = vqg_device_name(gpu, (int) sizeof gpu);
-            if (!rc) rc = sparkmv_model_apply_profile(L.model, prof, fp, gpu) < 0 ? -1 : 0;
-            sparkmv_profile_close(prof);
-            if (rc) { err = vqg_decode_error(); return nullptr; }
+        uint64_t fp = 0;
+        char gpu[256] = {};
+        void * prof = nullptr;
+        if (sparkmv_profile_fingerprint(dir, &fp)) {
+            note = std::string("profile: none; ") + dir + "/manifest.txt could not be fingerprinted";
+        } else if (!(prof = sparkmv_profile_load(prof_path.c_str()))) {
+            note = "profile: " + prof_path + " is absent or not version 1; heuristics";
+        } else if (vqg_device_name(gpu, (int) sizeof gpu)) {
+            note = "profile: device query failed; heuristics";
+        } else {
+            const int n = sparkmv_model_apply_profile(L.model, prof, fp, gpu);
+            note = n < 0 ? std::string("profile: ") + vqg_decode_error() + "; heuristics" : vqg_decode_error();
         }
+        if (prof) sparkmv_profile_close(prof);
     }
+    set_error("%s", note.c_str());
     void * m = L.model;
     L.model = nullptr;
     return m;
@@ -452,20 +472,30 @@ extern "C" {
 
 int sparkmv_config_load(const char * path, sparkmv_model_cfg * cfg, int * full, int max_layers) {
     if (!path || !cfg) { set_error("config path or output is null"); return -1; }
-    std::string err;
-    std::vector<int> f;
-    if (!load::config_load(path, *cfg, f, err)) { set_error("%s", err.c_str()); return -1; }
-    if (full)
-        for (int i = 0; i < max_layers && i < (int) f.size(); i++) full[i] = f[(size_t) i];
-    return 0;
+    try {
+        std::string err;
+        std::vector<int> f;
+        if (!load::config_load(path, *cfg, f, err)) { set_error("%s", err.c_str()); return -1; }
+        if (full)
+            for (int i = 0; i < max_layers && i < (int) f.size(); i++) full[i] = f[(size_t) i];
+        return 0;
+    } catch (const std::bad_alloc &) {
+        set_error("out of host memory reading %s", path);
+        return -1;
+    }
 }
 
 void * sparkmv_model_load(const char * dir, const char * config_path, int max_ctx, int x_dtype, int apply_profile) {
     if (!dir || !config_path) { set_error("artifact directory or config path is null"); return nullptr; }
-    std::string err;
-    void * m = load::model_load(dir, config_path, max_ctx, x_dtype, apply_profile, err);
-    if (!m) set_error("%s", err.c_str());
-    return m;
+    try {
+        std::string err;
+        void * m = load::model_load(dir, config_path, max_ctx, x_dtype, apply_profile, err);
+        if (!m) set_error("%s", err.c_str());
+        return m;
+    } catch (const std::bad_alloc &) {
+        set_error("out of host memory loading %s", dir);
+        return nullptr;
+    }
 }
 
 }  // extern "C"

@@ -612,12 +612,14 @@ class Model:
     def load(cls, directory, config_path, max_ctx, x_dtype=X_BF16, apply_profile=True):
         """The whole model from a VQ artifact directory and config.json
         (sparkmv_model_load: model.rs:121-185 over VqDir); the model owns
-        the weights it uploaded."""
+        the weights it uploaded. profile_note says what became of
+        DIR/vq-tune.profile (a bad or foreign profile keeps the heuristic)."""
         self = cls.__new__(cls)
         self.h = lib().sparkmv_model_load(os.fsencode(str(directory)), os.fsencode(str(config_path)), int(max_ctx),
                                           int(x_dtype), int(bool(apply_profile)))
         if not self.h:
             raise SparkmvError("model load: " + last_error())
+        self.profile_note = last_error()
         cfg, _ = config_load(config_path)
         self.cfg = dict(cfg, max_ctx=int(max_ctx), x_dtype=int(x_dtype))
         self.keep = []

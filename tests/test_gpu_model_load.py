@@ -141,13 +141,28 @@ def test_load_refusals(sm, ref, dev, tmp_path):
 
 
 def test_load_applies_a_trusted_profile(sm, ref, dev, tmp_path):
+    """A trusted profile is applied at load. As in the reference's runtime
+    (vq-model-gpu.cu:1097-1120), a profile that is absent, unreadable or for
+    another device never fails the load: the heuristic stays, and the note
+    says why."""
     c = CFG
     write_artifact(sm, tmp_path, c)
     hid, qd = c["hidden"], c["heads"] * c["head_dim"]
+    cfg_path = tmp_path / "config.json"
     e = sm.ProfileEntry(kind=0, dim=4, nc=4096, rows=hid, cols=qd, v3=1, variant=1, threads=256, rate=1.0)
     fp = sm.profile_fingerprint(tmp_path)
-    sm.profile_write(tmp_path / "vq-tune.profile", fp, sm.device_name(), "hip", [e])
-    m = sm.Model.load(tmp_path, tmp_path / "config.json", c["max_ctx"], sm.X_F32)
+    prof = tmp_path / "vq-tune.profile"
+    m = sm.Model.load(tmp_path, cfg_path, c["max_ctx"], sm.X_F32)
+    assert m.matvec_kernel(hid, qd) == (0, 0) and "absent" in m.profile_note
+    sm.profile_write(prof, fp, sm.device_name(), "hip", [e])
+    m = sm.Model.load(tmp_path, cfg_path, c["max_ctx"], sm.X_F32)
     assert m.matvec_kernel(hid, qd) == (1, 256)
-    m2 = sm.Model.load(tmp_path, tmp_path / "config.json", c["max_ctx"], sm.X_F32, apply_profile=False)
-    assert m2.matvec_kernel(hid, qd) == (0, 0)
+    assert "1 geometries take their tuned kernel" in m.profile_note
+    m2 = sm.Model.load(tmp_path, cfg_path, c["max_ctx"], sm.X_F32, apply_profile=False)
+    assert m2.matvec_kernel(hid, qd) == (0, 0) and "not requested" in m2.profile_note
+    sm.profile_write(prof, fp, "some other device", "hip", [e])
+    m3 = sm.Model.load(tmp_path, cfg_path, c["max_ctx"], sm.X_F32)
+    assert m3.matvec_kernel(hid, qd) == (0, 0) and "another artifact or device" in m3.profile_note
+    prof.write_text("VQPROF 7\n")
+    m4 = sm.Model.load(tmp_path, cfg_path, c["max_ctx"], sm.X_F32)
+    assert m4.matvec_kernel(hid, qd) == (0, 0) and "not version 1" in m4.profile_note

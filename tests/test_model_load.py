@@ -109,3 +109,6 @@ def test_refusals(sm, tmp_path):
         sm.config_load(tmp_path / "nope.json")
     with pytest.raises(sm.SparkmvError, match="outside"):
         sm.config_load(write(tmp_path, dict(SPARK, head_dim=0), "zero.json"))
+    # a layer count past any model is refused before its flags are allocated
+    with pytest.raises(sm.SparkmvError, match="1000000000 layers, above 65536"):
+        sm.config_load(write(tmp_path, dict(SPARK, num_hidden_layers=10 ** 9), "huge.json"))
