@@ -450,6 +450,27 @@ int sparkmv_model_apply_profile(void * model, const void * profile, uint64_t art
 int sparkmv_model_matvec_kernel(void * model, int rows, int cols, int * variant, int * threads);
 /* The device rows of layer's K and V cache ([max_ctx][kv_dim] f32 each). */
 int sparkmv_model_kv(void * model, int layer, float ** k, float ** v);
+/* Layer-input capture for a draft (model.rs:322-348 enable_capture;
+ * vq-model-gpu.cu:632-639, :704-736): from now on every forward, verify
+ * block and prompt chunk writes the residual entering each listed layer
+ * (model.rs:466-471), position-major, into the layer's slot; slot k is the
+ * k-th listed layer. At most 8 layers, each once, enabled once; the
+ * refusals carry the runtime's messages. A recorded graph is dropped
+ * (capture again to record the copies). */
+int sparkmv_model_enable_capture(void * model, const int * layers, int n);
+/* Slot k's rows (model.rs:346-348 captured): *rows = the device array
+ * [max_ctx][hidden] f32; returns how many leading rows are current (the
+ * cached positions; a rollback drops the rest as it drops KV rows), or -1. */
+int sparkmv_model_captured(void * model, int k, float ** rows);
+/* The tied embedding row of token id into out ([hidden] f32, device),
+ * asynchronous on stream (model.rs:352-354 embed_row). */
+int sparkmv_model_embed_row(void * model, uint32_t id, float * out, void * stream);
+/* The index of the largest of n device floats into *out (device int),
+ * asynchronous on stream: Model::argmax (model.rs:594-605): the first of
+ * equal maxima, NaN never chosen, 0 when no value exceeds -inf. Replaces
+ * the runtime's argmax_dev (vq-model-gpu.cu:471-488, :971-978), whose tree
+ * keeps the lowest thread's candidate on ties instead. */
+int sparkmv_argmax(const float * logits, int n, int * out, void * stream);
 
 /* A checkpoint's config.json (tools/vq-runtime/src/config.rs:39-85,
  * Config::load): hidden_size, num_hidden_layers, num_attention_heads,

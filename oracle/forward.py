@@ -87,6 +87,12 @@ class Forward:
         kvd = cfg["kv_heads"] * cfg["head_dim"]
         self.kv_k = [np.zeros((cfg["max_ctx"], kvd), F32) for _ in layers]
         self.kv_v = [np.zeros((cfg["max_ctx"], kvd), F32) for _ in layers]
+        self.capture = {}   # layer -> [max_ctx, hidden] rows of its input
+
+    def enable_capture(self, layer_ids):
+        """model.rs:322-348: every forward position then records the residual
+        entering each listed layer (model.rs:466-471)."""
+        self.capture = {li: np.zeros((self.c["max_ctx"], self.c["hidden"]), F32) for li in layer_ids}
 
     def forward(self, token, pos):
         """model.rs:441-591: the logits of token at pos."""
@@ -96,6 +102,8 @@ class Forward:
         scale = F32(1.0) / F32(math.sqrt(F32(hd)))
         h = self.embed[token].astype(F32).copy()
         for li, L in enumerate(self.layers):
+            if li in self.capture:
+                self.capture[li][pos] = h
             full = bool(L["full"])
             theta = c["rope_full_theta"] if full else c["rope_slide_theta"]
             partial = c["rope_full_partial"] if full else c["rope_slide_partial"]

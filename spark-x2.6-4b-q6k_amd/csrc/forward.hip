@@ -489,6 +489,43 @@ __global__ void fw_gelu_mul_kernel(const float * g, const float * u, float * act
     }
 }
 
+/* Layer-input capture: rows h[0 .. n) into slot rows pos .. pos + n - 1,
+ * the position read from st[1] when st is given (a replayed graph) */
+__global__ void fw_capture_kernel(const float * h, float * slot, const int * st, int pos, int n, int hidden) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+    if (i >= hidden || t >= n) return;
+    const int p = (st ? st[1] : pos) + t;
+    slot[(size_t) p * hidden + i] = h[(size_t) t * hidden + i];
+}
+
+/* The index of the largest value (Model::argmax, model.rs:594-605): the
+ * first of equal maxima, NaN never chosen, 0 when nothing beats -inf. One
+ * workgroup of 1024 threads: each scans a stride, then a tree keeps the
+ * larger value or, on a tie, the lower index. */
+__global__ __launch_bounds__(1024) void fw_argmax_kernel(const float * v, int n, int * out) {
+    __shared__ float bv[1024];
+    __shared__ int bi[1024];
+    const int t = threadIdx.x;
+    float best = -INFINITY;
+    int b = -1;
+    for (int i = t; i < n; i += 1024) {
+        const float x = v[i];
+        if (x > best) { best = x; b = i; }
+    }
+    bv[t] = best;
+    bi[t] = b;
+    __syncthreads();
+    for (int off = 512; off > 0; off >>= 1) {
+        if (t < off) {
+            const float o = bv[t + off];
+            const int oi = bi[t + off];
+            if (oi >= 0 && (bi[t] < 0 || o > bv[t] || (o == bv[t] && oi < bi[t]))) { bv[t] = o; bi[t] = oi; }
+        }
+        __syncthreads();
+    }
+    if (t == 0) out[0] = bi[0] < 0 ? 0 : bi[0];
+}
+
 /* ---- a prompt chunk: up to kPromptMax consecutive tokens at pos0 .. ----
  * (vq-model-gpu.cu:858-943 forward_batch). The steps are the verify
  * block's; the tokens come from device memory, and attention runs without
@@ -613,6 +650,11 @@ struct Model {
     float * vh, * vxn, * vqkv, * vg, * vattn, * vmg, * vmu, * vact, * vpart;
     uint16_t * vxn16, * vattn16, * vact16;
     int * vtok;
+    /* layer-input capture (model.rs:322-348, vq-model-gpu.cu:632-639):
+     * cap_slot[li] is layer li's slot or -1; cap is [cap_n][max_ctx][hidden] */
+    std::vector<int> cap_slot;
+    int cap_n = 0;
+    float * cap = nullptr;
 };
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t) 255; }
@@ -752,6 +794,7 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     m->c = c;
     m->layers.resize(c.layers);
     m->layer_set.assign(c.layers, 0);
+    m->cap_slot.assign(c.layers, -1);
     const size_t qd = (size_t) c.heads * c.head_dim, kvd = (size_t) c.kv_heads * c.head_dim;
     size_t off = 0;
     auto take = [&](size_t bytes) { const size_t o = off; off += align256(bytes); return o; };
@@ -789,6 +832,7 @@ void sparkmv_model_destroy(void * model) {
     if (m->graph) (void) hipGraphDestroy(m->graph);
     if (m->mem) (void) hipFree(m->mem);
     if (m->vmem) (void) hipFree(m->vmem);
+    if (m->cap) (void) hipFree(m->cap);
     for (void * p : m->owned) (void) hipFree(p);
     delete m;
 }
@@ -841,6 +885,17 @@ int sparkmv::model_adopt(void * model, void * dev_ptr) {
 
 namespace {
 
+/* Layer li's input rows into its capture slot (model.rs:466-471, before the
+ * layer runs; vq-model-gpu.cu:888-895): n rows of h at pos (from st[1] when
+ * st is given). */
+int capture_rows(const Model & m, int li, const float * h, const int * st, int pos, int n, hipStream_t s) {
+    if (!m.cap_n || m.cap_slot[(size_t) li] < 0) return 0;
+    float * slot = m.cap + (size_t) m.cap_slot[(size_t) li] * m.c.max_ctx * m.c.hidden;
+    hipLaunchKernelGGL(fw_capture_kernel, dim3((m.c.hidden + 255) / 256, n), dim3(256), 0, s, h, slot, st, pos, n,
+                       m.c.hidden);
+    return check_launch("capture launch");
+}
+
 int ready(const Model * m) {
     if (m->head_kind < 0) { set_error("the model has no head"); return -1; }
     for (int li = 0; li < m->c.layers; li++)
@@ -888,6 +943,7 @@ int chain(Model * m, float * logits, hipStream_t s) {
         float * kc = m->kv + (size_t) li * 2 * c.max_ctx * kvd;
         float * vc = kc + (size_t) c.max_ctx * kvd;
 
+        if (capture_rows(*m, li, m->h, m->st, 0, 1, s)) return -1;
         if (norm_gemv2(*m, m->h, L.in_norm, L.qkv, qd + 2 * kvd, m->qkv, L.attn_gate, c.heads, m->g, c.hidden, s))
             return -1;
 
@@ -1009,6 +1065,7 @@ int block(Model * m, const uint32_t * tokens, int N, int pos, float * logits, hi
         const bool full = L.full != 0;
         float * kc = m->kv + (size_t) li * 2 * c.max_ctx * kvd;
         float * vc = kc + (size_t) c.max_ctx * kvd;
+        if (capture_rows(*m, li, m->vh, nullptr, pos, N, s)) return -1;
         if (rmsnorm(*m, m->vh, L.in_norm, s, N, m->vxn, m->vxn16)) return -1;
         if (gemv2(*m, L.qkv, ldq, m->vqkv, L.attn_gate, c.heads, m->vg, c.hidden, xin, s, N, ldq)) return -1;
         const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
@@ -1083,6 +1140,7 @@ int prompt(Model * m, int N, int pos, float * logits, hipStream_t s) {
         const bool full = L.full != 0;
         float * kc = m->kv + (size_t) li * 2 * c.max_ctx * kvd;
         float * vc = kc + (size_t) c.max_ctx * kvd;
+        if (capture_rows(*m, li, m->vh, nullptr, pos, N, s)) return -1;
         if (rmsnorm(*m, m->vh, L.in_norm, s, N, m->vxn, m->vxn16)) return -1;
         if (N <= kMaxCols) {
             if (gemv2(*m, L.qkv, ldq, m->vqkv, L.attn_gate, c.heads, m->vg, c.hidden, xin, s, N, ldq)) return -1;
@@ -1317,6 +1375,71 @@ int sparkmv_model_kv(void * model, int li, float ** k, float ** v) {
     *k = m->kv + (size_t) li * 2 * m->c.max_ctx * kvd;
     *v = *k + (size_t) m->c.max_ctx * kvd;
     return 0;
+}
+
+int sparkmv_model_enable_capture(void * model, const int * layers, int n) {
+    Model * m = (Model *) model;
+    if (!m || (n > 0 && !layers)) { set_error("model or layer list is null"); return -1; }
+    /* the runtime's limits and messages (vq-model-gpu.cu:707-736) */
+    if (n <= 0 || n > 8) { set_error("capture: %d layers requested, the limit is 8", n); return -1; }
+    if (m->cap) { set_error("capture: already enabled"); return -1; }
+    std::vector<int> slot((size_t) m->c.layers, -1);
+    for (int k = 0; k < n; k++) {
+        const int li = layers[k];
+        if (li < 0 || li >= m->c.layers) { set_error("capture: layer %d is outside 0..%d", li, m->c.layers); return -1; }
+        if (slot[(size_t) li] >= 0) { set_error("capture: layer %d is listed twice", li); return -1; }
+        slot[(size_t) li] = k;
+    }
+    void * mem = nullptr;
+    hipError_t e = hipMalloc(&mem, (size_t) n * m->c.max_ctx * m->c.hidden * sizeof(float));
+    if (e != hipSuccess) {
+        set_error("capture: cannot allocate %d x %d x %d floats", n, m->c.max_ctx, m->c.hidden);
+        return -1;
+    }
+    m->cap = (float *) mem;
+    m->cap_n = n;
+    m->cap_slot = slot;
+    /* a recorded graph lacks the copies: record it again */
+    if (m->exec) { (void) hipGraphExecDestroy(m->exec); m->exec = nullptr; }
+    if (m->graph) { (void) hipGraphDestroy(m->graph); m->graph = nullptr; }
+    return 0;
+}
+
+int sparkmv_model_captured(void * model, int k, float ** rows) {
+    Model * m = (Model *) model;
+    if (!m || !rows) { set_error("model or output is null"); return -1; }
+    if (k < 0 || k >= m->cap_n) { set_error("capture slot %d is outside 0..%d", k, m->cap_n - 1); return -1; }
+    *rows = m->cap + (size_t) k * m->c.max_ctx * m->c.hidden;
+    return m->len;
+}
+
+int sparkmv_model_embed_row(void * model, uint32_t id, float * out, void * stream) {
+    Model * m = (Model *) model;
+    if (!m || !out) { set_error("model or output is null"); return -1; }
+    if (m->head_kind < 0) { set_error("the model has no head"); return -1; }
+    if ((long) id >= m->c.vocab) { set_error("token %u is outside the vocabulary", id); return -1; }
+    const hipStream_t s = (hipStream_t) stream;
+    const sparkmv_model_cfg & c = m->c;
+    if (m->head_kind == 0) {
+        hipLaunchKernelGGL(fw_fill_kernel, dim3((c.hidden + 255) / 256), dim3(256), 0, s, out, c.hidden, 0.0f);
+        if (check_launch("fill launch")) return -1;
+        const Layout L = make_layout(c.dim, c.nc, c.vocab, c.hidden, c.v3);
+        for (int st = 0; st < c.nstages; st++)
+            if (vq_row_dequant_launch(m->head_stages[st], L, (int) id, out, s)) return -1;
+        return 0;
+    }
+    FwTok8 tk;
+    for (int t = 0; t < 8; t++) tk.t[t] = (int) id;
+    hipLaunchKernelGGL(fw_q8_0_rows_kernel, dim3((c.hidden + 255) / 256, 1), dim3(256), 0, s,
+                       (const uint8_t *) m->head_blocks, c.hidden, tk, out);
+    return check_launch("embedding launch");
+}
+
+int sparkmv_argmax(const float * logits, int n, int * out, void * stream) {
+    if (!logits || !out) { set_error("logits or output is null"); return -1; }
+    if (n < 1) { set_error("argmax needs at least one value, not %d", n); return -1; }
+    hipLaunchKernelGGL(fw_argmax_kernel, dim3(1), dim3(1024), 0, (hipStream_t) stream, logits, n, out);
+    return check_launch("argmax launch");
 }
 
 }  // extern "C"

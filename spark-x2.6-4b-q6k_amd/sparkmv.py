@@ -179,6 +179,10 @@ SIGNATURES = {
     "sparkmv_model_rollback": (_I, [_P, _I]),
     "sparkmv_model_len": (_I, [_P]),
     "sparkmv_model_kv": (_I, [_P, _I, _PP, _PP]),
+    "sparkmv_model_enable_capture": (_I, [_P, ctypes.POINTER(_I), _I]),
+    "sparkmv_model_captured": (_I, [_P, _I, _PP]),
+    "sparkmv_model_embed_row": (_I, [_P, ctypes.c_uint32, _P, _P]),
+    "sparkmv_argmax": (_I, [_P, _I, _P, _P]),
     "sparkmv_config_load": (_I, [ctypes.c_char_p, ctypes.POINTER(ModelCfg), ctypes.POINTER(_I), _I]),
     "sparkmv_model_load": (_P, [ctypes.c_char_p, ctypes.c_char_p, _I, _I, _I]),
     "sparkmv_model_apply_profile": (_I, [_P, _P, _U64, ctypes.c_char_p]),
@@ -686,6 +690,59 @@ class Model:
         k, v = ctypes.c_void_p(), ctypes.c_void_p()
         check(lib().sparkmv_model_kv(self.h, layer, ctypes.byref(k), ctypes.byref(v)), "model kv")
         return k.value, v.value
+
+    def reset(self):
+        """Forget every cached position (model.rs:384-397)."""
+        self.rollback(0)
+
+    def enable_capture(self, layers):
+        """Capture the residual entering each listed layer at every position
+        from now on (model.rs:322-348); slot k is layers[k]."""
+        arr = (_I * len(layers))(*[int(x) for x in layers])
+        check(lib().sparkmv_model_enable_capture(self.h, arr, len(layers)), "model capture")
+        self.capture_layers = [int(x) for x in layers]
+
+    def captured(self, k):
+        """Slot k's current rows as a new device f32 tensor [positions, hidden]
+        (model.rs:346-348)."""
+        torch = _torch()
+        rows = ctypes.c_void_p()
+        n = lib().sparkmv_model_captured(self.h, int(k), ctypes.byref(rows))
+        check(0 if n >= 0 else -1, "model captured")
+        hidden = self.cfg["hidden"]
+        out = torch.empty((n, hidden), dtype=torch.float32, device="cuda")
+        if n:
+            _hip_copy(out.data_ptr(), rows.value, n * hidden * 4)
+        return out
+
+    def embed_row(self, token, out=None, stream=None):
+        """The tied embedding row of token (model.rs:352-354), device f32 [hidden]."""
+        torch = _torch()
+        if out is None:
+            out = torch.empty(self.cfg["hidden"], dtype=torch.float32, device="cuda")
+        check(lib().sparkmv_model_embed_row(self.h, int(token), out.data_ptr(), _stream_ptr(stream)),
+              "model embed row")
+        return out
+
+
+def argmax(logits, stream=None):
+    """Model::argmax (model.rs:594-605) of a device f32 vector on the GPU:
+    the first of equal maxima; returns a device int32 tensor of one element."""
+    torch = _torch()
+    out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    check(lib().sparkmv_argmax(logits.data_ptr(), logits.numel(), out.data_ptr(), _stream_ptr(stream)), "argmax")
+    return out
+
+
+def _hip_copy(dst, src, nbytes):
+    """A device-to-device copy between raw pointers (the HIP runtime torch
+    already loaded), synchronous."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.restype = ctypes.c_int
+    hip.hipMemcpy.argtypes = [_P, _P, _S, _I]
+    rc = hip.hipMemcpy(dst, src, nbytes, 3)
+    if rc != 0:
+        raise SparkmvError(f"device copy failed ({rc})")
 
 
 def profile_fingerprint(dirpath):
