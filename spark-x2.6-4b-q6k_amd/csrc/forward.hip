@@ -32,6 +32,7 @@
  * HIP graph and replayed per token (sparkmv_model_capture / _replay); each
  * attention launch reserves LDS for its longest window.
  */
+#include "act.h"
 #include "kq.h"
 #include "model.h"
 #include "prefill.h"
@@ -481,9 +482,7 @@ __global__ __launch_bounds__(256) void fw_attn_combine_n_kernel(const float * pa
  * calls it. */
 __global__ void fw_gelu_mul_kernel(const float * g, const float * u, float * act, uint16_t * act16, int n) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x) {
-        const float x = g[i];
-        const double e = erf((double) x * 0.70710678118654752440);
-        const float r = 0.5f * x * (1.0f + (float) e) * u[i];
+        const float r = gelu_mul(g[i], u[i]);
         act[i] = r;
         if (act16) act16[i] = fw_bf16(r);
     }
@@ -628,6 +627,7 @@ struct Model {
     void * mem = nullptr;
     float * h, * xn, * qkv, * g, * attn, * mg, * mu, * act, * kv;
     uint16_t * xn16, * attn16, * act16;
+    uint64_t * pslot;                    /* the gate/up launch's row exchange, intermediate words, kept zero */
     int * st;                            /* token, position */
     float * part;                        /* attention partials [heads][nch_max][head_dim + 2] */
     float * rtab;                        /* rope tables [full, sliding][cos, sin][128] */
@@ -718,24 +718,43 @@ int rmsnorm(const Model & m, const float * x, const float * w, hipStream_t s, in
             uint16_t * out16 = nullptr);
 
 int norm_gemv2(const Model & m, const float * h, const float * w, const void * const * st0, int rows0, float * y0,
-               const void * const * st1, int rows1, float * y1, int cols, hipStream_t s) {
+               const void * const * st1, int rows1, float * y1, int cols, hipStream_t s, const VqPair * pair = nullptr,
+               bool * act_done = nullptr) {
     const bool b16 = m.c.x_dtype == SPARKMV_X_BF16;
+    if (act_done) *act_done = false;
+    VqMatDesc d[2];
+    memset(d, 0, sizeof d);
+    for (int i = 0; i < m.c.nstages; i++) { d[0].stages[i] = st0[i]; d[1].stages[i] = st1[i]; }
+    d[0].y = y0; d[0].rows = rows0;
+    d[1].y = y1; d[1].rows = rows1;
+    VqCall c;
+    memset(&c, 0, sizeof c);
+    c.dim = m.c.dim; c.nc = m.c.nc; c.cols = cols; c.v3 = m.c.v3; c.nst = m.c.nstages;
+    c.mats = d; c.nmat = 2;
+    c.ncol = 1; c.ldy = rows0;
+    c.accumulate = 0; c.stream = s;
     if (b16 && m.picks.empty()) {
-        VqMatDesc d[2];
-        memset(d, 0, sizeof d);
-        for (int i = 0; i < m.c.nstages; i++) { d[0].stages[i] = st0[i]; d[1].stages[i] = st1[i]; }
-        d[0].y = y0; d[0].rows = rows0;
-        d[1].y = y1; d[1].rows = rows1;
-        VqCall c;
-        memset(&c, 0, sizeof c);
-        c.dim = m.c.dim; c.nc = m.c.nc; c.cols = cols; c.v3 = m.c.v3; c.nst = m.c.nstages;
-        c.mats = d; c.nmat = 2;
-        c.x = h; c.ldx = cols; c.xf32 = 1; c.ncol = 1; c.ldy = rows0;
-        c.accumulate = 0; c.stream = s;
+        c.x = h; c.ldx = cols; c.xf32 = 1;
+        if (pair) {
+            /* one launch for the norm, both matrices and the activation */
+            const int rc = vq_norm_launch(c, w, m.c.eps, nullptr, pair);
+            if (rc <= 0) {
+                if (rc == 0 && act_done) *act_done = true;
+                return rc;
+            }
+        }
         const int rc = vq_norm_launch(c, w, m.c.eps, nullptr);
         if (rc <= 0) return rc;
     }
     if (rmsnorm(m, h, w, s, 1, nullptr, nullptr)) return -1;
+    if (pair && b16 && m.picks.empty()) {
+        c.x = m.xn16; c.ldx = cols; c.xf32 = 0;
+        const int rc = vq_pair_launch(c, *pair);
+        if (rc <= 0) {
+            if (rc == 0 && act_done) *act_done = true;
+            return rc;
+        }
+    }
     return gemv2(m, st0, rows0, y0, st1, rows1, y1, cols, b16 ? (const void *) m.xn16 : (const void *) m.xn, s);
 }
 
@@ -806,6 +825,7 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     const size_t o_st = take(2 * sizeof(int));
     const size_t o_part = take((size_t) c.heads * nch_max * (c.head_dim + 2) * 4);
     const size_t o_rtab = take(512 * 4);
+    const size_t o_pslot = take((size_t) c.intermediate * 8);
     hipError_t e = hipMalloc(&m->mem, off);
     if (e != hipSuccess) {
         fail_hip("model buffers", e);
@@ -813,6 +833,14 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
         return nullptr;
     }
     uint8_t * b = (uint8_t *) m->mem;
+    e = hipMemset(b + o_pslot, 0, (size_t) c.intermediate * 8);
+    if (e != hipSuccess) {
+        fail_hip("model pair slots", e);
+        (void) hipFree(m->mem);
+        delete m;
+        return nullptr;
+    }
+    m->pslot = (uint64_t *) (b + o_pslot);
     m->h = (float *) (b + o_h); m->xn = (float *) (b + o_xn); m->qkv = (float *) (b + o_qkv);
     m->g = (float *) (b + o_g); m->attn = (float *) (b + o_attn); m->mg = (float *) (b + o_mg);
     m->mu = (float *) (b + o_mu); m->act = (float *) (b + o_act);
@@ -972,12 +1000,18 @@ int chain(Model * m, float * logits, hipStream_t s) {
         if (gemv(*m, L.out, c.hidden, qd, b16 ? (const void *) m->attn16 : (const void *) m->attn, m->h, 1, s))
             return -1;
 
-        /* MLP (model.rs:566-581) */
-        if (norm_gemv2(*m, m->h, L.post_norm, L.gate, c.intermediate, m->mg, L.up, c.intermediate, m->mu, c.hidden, s))
+        /* MLP (model.rs:566-581): the gate/up launch writes the activation
+         * itself when its shape allows, else the activation kernel does */
+        const VqPair pair{m->pslot, c.intermediate, m->act, b16 ? m->act16 : nullptr};
+        bool act_done = false;
+        if (norm_gemv2(*m, m->h, L.post_norm, L.gate, c.intermediate, m->mg, L.up, c.intermediate, m->mu, c.hidden, s,
+                       &pair, &act_done))
             return -1;
-        hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((c.intermediate + 255) / 256), dim3(256), 0, s, m->mg, m->mu,
-                           m->act, b16 ? m->act16 : nullptr, c.intermediate);
-        if (check_launch("gelu launch")) return -1;
+        if (!act_done) {
+            hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((c.intermediate + 255) / 256), dim3(256), 0, s, m->mg, m->mu,
+                               m->act, b16 ? m->act16 : nullptr, c.intermediate);
+            if (check_launch("gelu launch")) return -1;
+        }
         if (gemv(*m, L.down, c.hidden, c.intermediate, b16 ? (const void *) m->act16 : (const void *) m->act, m->h,
                  1, s))
             return -1;

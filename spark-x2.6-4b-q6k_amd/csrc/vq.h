@@ -42,13 +42,31 @@ int profile_gemv_pick(const void * profile, int dim, int nc, int rows, int cols,
 int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant);
 /* Validate and launch; returns 0, or -1 with the message set. */
 int vq_launch(const VqCall & c);
+/* A gate/up pair's activation written by the launch that computes the pair
+ * (c.nmat == 2, equal rows, one bf16 column): besides y of both matrices,
+ * act[r] = gelu(gate[r]) * up[r] (f32, when act is set) and its bf16
+ * (act16, when set), the bits the separate activation kernel would write.
+ * slot holds cap zeroed 64-bit words (cap >= rows) through which the two
+ * matrices' rows meet; they are zero again when the launch ends, and
+ * launches that share them must not overlap. vq_norm_launch with a pair
+ * does the same from the f32 residual. Both return 1 without launching when
+ * the call's shape has no kernel that writes the activation; the caller
+ * then runs its own. */
+struct VqPair {
+    uint64_t * slot;
+    int cap;
+    float * act;
+    uint16_t * act16;
+};
+int vq_pair_launch(const VqCall & c, const VqPair & pair);
+
 /* The same launch with x = bf16(rms_norm(h) * norm_w) staged by the kernel
  * itself from the f32 residual h = c.x (c.xf32 is ignored; x_out, when
  * non-null, receives those bf16 values). Only for calls the one-column
  * straight-line kernel takes: returns 1 without launching otherwise (the
  * caller then runs the norm and vq_launch), 0 after the launch, -1 on a
  * launch error. */
-int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t * x_out);
+int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t * x_out, const VqPair * pair = nullptr);
 
 /* Decode one stage into out (row-major rows x cols f32); accumulate 0 writes
  * the stage's values as if adding into zeros. */

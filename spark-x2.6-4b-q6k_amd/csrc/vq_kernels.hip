@@ -21,6 +21,7 @@
  *   vq_dequant_kernel / vq_row_dequant_kernel: bit-exact decode (each
  *                   codeword times gain is exact in f32, one rounding per add).
  */
+#include "act.h"
 #include "vq.h"
 #include "vq_tile.h"
 #include "xrange.h"
@@ -87,6 +88,14 @@ struct FastArgs {
     const float * nw;
     float eps;
     uint16_t * xout;
+    /* A gate/up pair (two matrices of equal rows, one column): each row's
+     * y goes, tagged 1 (gate) or 2 (up), into pslot[row] by an atomic
+     * exchange; the one of the two that finds the other's value there
+     * writes gelu(gate) * up into pact (f32) and pact16 (bf16) when they
+     * are set, and clears the slot. */
+    uint64_t * pslot;
+    float * pact;
+    uint16_t * pact16;
 };
 
 constexpr int kFastMats = 4;
@@ -121,8 +130,9 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
     /* straight-line units keep at most kLook macro steps of index words in
      * flight per wave: with every step requested up front the memory system
      * serves some CUs' words last, and those CUs then do their whole unit
-     * after the stream has ended */
-    constexpr int kLook = 3;
+     * after the stream has ended. Ten-step units (gate+up: 10 waves per CU
+     * streaming 40 MB) measured best with two. */
+    constexpr int kLook = MSC >= 10 ? 2 : 3;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t cbb = (uint32_t) A.nc * 8u;
     uint8_t * lx = lds + NST * cbb;
@@ -537,6 +547,11 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                 for (int u = 0; u < D; u++) {
                     mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc, 1.0f, xm);
                     if (u + kLook < D) ld(w[u + kLook], u + kLook);
+                    /* keep step u + kLook's loads here: left to itself the
+                     * scheduler sinks them to just before their step, which
+                     * then waits a whole memory round trip. (XG units hold
+                     * 4 steps of x too: pinned, they would spill.) */
+                    if constexpr (!XG) __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
                 for (int ms0 = 0; ms0 < MS; ms0 += D) {
@@ -637,6 +652,23 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                     if (row < rows) {
                         float * yp = M.y + row;
                         *yp = (A.accumulate ? *yp : 0.0f) + sum;
+                        if (A.pslot) {
+                            /* the pair's activation: whichever of gate and up
+                             * comes second gets the other's value back from
+                             * the exchange (one memory round trip, no wait) */
+                            const uint32_t mi = (int) blockIdx.x >= A.mat[1].wg0 ? 1u : 0u;
+                            const uint64_t mine = ((uint64_t) (1u + mi) << 32) | __float_as_uint(sum);
+                            const uint64_t old =
+                                __hip_atomic_exchange(A.pslot + row, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            if ((uint32_t) (old >> 32) == 2u - mi) {
+                                const float o = __uint_as_float((uint32_t) old);
+                                const float v = mi ? gelu_mul(o, sum) : gelu_mul(sum, o);
+                                if (A.pact) A.pact[row] = v;
+                                if (A.pact16) A.pact16[row] = (uint16_t) bf16_rne(v);
+                                __hip_atomic_store(A.pslot + row, (uint64_t) 0, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                            }
+                        }
                     }
                 }
             }
@@ -1087,8 +1119,19 @@ struct FastNorm {
 /* nrm: stage bf16(rms_norm(x) * w) from the f32 residual x (one column, the
  * whole row in one launch, a one-column straight-line shape); returns 1
  * without launching when the call's shape has no such kernel. */
+/* The unit lengths with a straight-line one-column kernel (launch_ms and
+ * launch_ms_norm below). */
+static int straight_ms(int MS, int ext, int norm) {
+    switch (MS) {
+        case 1: case 2: case 4: case 5: case 8: return 1;
+        case 3: case 6: return !norm;
+        case 10: return !ext;
+        default: return 0;
+    }
+}
+
 static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, int k0, int mk,
-                            const FastNorm * nrm = nullptr) {
+                            const FastNorm * nrm = nullptr, const VqPair * pair = nullptr) {
     const Layout L0 = make_layout(c.dim, c.nc, c.mats[0].rows, c.cols, 1);
     const int ext = L0.nbit > 12;
     VqCall part = c;
@@ -1150,6 +1193,17 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
      * several-column call runs the generic kernel, which the shape search
      * kept within 10 waves */
     const int mc = sh.xg ? 2 : c.ncol > 1 && straight;
+    if (pair) {
+        /* the pair's activation is written by the one-column straight-line
+         * kernels over the whole row, both stages in this launch */
+        if (c.ncol != 1 || c.nmat != 2 || c.mats[0].rows != c.mats[1].rows || mc || !straight ||
+            !straight_ms(MS, ext, nrm != nullptr) || k0 != 0 || mk * 128 != c.cols || accumulate || st0 != 0 ||
+            nst != c.nst || c.mats[0].rows > pair->cap)
+            return 1;
+        A.pslot = pair->slot;
+        A.pact = pair->act;
+        A.pact16 = pair->act16;
+    }
     if (nrm) {
         /* the staging holds 2 chunks of 4 columns per thread */
         if (c.ncol != 1 || c.xf32 || !straight || mc || k0 != 0 || mk * 128 != c.cols || ((uintptr_t) nrm->w & 15u) ||
@@ -1238,12 +1292,13 @@ static int launch_wave(const VqCall & c, int variant) {
     return 0;
 }
 
-int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t * x_out) {
+int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t * x_out, const VqPair * pair) {
     /* the fused kernel's conditions: one f32 column, every matrix on the
      * block kernel, at most two stages and four matrices, one K range */
     if (!norm_w || c.ncol != 1 || !c.x || ((uintptr_t) c.x & 15u) || c.nst < 1 || c.nst > 2 || c.nmat < 1 ||
         c.nmat > kFastMats || c.variant || c.threads || c.grid || c.dim != 4 || c.cols % 128)
         return 1;
+    if (pair && (!pair->slot || pair->cap < 1)) return 1;
     for (int m = 0; m < c.nmat; m++) {
         if (!c.mats[m].y || c.mats[m].rows <= 0) return 1;
         for (int s = 0; s < c.nst; s++)
@@ -1255,7 +1310,23 @@ int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t *
     b.xf32 = 0;   /* what is staged: one bf16 column */
     if (fast_splits(b, c.nst) != 1) return 1;
     const FastNorm nrm{norm_w, eps, x_out};
-    return launch_fast_part(b, 0, c.nst, c.accumulate, 0, c.cols / 128, &nrm);
+    return launch_fast_part(b, 0, c.nst, c.accumulate, 0, c.cols / 128, &nrm, pair);
+}
+
+int vq_pair_launch(const VqCall & c, const VqPair & pair) {
+    /* one bf16 column in one K range, both matrices on the block kernel */
+    if (!pair.slot || pair.cap < 1 || c.ncol != 1 || !c.x || c.xf32 || ((uintptr_t) c.x & 15u) || c.nst < 1 ||
+        c.nst > 2 || c.nmat != 2 || c.variant || c.threads || c.grid || c.dim != 4 || c.cols % 128 || c.accumulate)
+        return 1;
+    for (int m = 0; m < c.nmat; m++) {
+        if (!c.mats[m].y || c.mats[m].rows <= 0) return 1;
+        for (int s = 0; s < c.nst; s++)
+            if (!c.mats[m].stages[s] || !aligned4(c.mats[m].stages[s])) return 1;
+        if (!fast_geometry_ok(c.dim, c.nc, c.mats[m].rows, c.cols, c.v3)) return 1;
+    }
+    if (c.v3 && bits_for(c.nc) > 13) return 1;
+    if (fast_splits(c, c.nst) != 1) return 1;
+    return launch_fast_part(c, 0, c.nst, 0, 0, c.cols / 128, nullptr, &pair);
 }
 
 int vq_launch(const VqCall & c) {
