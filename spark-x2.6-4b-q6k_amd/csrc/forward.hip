@@ -40,6 +40,7 @@
 
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <map>
@@ -628,6 +629,9 @@ struct Model {
     float * h, * xn, * qkv, * g, * attn, * mg, * mu, * act, * kv;
     uint16_t * xn16, * attn16, * act16;
     uint64_t * pslot;                    /* the gate/up launch's row exchange, intermediate words, kept zero */
+    /* gelu * up written by the gate/up launch (1), or by the activation
+     * kernel (0: SPARKMV_SEPARATE_ACT=1 at creation; the same bits, slower) */
+    int fuse_act = 1;
     int * st;                            /* token, position */
     float * part;                        /* attention partials [heads][nch_max][head_dim + 2] */
     float * rtab;                        /* rope tables [full, sliding][cos, sin][128] */
@@ -841,6 +845,8 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
         return nullptr;
     }
     m->pslot = (uint64_t *) (b + o_pslot);
+    const char * sep = getenv("SPARKMV_SEPARATE_ACT");
+    m->fuse_act = !(sep && sep[0] == '1');
     m->h = (float *) (b + o_h); m->xn = (float *) (b + o_xn); m->qkv = (float *) (b + o_qkv);
     m->g = (float *) (b + o_g); m->attn = (float *) (b + o_attn); m->mg = (float *) (b + o_mg);
     m->mu = (float *) (b + o_mu); m->act = (float *) (b + o_act);
@@ -1005,7 +1011,7 @@ int chain(Model * m, float * logits, hipStream_t s) {
         const VqPair pair{m->pslot, c.intermediate, m->act, b16 ? m->act16 : nullptr};
         bool act_done = false;
         if (norm_gemv2(*m, m->h, L.post_norm, L.gate, c.intermediate, m->mg, L.up, c.intermediate, m->mu, c.hidden, s,
-                       &pair, &act_done))
+                       m->fuse_act ? &pair : nullptr, &act_done))
             return -1;
         if (!act_done) {
             hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((c.intermediate + 255) / 256), dim3(256), 0, s, m->mg, m->mu,

@@ -101,6 +101,46 @@ def test_forward_against_oracle(sm, ref, dev, head_kind, xd):
     print(f"head {head_kind} x {xd}: worst relL2 {worst:.2e}")
 
 
+# hidden 2560 and intermediate 4096: the gate/up launch takes the one-column
+# straight-line kernel (S = 4, 8 waves, 5-step units), which writes the
+# activation itself; the small CFG's launch falls back to the activation kernel
+FA_CFG = dict(CFG, hidden=2560, intermediate=4096, layers=2)
+
+
+@pytest.mark.parametrize("head_kind", ["q8_0", "vq"])
+def test_fused_activation_is_bit_exact(sm, ref, dev, head_kind, monkeypatch):
+    """With bf16 activations the gate/up launch writes gelu(gate) * up itself
+    (a per-row atomic exchange between gate's and up's workgroups); a model
+    made with SPARKMV_SEPARATE_ACT=1 runs the activation kernel instead. Both
+    call the same gelu, so every logit agrees bit for bit, eager and replayed,
+    and the fused model stays within the bf16 bar of the oracle."""
+    import torch
+    fused, oracle = build(sm, ref, dev, head_kind, sm.X_BF16, FA_CFG)
+    monkeypatch.setenv("SPARKMV_SEPARATE_ACT", "1")
+    separate, _ = build(sm, ref, dev, head_kind, sm.X_BF16, FA_CFG)
+    monkeypatch.delenv("SPARKMV_SEPARATE_ACT")
+    V = FA_CFG["vocab"]
+    a = torch.zeros(V, device=dev)
+    b = torch.zeros(V, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for pos, tok in enumerate(TOKENS[:4]):
+            fused.forward(tok, pos, a, stream)
+            separate.forward(tok, pos, b, stream)
+            stream.synchronize()
+            assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32)), pos
+            assert rel_l2(a.cpu().numpy(), oracle.forward(tok, pos)) <= 2e-2
+        fused.capture(a, stream)
+        separate.capture(b, stream)
+        for pos in range(4, len(TOKENS)):
+            fused.replay(TOKENS[pos], pos, stream)
+            separate.replay(TOKENS[pos], pos, stream)
+            stream.synchronize()
+            assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32)), pos
+            assert rel_l2(a.cpu().numpy(), oracle.forward(TOKENS[pos], pos)) <= 2e-2
+    torch.cuda.synchronize()
+
+
 def test_forward_refusals(sm, ref, dev):
     import torch
     model, _ = build(sm, ref, dev, "q8_0", sm.X_F32)
