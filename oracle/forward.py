@@ -1,6 +1,6 @@
 """CPU restatement of the reference's decode forward, in numpy.
 
-Test infrastructure only: tests/ use it as the checker for the GPU forward
+Test infrastructure only: tests/ compare the GPU forward against it
 (sparkmv_model_forward); the product library never imports it.
 
 It follows tools/vq-runtime/src/model.rs:441-591 (Model::forward) in f32

@@ -1,7 +1,7 @@
 """ctypes binding of the oracle (oracle/_build/libsparkref.so).
 
 Test infrastructure only: tests/, the smoke check and bench.py's CPU-baseline
-leg load it as the checker. The product library never does.
+leg load it, to compare against. The product library never does.
 """
 import ctypes
 import os

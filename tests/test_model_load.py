@@ -2,7 +2,7 @@
 tools/vq-runtime/src/config.rs:39-85 Config::load). Host only: no GPU.
 
 The reference ships no config.json, so the files are written here: the
-shapes of the Spark checkpoint BASELINE's configs name (hidden 2560, GQA
+shapes of the Spark checkpoint (hidden 2560, GQA
 16/4 heads of 256, FFN 10240, a full layer every fourth), and variations
 that exercise each rule of Config::load: required numeric keys and
 layer_types, "full_attention" as the only sliding/full switch (other
