@@ -135,7 +135,7 @@ def build_decode_set(sm, torch, dev, ncol=1, head_rows=VOCAB, layers=LAYERS, kee
 
 
 def check_decode_set(ds, layers):
-    """The checker (oracle, after timing): each kept layer's outputs against
+    """The output check (oracle, after timing): each kept layer's outputs against
     the oracle's bit-exact decode times x in f64, every row and column, and
     every head row against the closed-form Q8_0 dot. Returns the largest
     relative L2 error per launch group."""

@@ -1,7 +1,7 @@
 """Oracle checks of a decode chain's outputs (sparkmv.DecodeChain).
 
-Test infrastructure only: tests/ and bench.py's output check use it as the
-checker; the product library never imports it.
+Test infrastructure only: tests/ and bench.py's output check compare against
+it; the product library never imports it.
 
 Every op of the chain is checked from what the GPU actually read: the
 inputs are rebuilt from the chain's own intermediate buffers with the
