@@ -14,7 +14,7 @@ are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--mode graph|eager]
                     [--workload decode-set|ffn-up|q6k-down|verify8|prefill512|forward|verify-block|
-                                decode-set-q6k]
+                                decode-set-q6k|prompt512]
 
 Prints one JSON line (rank 0). The metric is time per token (lower is
 better); achieved GB/s over the algorithmic bytes (container + bf16 x + f32 y
@@ -409,8 +409,9 @@ def bench_forward(args, sm, torch, dev):
     out / norm / gate + up / gelu / down, final norm, Q8_0 tied head. The
     cache is first filled with `context` tokens (untimed); then each step is
     one token at the next position, replayed as one HIP graph."""
-    P = args.context
-    max_ctx = P + args.warmup + args.steps + 16
+    prompt = args.workload == "prompt512"
+    P = 0 if prompt else args.context
+    max_ctx = (512 if prompt else P + args.warmup + args.steps) + 16
     cfg = dict(hidden=HIDDEN, layers=LAYERS, heads=NHEAD, kv_heads=KVD // (QD // NHEAD), head_dim=QD // NHEAD,
                intermediate=FFN, vocab=args.head_rows, eps=1e-6, sliding_window=FW_WINDOW, rope_full_theta=5.0e6,
                rope_full_partial=0.25, rope_slide_theta=1.0e4, rope_slide_partial=1.0, max_ctx=max_ctx,
@@ -443,6 +444,8 @@ def bench_forward(args, sm, torch, dev):
     logits = torch.zeros(args.head_rows, device=dev)
     toks = np.random.default_rng(6).integers(0, args.head_rows, size=max_ctx)
     ev = lambda: torch.cuda.Event(enable_timing=True)
+    if prompt:
+        return bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch)
     with torch.cuda.stream(stream):
         t0 = time.time()
         for p in range(P):
@@ -529,6 +532,50 @@ def bench_forward(args, sm, torch, dev):
         "bytes_per_token": int(total),
         "achieved_gbps": round(total / (ms * 1e-3) / 1e9, 1),
         "frac_of_peak": round(total / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
+    }
+
+
+def bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch):
+    """prompt512: one 512-token prompt chunk through the whole model
+    (sparkmv_model_forward_batch, the reference's forward_batch + tail_logits,
+    vq-model-gpu.cu:858-953, over the 512-token chunks of :1161-1173): every
+    matvec on the prefill GEMM over the chunk's tokens, batched norms, rope +
+    KV store and causal attention, then the last token's final norm and head.
+    Each step runs the chunk at position 0 and rolls the cache back."""
+    N = 512
+    chunk = [int(t) for t in toks[:N]]
+    model.reserve(N)
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            model.forward_batch(chunk, 0, logits, stream)
+            model.rollback(0)
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record(stream)
+        for _ in range(args.steps):
+            model.forward_batch(chunk, 0, logits, stream)
+            model.rollback(0)
+        b.record(stream)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    assert bool(torch.isfinite(logits).all()), "non-finite logits"
+    # matvec work: 2 flop per weight and token over the trunk, the head for one token
+    weights = LAYERS * ((QD + 2 * KVD + NHEAD) * HIDDEN + HIDDEN * QD + 3 * FFN * HIDDEN)
+    flop = 2.0 * weights * N + 2.0 * args.head_rows * HIDDEN
+    log(f"  prompt chunk of {N}: {ms * 1e3:.1f} us, {N / (ms * 1e-3):.0f} tokens/s, "
+        f"{flop / (ms * 1e-3) / 1e12:.0f} TFLOP/s of matvec work")
+    return {
+        "metric": "prompt chunk us/chunk (512 tokens at position 0, whole model, last token's logits)",
+        "value": round(ms * 1e3, 2), "unit": "us/chunk", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16xf16->f32 prefill GEMM (bf16 x rounded to f16), f32 elementwise",
+        "data": "synthetic (seeded, random-init weights of the real shapes)",
+        "config": {"workload": "prompt chunk of 512 tokens at position 0", "layers": LAYERS, "hidden": HIDDEN,
+                   "ffn": FFN, "heads": NHEAD, "sliding_window": FW_WINDOW, "head": f"Q8_0 {args.head_rows}x{HIDDEN}",
+                   "mode": "eager"},
+        "tokens_per_s": round(N / (ms * 1e-3), 1),
+        "matvec_tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+        "weight_bytes": int(mat_bytes + head.nbytes),
     }
 
 
@@ -698,7 +745,7 @@ def main():
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--workload", default="decode-set",
                     choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512", "forward",
-                             "verify-block", "decode-set-q6k", "decode-chain"])
+                             "verify-block", "decode-set-q6k", "decode-chain", "prompt512"])
     ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -737,7 +784,7 @@ def main():
         out = bench_decode_set_q6k(args, sm, torch, dev)
     elif args.workload == "decode-chain":
         out = bench_decode_chain(args, sm, torch, dev)
-    elif args.workload in ("forward", "verify-block"):
+    elif args.workload in ("forward", "verify-block", "prompt512"):
         out = bench_forward(args, sm, torch, dev)
     else:
         out = bench_single(args, sm, torch, dev)

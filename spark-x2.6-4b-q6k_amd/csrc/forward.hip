@@ -612,6 +612,243 @@ __global__ __launch_bounds__(256) void fw_attn_prompt_kernel(const float * qkv, 
     }
 }
 
+/* The same prompt attention on the f32 matrix cores, for 256-element heads
+ * (the reference model's): one workgroup per (query head, 16 query tokens),
+ * the grid ordered so that the blocks with the longest causal range start
+ * first. The block's positions are cut into tiles of 16; wave w of the 4
+ * takes tiles w, w + 4, w + 8, ..., with its own running maximum, sum and
+ * output, merged at the end. No wave reads another's K or V rows, so a wave
+ * loads them from global memory straight into the MFMA operand layout, with
+ * no LDS staging and no barrier in the loop: V of a tile is requested before
+ * the tile's scores are formed and K of the next tile right after, so both
+ * arrive while MFMAs run. Per tile a wave forms the 16 x 16 scores
+ * S^T = K Q^T (positions x tokens) with 64 v_mfma_f32_16x16x4f32 (four
+ * accumulators, so consecutive MFMAs do not wait for each other), masks
+ * positions outside each token's window (causal, and the sliding window),
+ * weights them by exp(score - m) for a per-token reference m, and adds
+ * O^T += V^T P^T with 64 more. Unlike the kernel above, m is not the running
+ * maximum itself: it moves (the sums and outputs rescaled) only when a score
+ * passes it by more than kPaLag, which keeps every weight below e^8 and
+ * spares most tiles the exchange between lanes and the rescale. The quotient
+ * of outputs and sums does not depend on m; products and sums stay in f32,
+ * and only the rounding and the order of the additions differ from the
+ * kernel above.
+ *
+ * Operand layouts (lane l = 16 g + c): an A operand is A[l % 16][l / 16]
+ * (16 x 4), a B operand B[l / 16][l % 16] (4 x 16), and the 16 x 16 result
+ * sits as D[4 (l / 16) + i][l % 16], i < 4. Which head element a (k-step,
+ * lane group) pair contracts over is free as long as both operands agree:
+ * lane (g, c) feeds K[c][pa_k(ks, g)] and Q[c][pa_k(ks, g)] at k-step ks:
+ * it reads its K row as 16 runs of 4 floats, the 4 lane groups of a row
+ * together 64 contiguous bytes (a load instruction touches 16 cache lines,
+ * not 64), and holds the scores of token c at positions 4 g + i. For O^T, k-step ks takes positions 4 g + ks: the B
+ * value is the lane's own probability i = ks, and the A value is
+ * V[4 g + ks][d], with the rows of O^T permuted (pa_d) so that d too runs in
+ * groups of 4: the 16 lanes of a group read 256 contiguous bytes of a row. */
+constexpr int kPaTok = 16;     /* query tokens per workgroup */
+constexpr float kPaLag = 8.0f; /* how far a score may pass the reference maximum */
+
+/* head element contracted at k-step ks by lane group g in S^T = K Q^T */
+static __device__ __forceinline__ int pa_k(int ks, int g) { return 16 * (ks >> 2) + 4 * g + (ks & 3); }
+/* head element of row R of O^T block b */
+static __device__ __forceinline__ int pa_d(int b, int R) { return 64 * (b >> 2) + 4 * R + (b & 3); }
+
+__global__ __launch_bounds__(256) void fw_attn_prompt_mfma_kernel(const float * qkv, int ldq, int kvd,
+                                                                   const float * kc, const float * vc,
+                                                                   const float * gate, int ldg, int pos0, int N,
+                                                                   int window, int heads, int kv_heads, float scale,
+                                                                   float * out, uint16_t * out16) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    /* the merge after the loop: outputs handed between waves, 3 x 4 blocks
+     * of 64 x 4 floats per wave, and the maximum and sum per token of each */
+    __shared__ f4v lds_o[48 * 64];
+    __shared__ float lds_s[4 * 32];
+    const int h = blockIdx.x, t0 = ((int) gridDim.y - 1 - (int) blockIdx.y) * kPaTok;
+    const int kvh = h / (heads / kv_heads);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
+    /* this lane's token (column c); tokens past N compute a copy of the last
+     * one and store nothing */
+    const int tv = min(t0 + c, N - 1), pos_t = pos0 + tv;
+    const int start_t = window > 0 && pos_t + 1 > window ? pos_t + 1 - window : 0;
+    /* the block's positions: from the first token's window start to the last token */
+    const int tl = min(t0 + kPaTok - 1, N - 1);
+    const int pfirst = window > 0 && pos0 + t0 + 1 > window ? pos0 + t0 + 1 - window : 0;
+    const int plast = pos0 + tl;
+    /* Q^T as the B operand: Q[c][pa_k(ks, g)], ks < 64 */
+    float qv[64];
+    {
+        const float * qp = qkv + (size_t) tv * ldq + (size_t) h * 256;
+#pragma unroll
+        for (int ks = 0; ks < 64; ks += 4) {
+            const f4v q4 = *(const f4v *) (qp + pa_k(ks, g));
+            qv[ks] = q4[0];
+            qv[ks + 1] = q4[1];
+            qv[ks + 2] = q4[2];
+            qv[ks + 3] = q4[3];
+        }
+    }
+    f4v o[16];
+#pragma unroll
+    for (int db = 0; db < 16; db++) o[db] = f4v{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.0f;
+    const float * kbase = kc + (size_t) kvh * 256;
+    const float * vbase = vc + (size_t) kvh * 256;
+    /* K rows pw + c and V rows pw + 4 g + ks of the tile at pw; rows past
+     * plast repeat it and are masked. Each is requested for the next tile as
+     * soon as this tile's MFMAs have read it, so it has most of a tile's time
+     * to arrive. The requests are unconditional (past the last tile they all
+     * read row plast again): behind a branch, the waits for this tile's V
+     * would also cover the next tile's K */
+    f4v kf[16], vf[16];
+    auto fetch_k = [&](int pw) {
+        const float * kp = kbase + (size_t) min(pw + c, plast) * kvd;
+#pragma unroll
+        for (int j = 0; j < 16; j++) kf[j] = *(const f4v *) (kp + pa_k(4 * j, g));
+    };
+    auto fetch_v = [&](int pw) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const float * vp = vbase + (size_t) min(pw + 4 * g + ks, plast) * kvd + 4 * c;
+#pragma unroll
+            for (int q = 0; q < 4; q++) vf[4 * ks + q] = *(const f4v *) (vp + 64 * q);
+        }
+    };
+    const int pbeg = (pfirst & ~15) + 16 * wave;
+    /* Q, then K, then V, in the order the loop waits for them */
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_k(pbeg);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_v(pbeg);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int pw = pbeg; pw <= plast; pw += 64) {
+        /* S^T = K Q^T */
+        f4v s0 = f4v{0.f, 0.f, 0.f, 0.f}, s1 = s0, s2 = s0, s3 = s0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j][0], qv[4 * j], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j][1], qv[4 * j + 1], s1, 0, 0, 0);
+            s2 = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j][2], qv[4 * j + 2], s2, 0, 0, 0);
+            s3 = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j][3], qv[4 * j + 3], s3, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_k(pw + 64);
+        __builtin_amdgcn_sched_barrier(0);
+        const f4v s = (s0 + s1) + (s2 + s3);
+        /* scale and mask: position pw + 4 g + i for token c */
+        float e[4];
+        float mc = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int pp = pw + 4 * g + i;
+            const bool ok = pp >= start_t && pp <= pos_t;
+            e[i] = ok ? s[i] * scale : -INFINITY;
+            mc = fmaxf(mc, e[i]);
+        }
+        /* the weights are exp(score - m) for a reference m per token that
+         * moves only when a score passes it by more than kPaLag (then to the
+         * token's maximum so far, the sum and outputs rescaled): the weights
+         * stay below e^kPaLag, and most tiles need neither an exchange
+         * between lanes nor a rescale */
+        if (__any(mc > m + kPaLag)) {   /* uniform */
+            mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
+            mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
+            const float mn = fmaxf(m, mc);
+            /* nothing seen yet for this token: no rescale */
+            const float a = mn == -INFINITY ? 1.0f : expf(m - mn);
+            l *= a;
+#pragma unroll
+            for (int db = 0; db < 16; db++) o[db] *= a;
+            m = mn;
+        }
+        /* l holds this lane's share of the sum (its 4 positions), reduced
+         * over the lane groups after the loop */
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            e[i] = e[i] == -INFINITY ? 0.0f : expf(e[i] - m);
+            l += e[i];
+        }
+        /* O^T += V^T P^T; row c of block db is element pa_d(db, c) */
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    o[4 * q + r] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[4 * ks + q][r], e[ks], o[4 * q + r], 0, 0,
+                                                                        0);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_v(pw + 64);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    /* merge: wave w finishes head elements 64 w .. 64 w + 63 (blocks
+     * 4 w .. 4 w + 3 of O^T) of the 16 tokens. The other waves hand it their
+     * outputs for those blocks through LDS in their register layout, a slot
+     * of 64 x 4 floats per (source wave, owner, block), owners' own blocks
+     * not stored; every wave hands over its maximum and sum per token */
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        if (w == wave) continue;   /* uniform */
+        const int k = (w - wave + 3) & 3;   /* 0 .. 2: the owner's index among the others */
+#pragma unroll
+        for (int b = 0; b < 4; b++) lds_o[((wave * 3 + k) * 4 + b) * 64 + lane] = o[4 * w + b];
+    }
+    if (g == 0) {
+        lds_s[wave * 32 + c] = m;
+        lds_s[wave * 32 + 16 + c] = l;
+    }
+    __syncthreads();
+    float mw[4], aw[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) mw[w] = lds_s[w * 32 + c];
+    const float mt = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+    float lt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        aw[w] = mw[w] == -INFINITY ? 0.0f : expf(mw[w] - mt);
+        lt += lds_s[w * 32 + 16 + c] * aw[w];
+    }
+    /* sum over the source waves in wave order, this wave's own blocks from
+     * its registers */
+    f4v v[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            f4v x;
+            if (w == wave) {   /* uniform */
+                x = o[4 * w + b];
+            } else {
+                const int k = (wave - w + 3) & 3;
+                x = lds_o[((w * 3 + k) * 4 + b) * 64 + lane];
+            }
+            v[b] = w == 0 ? x * aw[0] : v[b] + x * aw[w];
+        }
+    }
+    if (t0 + c >= N) return;
+    const float gs = 1.0f / (1.0f + expf(-gate[(size_t) tv * ldg + h]));
+    const float inv = 1.0f / lt;
+    /* element pa_d(4 wave + b, 4 g + i) = 64 wave + 16 g + 4 i + b: four
+     * consecutive elements per i */
+    const size_t ob = (size_t) tv * heads * 256 + (size_t) h * 256 + 64 * wave + 16 * g;
+    f4v r[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r[i] = f4v{v[0][i], v[1][i], v[2][i], v[3][i]} * inv * gs;
+        *(f4v *) (out + ob + 4 * i) = r[i];
+    }
+    if (out16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint2 p;
+            p.x = (uint32_t) fw_bf16(r[i][0]) | ((uint32_t) fw_bf16(r[i][1]) << 16);
+            p.y = (uint32_t) fw_bf16(r[i][2]) | ((uint32_t) fw_bf16(r[i][3]) << 16);
+            *(uint2 *) (out16 + ob + 4 * i) = p;
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ host -- */
 
 namespace {
@@ -1197,7 +1434,12 @@ int prompt(Model * m, int N, int pos, float * logits, hipStream_t s) {
         const int window = full ? 0 : c.sliding_window;
         const dim3 ag((unsigned) c.kv_heads, (unsigned) N), ab((unsigned) (64 * (c.heads / c.kv_heads)));
         uint16_t * a16 = b16 ? m->vattn16 : nullptr;
-        if (hd == 64)
+        if (hd == 256) {
+            hipLaunchKernelGGL(fw_attn_prompt_mfma_kernel, dim3((unsigned) c.heads, (unsigned) ((N + kPaTok - 1) / kPaTok)),
+                               dim3(256), 0, s, m->vqkv, ldq, kvd, kc, vc, m->vg, ldq, pos, N, window,
+                               c.heads, c.kv_heads, scale, m->vattn, a16);
+        }
+        else if (hd == 64)
             hipLaunchKernelGGL(fw_attn_prompt_kernel<1>, ag, ab, 0, s, m->vqkv, ldq, kvd, kc, vc, m->vg, ldq, pos,
                                window, c.heads, c.kv_heads, scale, m->vattn, a16);
         else if (hd == 128)

@@ -50,10 +50,11 @@ def kv_rows(model, dev, li, n, kvd):
     return out
 
 
-def check_kv(model, oracle, dev, n, bar, label):
-    kvd = LONG["kv_heads"] * LONG["head_dim"]
+def check_kv(model, oracle, dev, n, bar, label, cfg=None):
+    cfg = cfg or LONG
+    kvd = cfg["kv_heads"] * cfg["head_dim"]
     worst = 0.0
-    for li in range(LONG["layers"]):
+    for li in range(cfg["layers"]):
         for got, want in zip(kv_rows(model, dev, li, n, kvd), (oracle.kv_k[li], oracle.kv_v[li])):
             worst = max(worst, rel_l2(got, want[:n]))
     print(f"{label}: KV rows 0..{n - 1} worst relL2 {worst:.2e}")
@@ -128,6 +129,40 @@ def test_forward_batch_against_oracle(sm, ref, dev, head_kind, xd):
         check_kv(model, oracle, dev, NTOK + 2, bar, f"head {head_kind} prompt")
 
 
+@pytest.mark.parametrize("heads,kvh", [(4, 1), (8, 2)], ids=["kv1", "kv2"])
+def test_forward_batch_mfma_attention(sm, ref, dev, heads, kvh):
+    """Heads of 256 with 4 query heads per kv head (the reference model's
+    shape) take the matrix-core prompt attention (16 tokens per workgroup,
+    K and V through LDS 16 positions at a time). Chunks of 100 and 37
+    tokens cross the 40-position window and tile boundaries mid-block; the
+    last logits, the decode steps after and every KV row (each layer's rows
+    depend on every token's attention output in the layers below) meet the
+    f32 prompt bar against the oracle."""
+    import torch
+    cfg = dict(LONG, head_dim=256, heads=heads, kv_heads=kvh)
+    model, oracle = build(sm, ref, dev, "q8_0", sm.X_F32, cfg)
+    model.reserve(128)
+    toks = tokens(139, seed=17)
+    logits = torch.full((cfg["vocab"],), float("nan"), device=dev)
+    bar = 5e-3
+    for lo, hi in ((0, 100), (100, 137)):
+        want = None
+        for p in range(lo, hi):
+            want = oracle.forward(toks[p], p)
+        model.forward_batch(toks[lo:hi], lo, logits)
+        torch.cuda.synchronize()
+        err = rel_l2(logits.cpu().numpy(), want)
+        print(f"heads {heads}/{kvh}: chunk {lo}..{hi - 1}, last logits relL2 {err:.2e}")
+        assert err <= bar
+    for p in (137, 138):
+        model.forward(toks[p], p, logits)
+        torch.cuda.synchronize()
+        err = rel_l2(logits.cpu().numpy(), oracle.forward(toks[p], p))
+        print(f"heads {heads}/{kvh}: decode at {p}, relL2 {err:.2e}")
+        assert err <= bar
+    check_kv(model, oracle, dev, 139, bar, f"heads {heads}/{kvh} prompt", cfg)
+
+
 def test_forward_batch_short_chunk_is_exact(sm, ref, dev):
     """A chunk of 12 tokens (at most 16: every matvec on the batched GEMV)
     keeps the decode arithmetic: 1e-5 with f32 activations for the last
@@ -146,6 +181,39 @@ def test_forward_batch_short_chunk_is_exact(sm, ref, dev):
     print(f"12-token chunk: last logits relL2 {err:.2e}")
     assert err <= 1e-5
     check_kv(model, oracle, dev, 12, 1e-5, "12-token chunk")
+
+
+@pytest.mark.parametrize("heads,kvh", [(4, 1), (8, 2)], ids=["kv1", "kv2"])
+def test_forward_batch_mfma_attention_is_exact(sm, ref, dev, heads, kvh):
+    """The matrix-core prompt attention alone, held to the decode bar: 30
+    decode steps, then a chunk of 12 tokens at position 30 (the batched GEMV
+    keeps every matvec exact in f32), whose last two tokens' 40-position
+    windows start past 0, then two decode steps. Its products and sums are
+    f32 like the decode attention's, only summed in another order, so the
+    last logits and every KV row meet 1e-5."""
+    import torch
+    cfg = dict(LONG, head_dim=256, heads=heads, kv_heads=kvh)
+    model, oracle = build(sm, ref, dev, "q8_0", sm.X_F32, cfg)
+    toks = tokens(44, seed=19)
+    logits = torch.full((cfg["vocab"],), float("nan"), device=dev)
+    for p in range(30):
+        model.forward(toks[p], p, logits)
+        oracle.forward(toks[p], p)
+    want = None
+    for p in range(30, 42):
+        want = oracle.forward(toks[p], p)
+    model.forward_batch(toks[30:42], 30, logits)
+    torch.cuda.synchronize()
+    err = rel_l2(logits.cpu().numpy(), want)
+    print(f"heads {heads}/{kvh}: 12-token chunk at 30, last logits relL2 {err:.2e}")
+    assert err <= 1e-5
+    for p in (42, 43):
+        model.forward(toks[p], p, logits)
+        torch.cuda.synchronize()
+        err = rel_l2(logits.cpu().numpy(), oracle.forward(toks[p], p))
+        print(f"heads {heads}/{kvh}: decode at {p}, relL2 {err:.2e}")
+        assert err <= 1e-5
+    check_kv(model, oracle, dev, 44, 1e-5, f"heads {heads}/{kvh} chunk at 30", cfg)
 
 
 def test_forward_batch_refusals(sm, ref, dev):
