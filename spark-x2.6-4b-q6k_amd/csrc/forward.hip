@@ -660,7 +660,8 @@ __global__ __launch_bounds__(256) void fw_attn_prompt_mfma_kernel(const float * 
                                                                    float * out, uint16_t * out16) {
     typedef float f4v __attribute__((ext_vector_type(4)));
     /* the merge after the loop: outputs handed between waves, 3 x 4 blocks
-     * of 64 x 4 floats per wave, and the maximum and sum per token of each */
+     * of 64 x 4 floats per wave, and the maximum and sum per token of each;
+     * before the loop the block's Q rows pass through the first part */
     __shared__ f4v lds_o[48 * 64];
     __shared__ float lds_s[4 * 32];
     const int h = blockIdx.x, t0 = ((int) gridDim.y - 1 - (int) blockIdx.y) * kPaTok;
@@ -674,18 +675,30 @@ __global__ __launch_bounds__(256) void fw_attn_prompt_mfma_kernel(const float * 
     const int tl = min(t0 + kPaTok - 1, N - 1);
     const int pfirst = window > 0 && pos0 + t0 + 1 > window ? pos0 + t0 + 1 - window : 0;
     const int plast = pos0 + tl;
-    /* Q^T as the B operand: Q[c][pa_k(ks, g)], ks < 64 */
+    /* the gate, requested first: it is needed at the end */
+    const float gate_t = gate[(size_t) tv * ldg + h];
+    /* Q^T as the B operand: Q[c][pa_k(ks, g)], ks < 64. The block's 16 Q rows
+     * are read once per workgroup into LDS (rows of 65 x 4 floats, so the 16
+     * rows of a lane group fall on distinct banks), in the space the merge
+     * uses after the loop */
     float qv[64];
     {
-        const float * qp = qkv + (size_t) tv * ldq + (size_t) h * 256;
+        f4v * lds_q = lds_o;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = tid + 256 * k, tk = i >> 6, c4 = i & 63;
+            lds_q[tk * 65 + c4] = *(const f4v *) (qkv + (size_t) min(t0 + tk, N - 1) * ldq + (size_t) h * 256 + 4 * c4);
+        }
+        __syncthreads();
 #pragma unroll
         for (int ks = 0; ks < 64; ks += 4) {
-            const f4v q4 = *(const f4v *) (qp + pa_k(ks, g));
+            const f4v q4 = lds_q[c * 65 + pa_k(ks, g) / 4];
             qv[ks] = q4[0];
             qv[ks + 1] = q4[1];
             qv[ks + 2] = q4[2];
             qv[ks + 3] = q4[3];
         }
+        __syncthreads();   /* every wave holds its Q before any writes the merge */
     }
     f4v o[16];
 #pragma unroll
@@ -827,17 +840,16 @@ __global__ __launch_bounds__(256) void fw_attn_prompt_mfma_kernel(const float * 
         }
     }
     if (t0 + c >= N) return;
-    const float gs = 1.0f / (1.0f + expf(-gate[(size_t) tv * ldg + h]));
+    const float gs = 1.0f / (1.0f + expf(-gate_t));
     const float inv = 1.0f / lt;
     /* element pa_d(4 wave + b, 4 g + i) = 64 wave + 16 g + 4 i + b: four
      * consecutive elements per i */
     const size_t ob = (size_t) tv * heads * 256 + (size_t) h * 256 + 64 * wave + 16 * g;
+    /* the bf16 copy when one is asked for (the next matvec reads only it),
+     * else the f32 output */
     f4v r[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        r[i] = f4v{v[0][i], v[1][i], v[2][i], v[3][i]} * inv * gs;
-        *(f4v *) (out + ob + 4 * i) = r[i];
-    }
+    for (int i = 0; i < 4; i++) r[i] = f4v{v[0][i], v[1][i], v[2][i], v[3][i]} * inv * gs;
     if (out16) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -846,6 +858,9 @@ __global__ __launch_bounds__(256) void fw_attn_prompt_mfma_kernel(const float * 
             p.y = (uint32_t) fw_bf16(r[i][2]) | ((uint32_t) fw_bf16(r[i][3]) << 16);
             *(uint2 *) (out16 + ob + 4 * i) = p;
         }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(f4v *) (out + ob + 4 * i) = r[i];
     }
 }
 
