@@ -334,34 +334,76 @@ __global__ void fw_q8_0_rows_kernel(const uint8_t * blocks, int cols, FwTok8 tok
     out[(size_t) t * cols + i] = (float) d * (float) (int8_t) b[2 + (i & 31)];
 }
 
-/* Rope and the KV store for token t = blockIdx.y at position pos0 + t:
- * items [0, (heads + kv_heads) * half) rotate a pair of one q or k head in
- * place (model.rs:416-438, f32 table), items [0, kvd) store v and the k
- * elements past pdim; a rotated k pair goes to the cache too. */
-__global__ void fw_rope_kv_n_kernel(float * qkv, int ldq, int qd, int kvd, int heads, int kv_heads, int hd, int pdim,
-                                    float theta, int pos0, float * kc, float * vc) {
-    const int half = pdim / 2, t = blockIdx.y, pos = pos0 + t;
-    const int i0 = blockIdx.x * blockDim.x + threadIdx.x;
+/* Rope and the KV store for token t = blockIdx.x at position pos0 + t: pair
+ * i's cos and sin computed once per token with the expressions of the decode
+ * tables (model.rs:416-438, f32), then pair i of every q and k head rotated
+ * in place, a rotated k pair stored to the cache too; v and the k elements
+ * past pdim stored to the cache. pdim <= 256. */
+__global__ __launch_bounds__(256) void fw_rope_kv_n_kernel(float * qkv, int ldq, int qd, int kvd, int heads,
+                                                            int kv_heads, int hd, int pdim, float theta, int pos0,
+                                                            float * kc, float * vc) {
+    __shared__ float cs[2][128];
+    const int half = pdim / 2, t = blockIdx.x, pos = pos0 + t, tid = threadIdx.x;
     float * row = qkv + (size_t) t * ldq;
-    if (i0 < (heads + kv_heads) * half) {
-        const int h = i0 / half, i = i0 - h * half;
-        const float freq = 1.0f / powf(theta, (float) (2 * i) / (float) pdim);
+    if (tid < half) {
+        const float freq = 1.0f / powf(theta, (float) (2 * tid) / (float) pdim);
         const float a = (float) pos * freq;
-        const float c = cosf(a), sn = sinf(a);
-        float * base = h < heads ? row + (size_t) h * hd : row + qd + (size_t) (h - heads) * hd;
-        const float x0 = base[i], x1 = base[i + half];
-        const float r0 = x0 * c - x1 * sn, r1 = x1 * c + x0 * sn;
-        base[i] = r0;
-        base[i + half] = r1;
-        if (h >= heads) {
-            float * k = kc + (size_t) pos * kvd + (size_t) (h - heads) * hd;
-            k[i] = r0;
-            k[i + half] = r1;
+        cs[0][tid] = cosf(a);
+        cs[1][tid] = sinf(a);
+    }
+    __syncthreads();
+    /* four items per thread at a time, every load issued before the stores
+     * (which write the rows read) */
+    constexpr int B = 4;
+    const int nrot = (heads + kv_heads) * half;
+    for (int j0 = tid; j0 < nrot; j0 += B * blockDim.x) {
+        float x0[B], x1[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const int j = j0 + b * blockDim.x;
+            if (j < nrot) {
+                const int h = j / half, i = j - h * half;
+                const float * base = h < heads ? row + (size_t) h * hd : row + qd + (size_t) (h - heads) * hd;
+                x0[b] = base[i];
+                x1[b] = base[i + half];
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const int j = j0 + b * blockDim.x;
+            if (j < nrot) {
+                const int h = j / half, i = j - h * half;
+                const float c = cs[0][i], sn = cs[1][i];
+                float * base = h < heads ? row + (size_t) h * hd : row + qd + (size_t) (h - heads) * hd;
+                const float r0 = x0[b] * c - x1[b] * sn, r1 = x1[b] * c + x0[b] * sn;
+                base[i] = r0;
+                base[i + half] = r1;
+                if (h >= heads) {
+                    float * k = kc + (size_t) pos * kvd + (size_t) (h - heads) * hd;
+                    k[i] = r0;
+                    k[i + half] = r1;
+                }
+            }
         }
     }
-    if (i0 < kvd) {
-        vc[(size_t) pos * kvd + i0] = row[qd + kvd + i0];
-        if (i0 % hd >= 2 * half) kc[(size_t) pos * kvd + i0] = row[qd + i0];
+    for (int j0 = tid; j0 < kvd; j0 += B * blockDim.x) {
+        float v[B], k[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const int j = j0 + b * blockDim.x;
+            if (j < kvd) {
+                v[b] = row[qd + kvd + j];
+                k[b] = row[qd + j];
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const int j = j0 + b * blockDim.x;
+            if (j < kvd) {
+                vc[(size_t) pos * kvd + j] = v[b];
+                if (j % hd >= 2 * half) kc[(size_t) pos * kvd + j] = k[b];
+            }
+        }
     }
 }
 
@@ -1362,9 +1404,8 @@ int block(Model * m, const uint32_t * tokens, int N, int pos, float * logits, hi
         if (gemv2(*m, L.qkv, ldq, m->vqkv, L.attn_gate, c.heads, m->vg, c.hidden, xin, s, N, ldq)) return -1;
         const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
         const int pdim = rope_dim(hd, full ? c.rope_full_partial : c.rope_slide_partial);
-        const int items = (c.heads + c.kv_heads) * (pdim / 2) > kvd ? (c.heads + c.kv_heads) * (pdim / 2) : kvd;
-        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3((items + 255) / 256, N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd,
-                           c.heads, c.kv_heads, hd, pdim, (float) theta, pos, kc, vc);
+        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3(N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd, c.heads, c.kv_heads, hd,
+                           pdim, (float) theta, pos, kc, vc);
         if (check_launch("rope launch")) return -1;
         const int window = full ? 0 : c.sliding_window;
         const int last = pos + N - 1;
@@ -1442,9 +1483,8 @@ int prompt(Model * m, int N, int pos, float * logits, hipStream_t s) {
         }
         const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
         const int pdim = rope_dim(hd, full ? c.rope_full_partial : c.rope_slide_partial);
-        const int items = (c.heads + c.kv_heads) * (pdim / 2) > kvd ? (c.heads + c.kv_heads) * (pdim / 2) : kvd;
-        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3((items + 255) / 256, N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd,
-                           c.heads, c.kv_heads, hd, pdim, (float) theta, pos, kc, vc);
+        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3(N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd, c.heads, c.kv_heads, hd,
+                           pdim, (float) theta, pos, kc, vc);
         if (check_launch("rope launch")) return -1;
         const int window = full ? 0 : c.sliding_window;
         const dim3 ag((unsigned) c.kv_heads, (unsigned) N), ab((unsigned) (64 * (c.heads / c.kv_heads)));
