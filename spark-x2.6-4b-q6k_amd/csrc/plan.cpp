@@ -33,6 +33,7 @@ struct PlanOp {
 
 struct Plan {
     std::vector<PlanOp> ops;
+    std::vector<void *> slots;   /* each several-column op's shared-tile words */
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
@@ -66,6 +67,7 @@ void sparkmv_plan_destroy(void * plan) {
     Plan * p = (Plan *) plan;
     if (!p) return;
     drop_graph(p);
+    for (void * q : p->slots) hipFree(q);
     delete p;
 }
 
@@ -95,6 +97,23 @@ int sparkmv_plan_add_vq(void * plan, const sparkmv_vq_matrix * mats, int nmat, i
     c.nmat = nmat; c.x = x; c.ldx = ldx; c.xf32 = x_dtype == SPARKMV_X_F32; c.ncol = ncols; c.ldy = ldy;
     c.accumulate = accumulate ? 1 : 0;
     c.variant = variant;
+    if (nmat == 1 && ncols > 1 && mats[0].rows > 0) {
+        /* zeroed words for workgroups that share a tile (the kernel leaves
+         * them zero); allocated here, so running the plan allocates nothing */
+        const size_t n = (size_t) mats[0].rows * ncols;
+        void * q = nullptr;
+        hipError_t e = hipMalloc(&q, n * sizeof(uint64_t));
+        if (e == hipSuccess) e = hipMemset(q, 0, n * sizeof(uint64_t));
+        /* the zeros land before any stream's first launch of the plan */
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            if (q) hipFree(q);
+            return fail_hip("plan shared-tile words", e);
+        }
+        p->slots.push_back(q);
+        c.kslot = (uint64_t *) q;
+        c.kslot_cap = (long) n;
+    }
     p->ops.push_back(op);
     drop_graph(p);
     return 0;

@@ -28,6 +28,13 @@ struct VqCall {
     int variant;   /* 0 auto, 1 generic, 2 LDS-codebook wave kernel, 3 MFMA block kernel */
     int threads;   /* workgroup width, a multiple of 64; 0 = the default */
     int grid;      /* workgroups; 0 = the default */
+    /* Zeroed 64-bit words, at least rows * ncol of them, through which two
+     * workgroups that share a tile's K chunks meet (several columns with x
+     * read from global memory, one matrix); null keeps every tile inside one
+     * workgroup. They are zero again when a launch ends; launches that share
+     * them must not overlap. */
+    uint64_t * kslot = nullptr;
+    long kslot_cap = 0;
 };
 
 /* The kernel a profile's gemv entry (tools/vq/gpu/vq-profile.h, the

@@ -96,6 +96,15 @@ struct FastArgs {
     uint64_t * pslot;
     float * pact;
     uint16_t * pact16;
+    /* Shared tiles (XG, one matrix): workgroup b works the W consecutive
+     * (tile, K chunk) units W*b .. W*b + W - 1 in tile-major order (W waves),
+     * so every CU gets the same share even when tiles do not divide over the
+     * CUs. A tile whose chunks fall to two workgroups meets in kslot[row *
+     * ncol + col]: each side exchanges its sum there, and the one that finds
+     * the other's adds the two (addition commutes, so the bits do not depend
+     * on which comes second), writes y and clears the word. */
+    int sk;
+    uint64_t * kslot;
 };
 
 constexpr int kFastMats = 4;
@@ -159,11 +168,17 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         M.wg0 = take ? A.mat[k].wg0 : M.wg0;
     }
     const int rows = M.rows;
-    /* T consecutive tiles per workgroup (the host sized nwg = ceil(tiles / T)) */
-    const int t0 = ((int) blockIdx.x - M.wg0) * A.T, t1 = min(t0 + A.T, M.tiles);
     const int S = 1 << A.lgS, C = A.C, T = A.T, ncol = A.ncol;
     const int rpt = 16 >> A.lgS;                   /* rows per tile */
-    const int j = wave / C, c = wave - j * C;      /* tile slot, K chunk */
+    /* T consecutive tiles per workgroup (the host sized nwg = ceil(tiles / T)),
+     * or, with shared tiles, this wave's one (tile, chunk) unit */
+    const bool sk = XG && A.sk;
+    const int W = A.threads >> 6;
+    const int usk = ((int) blockIdx.x - M.wg0) * W + wave;
+    const int t0 = sk ? usk / C : ((int) blockIdx.x - M.wg0) * A.T;
+    const int t1 = sk ? M.tiles : min(t0 + A.T, M.tiles);
+    const int j = sk ? 0 : wave / C;               /* tile slot */
+    const int c = sk ? usk - t0 * C : wave - j * C;  /* K chunk */
     const int MP = A.M >> A.lgS;                   /* macro steps per part */
     const int MS = MSC > 0 ? MSC : MP / C;         /* macro steps per unit */
     const int r_in = m16 >> A.lgS, h = m16 & (S - 1);  /* A side: tile row, part */
@@ -175,7 +190,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * putting the parts that lanes read at once on different banks */
     const uint8_t * xb = lx + (bval ? cn : 0) * A.xstride + 264 * msb + 64 * q;
     const uint8_t * xbl = xb + ncol * A.xstride;
-    const int iters = (t1 - t0 + T - 1) / T;
+    const int iters = sk ? 1 : (t1 - t0 + T - 1) / T;
     const uint32_t stream_off = A.gain_off + (uint32_t) rows * 2u;
 
     /* the matrix's stage payloads, read once (uniform) */
@@ -693,8 +708,13 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         /* y[col][row] = sum over parts hh (and over the C chunk waves) of
-         * C[r*S + hh][hh*ncol + col], added in a fixed order */
-        if (active && c == 0) {
+         * C[r*S + hh][hh*ncol + col], added in a fixed order. With shared
+         * tiles the tile's first wave in this workgroup adds the nin chunk
+         * waves that follow it here; a tile split over two workgroups then
+         * meets the other half's sum through kslot. */
+        const int nin = sk ? min(C - c, W - wave) : C;
+        const bool split = sk && (c != 0 || nin < C);
+        if (active && (c == 0 || (sk && wave == 0))) {
             for (int e = lane; e < rpt * ncol; e += 64) {
                 const int r = ncol == 1 ? e : e / ncol, col = e - r * ncol;
                 const int row = tile * rpt + r;
@@ -714,13 +734,24 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                     for (int hh = 0; hh < S; hh++) {
                         const float * rr = red + wave * kRedStride + (r * S + hh) * 17 + hh * ncol + col;
                         float part = rr[0];
-                        for (int cw = 1; cw < C; cw++) part += rr[cw * kRedStride];
+                        for (int cw = 1; cw < nin; cw++) part += rr[cw * kRedStride];
                         sum += part;
                     }
                 }
                 if (row < rows) {
                     float * yp = M.y + (size_t) col * A.ldy + row;
-                    *yp = (A.accumulate ? *yp : 0.0f) + sum;
+                    bool last = true;
+                    if (split) {
+                        uint64_t * sl = A.kslot + (size_t) row * ncol + col;
+                        const uint64_t old = __hip_atomic_exchange(sl, (1ull << 32) | __float_as_uint(sum),
+                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        last = (uint32_t) (old >> 32) == 1u;
+                        if (last) {
+                            sum = __uint_as_float((uint32_t) old) + sum;
+                            __hip_atomic_store(sl, (uint64_t) 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    }
+                    if (last) *yp = (A.accumulate ? *yp : 0.0f) + sum;
                 }
             }
         }
@@ -917,6 +948,7 @@ struct FastShape {
     int S, C, T, W, nwg;
     size_t lds;
     int xg;   /* several columns with x read from global memory (no x in LDS) */
+    int sk;   /* shared tiles: W (tile, chunk) units per workgroup */
 };
 
 /* LDS bytes per activation column: 264 bytes per 128 columns (256 of f16
@@ -959,16 +991,50 @@ static int fast_shape_xg(const VqCall & c, int nst, FastShape & sh) {
                 if (best < 0 || cost < best) {
                     best = cost;
                     sh.S = s; sh.C = cc; sh.T = tt; sh.W = tt * cc; sh.nwg = (int) nwg; sh.lds = lds; sh.xg = 1;
+                    sh.sk = 0;
                 }
             }
         }
     }
-    return best < 0 ? -1 : 0;
+    if (best < 0) return -1;
+    /* Shared tiles, when the caller gave the slot words and whole tiles leave
+     * more than a fifth of the CUs idle (N = 8 over 2560 rows: 160 of 256
+     * busy): ten waves per workgroup, each one (tile, chunk) unit, a tile's
+     * chunks over at most two workgroups (W >= C), as many workgroups as
+     * fit one round; then the shortest unit. Units under 4 macro steps do
+     * not pay for their own staging (N = 8 over 4096 columns: 2-step units
+     * measured slower than whole tiles on 160 CUs). */
+    if (c.kslot && c.nmat == 1 && (long) c.mats[0].rows * c.ncol <= c.kslot_cap && 5 * sh.nwg < 4 * G) {
+        const int W = 10;
+        int bn = 0, bms = 0;
+        for (int s = 1; s <= 16; s *= 2) {
+            if (s * c.ncol > 16 || M % s) continue;
+            const int MP = M / s;
+            const long tiles = (c.mats[0].rows * (long) s + 15) / 16;
+            for (int cc = 2; cc <= W; cc++) {
+                if (MP % cc) continue;
+                const int ms = MP / cc;
+                if (ms != 4 && ms != 5 && ms != 8 && (ms != 10 || c.nc > 4096)) continue;
+                if (5 * 64 * W < n16) continue;
+                const long nwg = (tiles * cc + W - 1) / W;
+                const size_t lds = fast_lds(c, nst, s, W, 1);
+                if (nwg > G || lds > (size_t) kLdsMax) continue;
+                if (nwg > bn || (nwg == bn && ms < bms)) {
+                    bn = (int) nwg; bms = ms;
+                    if (bn > sh.nwg) {
+                        sh.S = s; sh.C = cc; sh.T = 1; sh.W = W; sh.nwg = bn; sh.lds = lds; sh.xg = 1; sh.sk = 1;
+                    }
+                }
+            }
+        }
+    }
+    return 0;
 }
 
 static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
     if (kFastXg && fast_shape_xg(c, nst, sh) == 0) return 0;
     sh.xg = 0;
+    sh.sk = 0;
     const int M = c.cols / 4 / 32;
     const int G = cu_count();
     const int want = G * 8;
@@ -1163,6 +1229,8 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     A.lgS = 0;
     while ((1 << A.lgS) < sh.S) A.lgS++;
     A.C = sh.C; A.T = sh.T;
+    A.sk = sh.sk;
+    A.kslot = sh.sk ? c.kslot : nullptr;
     A.M = mk;
     A.kofs = k0;
     A.xstride = sh.xg ? 0 : fast_xstride(part.cols, sh.S);
@@ -1173,7 +1241,7 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
         A.mat[m].rows = c.mats[m].rows;
         A.mat[m].tiles = (int) ((c.mats[m].rows * (long) sh.S + 15) / 16);
         A.mat[m].wg0 = wg;
-        A.mat[m].nwg = (A.mat[m].tiles + sh.T - 1) / sh.T;
+        A.mat[m].nwg = sh.sk ? (A.mat[m].tiles * sh.C + sh.W - 1) / sh.W : (A.mat[m].tiles + sh.T - 1) / sh.T;
         wg += A.mat[m].nwg;
     }
     const int threads = sh.W * 64;
