@@ -376,6 +376,20 @@ def bench_decode_chain(args, sm, torch, dev):
         chain_ms = c0.elapsed_time(c1) / args.steps
     log(f"  decode chain: {ms * 1e3:.1f} us/token ({chain_ms * 1e3:.1f} us for the chain launch), "
         f"{nbytes / (ms * 1e-3) / 1e9:.0f} GB/s of weights")
+    phases = None
+    if args.chain_trace:
+        buf = dc.chain.trace(True, device=dev)
+        with torch.cuda.stream(stream):
+            dc.chain.launch(stream)
+        torch.cuda.synchronize()
+        dc.chain.status()
+        dc.chain.trace(False)
+        tr = buf.cpu().numpy()
+        if args.chain_trace_out:
+            np.save(args.chain_trace_out, tr)
+        phases = chain_phases(tr, dc.chain.labels)
+        for k, v in phases.items():
+            log(f"  phases {k}: " + ", ".join(f"{a} {b}" for a, b in v.items()))
     out = {"metric": "decode matvec us/token, dependent chain (36-layer trunk as one persistent launch + Q8_0 head)",
            "value": round(ms * 1e3, 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
@@ -385,7 +399,7 @@ def bench_decode_chain(args, sm, torch, dev):
                                   "then the Q8_0 head", "layers": LAYERS, "hidden": HIDDEN, "ffn": FFN,
                       "head": f"Q8_0 {args.head_rows}x{HIDDEN}", "waves": args.chain_waves,
                       "look": args.chain_look, "min_units": args.chain_units},
-           "chain_launch_us": round(chain_ms * 1e3, 2), "weight_bytes": int(nbytes),
+           "chain_launch_us": round(chain_ms * 1e3, 2), "weight_bytes": int(nbytes), "phases_us": phases,
            "achieved_gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
            "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4)}
     if args.check:
@@ -397,6 +411,45 @@ def bench_decode_chain(args, sm, torch, dev):
         out["check"] = {"rel_l2_max": cc.worst_matvec(res), "detail": res, "layers": list(kept),
                         "method": "each op of the timed chain vs the oracle from the inputs the GPU read; every "
                                   "head row"}
+    return out
+
+
+def chain_phases(tr, labels):
+    """Per op kind (the label after the layer prefix), medians over the
+    layers of the median workgroup's phases: req (op start to x requested),
+    spin (x requested to x arrived everywhere), stage (to x staged), enter
+    (to the step loop's start), loop (wave 0's steps), tail (to every unit
+    done), epi (to the stores issued); handoff (the op before's last
+    workgroup's stores to this op's median x arrival) and span (last stores
+    of the op before to last stores of this one). tr: [workgroups, ops, 8]
+    clock ticks of 10 ns, then the shader clock at each op's start and end
+    (their ratio to the 100 MHz clock gives the shader clock's rate)."""
+    clk = tr[:, :, 8:].astype(np.int64)
+    t = tr[:, :, :8].astype(np.int64)
+    t = (t - t[0, 0, 0] + (1 << 31)) % (1 << 32) - (1 << 31)   # signed ticks from workgroup 0's start
+    t = t * 0.01   # us
+    dt = t[:, :, 6] - t[:, :, 0]
+    ok = dt > 0.5
+    ghz = float(np.median(((clk[:, :, 1] - clk[:, :, 0]) % (1 << 32))[ok] / (dt[ok] * 1e3)))
+    kinds = {}
+    for i, lab in enumerate(labels):
+        kinds.setdefault(lab.split(":", 1)[-1], []).append(i)
+    names = ("req", "spin", "stage", "enter", "loop", "tail", "epi", "handoff", "span")
+    out = {}
+    for k, idx in kinds.items():
+        rows = []
+        for i in idx:
+            if i == 0:
+                continue
+            a = t[:, i]
+            last_prev = t[:, i - 1, 6].max()
+            md = lambda u, v: np.median(a[:, v] - a[:, u])  # noqa: E731
+            rows.append([md(0, 7), md(7, 1), md(1, 2), md(2, 3), md(3, 4), md(4, 5), md(5, 6),
+                         np.median(a[:, 1]) - last_prev, a[:, 6].max() - last_prev])
+        if rows:
+            m = np.median(np.array(rows), axis=0)
+            out[k] = {n: round(float(v), 2) for n, v in zip(names, m)}
+    out["shader_clock_ghz"] = {"median": round(ghz, 3)}
     return out
 
 
@@ -749,9 +802,12 @@ def main():
     ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--chain-waves", type=int, default=16, help="decode-chain: waves per workgroup")
+    ap.add_argument("--chain-waves", type=int, default=12, help="decode-chain: waves per workgroup")
     ap.add_argument("--chain-look", type=int, default=2, help="decode-chain: index steps in flight per wave")
-    ap.add_argument("--chain-units", type=int, default=16, help="decode-chain: units per workgroup aimed for")
+    ap.add_argument("--chain-units", type=int, default=0,
+                    help="decode-chain: units per workgroup aimed for (0: the chain's cost model)")
+    ap.add_argument("--chain-trace", action="store_true", help="decode-chain: one more launch with a phase trace")
+    ap.add_argument("--chain-trace-out", default=None, metavar="NPY", help="decode-chain: also save the raw trace")
     ap.add_argument("--no-check", dest="check", action="store_false",
                     help="skip the oracle check of the timed outputs")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",

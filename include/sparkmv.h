@@ -299,8 +299,9 @@ void * sparkmv_chain_create(void);
 void sparkmv_chain_destroy(void * chain);
 int sparkmv_chain_size(void * chain);
 /* Waves per workgroup (8, 12 or 16), macro steps of index words each wave
- * keeps in flight (2 or 4), and the units per workgroup the shape search
- * aims for; applies at the next launch. */
+ * keeps in flight (2 or 4; 8 with 8 waves), and the units per workgroup the
+ * shape search aims for (0: fewest rounds of units per wave); applies at
+ * the next launch. */
 int sparkmv_chain_tune(void * chain, int waves, int look, int min_units);
 int sparkmv_chain_add_vq(void * chain, const sparkmv_chain_matrix * mats, int nmat, int nstages, int dim, int nc,
                          int cols, int v3, const void * x, int x_mode, const float * norm_w, float eps,
@@ -312,6 +313,14 @@ int sparkmv_chain_launch(void * chain, void * stream);
 /* 0, or -1 if a wait of any launch so far gave up (flags are then cleared);
  * synchronizes the device. */
 int sparkmv_chain_status(void * chain);
+/* Phase trace of later launches into buf (device memory, NULL = off): per
+ * workgroup w and op i, buf[(w * ops + i) * 10 + k] holds the 100 MHz clock
+ * (low 32 bits) at the op's start, x arrived, x staged, step loop entered,
+ * wave 0's steps done, every unit done, epilogue issued and x requested,
+ * then the shader clock at the op's start and end. Returns the words needed
+ * (workgroups * ops * 10), or -1 when words is too small. No counterpart in
+ * the reference: a diagnostic of this chain. */
+int sparkmv_chain_trace(void * chain, uint32_t * buf, long words);
 /* The shape chosen for op i: MFMA parts S, K chunks C, macro steps per unit. */
 int sparkmv_chain_op_shape(void * chain, int i, int * S, int * C, int * msc);
 

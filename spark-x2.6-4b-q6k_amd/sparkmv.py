@@ -147,6 +147,7 @@ SIGNATURES = {
     "sparkmv_chain_launch": (_I, [_P, _P]),
     "sparkmv_chain_status": (_I, [_P]),
     "sparkmv_chain_op_shape": (_I, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
+    "sparkmv_chain_trace": (_I, [_P, _P, ctypes.c_long]),
     "sparkmv_gguf_open": (_P, [ctypes.c_char_p]),
     "sparkmv_gguf_close": (None, [_P]),
     "sparkmv_gguf_version": (_I, [_P]),
@@ -1019,7 +1020,7 @@ class Chain:
     def __len__(self):
         return lib().sparkmv_chain_size(self.h)
 
-    def tune(self, waves=16, look=2, min_units=16):
+    def tune(self, waves=12, look=2, min_units=0):
         check(lib().sparkmv_chain_tune(self.h, waves, look, min_units), "chain tune")
 
     def add_vq(self, mats, x, x_mode, ys=None, ys_bf16=None, y_add=None, norm_w=None, eps=1e-6, x_out=None,
@@ -1057,6 +1058,29 @@ class Chain:
 
     def status(self):
         check(lib().sparkmv_chain_status(self.h), "chain")
+
+    def trace(self, on=True, device="cuda"):
+        """Record a phase trace in every later launch (on=False stops it).
+        Returns the int32 device tensor [workgroups, ops, 10] that each launch
+        overwrites: the 100 MHz clock (low 32 bits) at each op's start, x
+        arrived, x staged, step loop entered, wave 0's steps done, every unit
+        done, epilogue issued and x requested, then the shader clock at the
+        op's start and end."""
+        torch = _torch()
+        if not on:
+            if lib().sparkmv_chain_trace(self.h, None, 0) < 0:
+                check(-1, "chain trace")
+            self.trace_buf = None
+            return None
+        need = lib().sparkmv_chain_trace(self.h, None, 0)
+        if need < 0:
+            check(need, "chain trace")
+        n = len(self)
+        buf = torch.zeros(need // (10 * n), n, 10, dtype=torch.int32, device=device)
+        if lib().sparkmv_chain_trace(self.h, ctypes.c_void_p(buf.data_ptr()), need) < 0:
+            check(-1, "chain trace")
+        self.trace_buf = buf
+        return buf
 
     def op_shape(self, i):
         S, C, msc = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()

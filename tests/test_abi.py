@@ -224,7 +224,10 @@ def test_chain_refusals(sm):
             assert msg in sm.last_error(), (msg, sm.last_error())
         assert add(mats(1), 1) == 0 and sm.lib().sparkmv_chain_size(h) == 1
         assert sm.lib().sparkmv_chain_tune(h, 10, 2, 16) == -1 and "8, 12 or 16" in sm.last_error()
-        assert sm.lib().sparkmv_chain_tune(h, 16, 3, 16) == -1 and "2 or 4" in sm.last_error()
+        assert sm.lib().sparkmv_chain_tune(h, 16, 3, 16) == -1 and "2, 4 or 8" in sm.last_error()
+        assert sm.lib().sparkmv_chain_tune(h, 16, 8, 16) == -1 and "8 waves" in sm.last_error()
+        assert sm.lib().sparkmv_chain_tune(h, 12, 4, -1) == -1 and "0..1024" in sm.last_error()
         assert sm.lib().sparkmv_chain_tune(h, 12, 4, 24) == 0
+        assert sm.lib().sparkmv_chain_tune(h, 8, 8, 0) == 0
     finally:
         sm.lib().sparkmv_chain_destroy(h)
