@@ -150,10 +150,12 @@ def bench_decode_set_q6k(args, sm, torch, dev):
     stream = torch.cuda.Stream(device=dev)
     t0 = time.time()
     with torch.cuda.stream(stream):
-        xs = {c: torch.from_numpy(sm.synth_bf16(c, c).view(np.int16).reshape(1, c).copy()).to(dev)
-              for c in (HIDDEN, QD, FFN)}
+        xb = {c: sm.synth_bf16(c, c) for c in (HIDDEN, QD, FFN)}
+        xs = {c: torch.from_numpy(xb[c].view(np.int16).reshape(1, c).copy()).to(dev) for c in (HIDDEN, QD, FFN)}
         plan = sm.Plan()
         op_bytes = []
+        kept = (0, LAYERS // 2, LAYERS - 1)
+        groups = []   # kept layers' (key, host blocks, rows, cols, y) for the output check
         with concurrent.futures.ThreadPoolExecutor(min(16, os.cpu_count() or 4)) as ex:
             futs = [[ex.submit(sm.synth_q6k, seed_of(l, i), r, c) for i, (_, r, c, _) in enumerate(LAYER_MATS)]
                     for l in range(LAYERS)]
@@ -170,9 +172,11 @@ def bench_decode_set_q6k(args, sm, torch, dev):
                     blocks = np.concatenate([futs[l][i].result() for i in idx])
                     d = torch.from_numpy(blocks).to(dev)
                     y = torch.zeros(r, device=dev)
-                    plan.add_kquant("q6_k", d, r, c, xs[c], y,
-                                    label=f"L{l}:" + "+".join(LAYER_MATS[i][0] for i in idx))
+                    key = "+".join(LAYER_MATS[i][0] for i in idx)
+                    plan.add_kquant("q6_k", d, r, c, xs[c], y, label=f"L{l}:" + key)
                     plan.keep.append((d, y))
+                    if l in kept:
+                        groups.append((key, blocks, r, c, y))
                     op_bytes.append(blocks.nbytes + 2 * c + 4 * r)
                 futs[l] = None
         hb = torch.from_numpy(head).to(dev)
@@ -190,6 +194,16 @@ def bench_decode_set_q6k(args, sm, torch, dev):
     log(f"  step {ms * 1e3:.1f} us ({args.mode}); Q6_K kernels {trunk_ms * 1e3:.1f} us over {len(op_ms) - 1} launches "
         f"({trunk_b / (trunk_ms * 1e-3) / 1e9:.1f} GB/s); head {op_ms[-1] * 1e3:.1f} us")
     achieved = trunk_b / (trunk_ms * 1e-3) / 1e9
+    check = None
+    if args.check:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import chain_check as cc
+        t = time.time()
+        res = cc.check_kquant_set(groups, {c: sm.bf16_to_f32(v) for c, v in xb.items()}, head, args.head_rows, logits)
+        log(f"  output check ({time.time() - t:.1f} s): {res}")
+        check = {"rel_l2_max": max(res.values()), "detail": res, "layers": list(kept),
+                 "method": "every row of the kept layers' launches vs the oracle's Q6_K dequant times x in f64; "
+                           "every head row vs the closed-form Q8_0 dot"}
     return {
         "metric": "decode matvec us/token (36-layer Q6_K trunk, N=1, tied Q8_0 head)",
         "value": round(ms * 1e3, 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -202,6 +216,7 @@ def bench_decode_set_q6k(args, sm, torch, dev):
         "algorithmic_bytes_per_step": int(total),
         "roofline": {"bound": "hbm", "kernel": "q6k_gemv_staged_kernel", "achieved": round(achieved, 1),
                      "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4), "traffic": None},
+        "check": check,
     }
 
 

@@ -140,3 +140,21 @@ def check_decode_set(ds, layer_mats, layers):
         worst = max(worst, rel_l2(got[n], want))
     res["head"] = worst
     return res
+
+
+def check_kquant_set(groups, xs, head_blocks, head_rows, logits):
+    """The Q6_K decode set's outputs (bench.py --workload decode-set-q6k):
+    groups is a list of (key, Q6_K blocks of the stacked rows, rows, cols, y
+    tensor); each y against the oracle's closed-form Q6_K dequant (ggml
+    layout, 210 B per 256 weights) times x in f64, and every head row
+    against the closed-form Q8_0 dot. xs[cols] is the f32 value of the bf16
+    x each launch read. Returns the largest relative L2 error per key and
+    for the head."""
+    res = {}
+    for key, blocks, rows, cols, y in groups:
+        W = ref.q6k_dequant(blocks, rows, cols)
+        want = ref.matvec_f64(W, np.asarray(xs[cols], F32))
+        res[key] = max(res.get(key, 0.0), rel_l2(_f32(y)[:rows], want))
+    x = np.asarray(xs[head_blocks.size // (head_rows * 34) * 32], F32)
+    res["head"] = rel_l2(_f32(logits), ref.q8_0_matvec(np.asarray(head_blocks), head_rows, x.size, x))
+    return res

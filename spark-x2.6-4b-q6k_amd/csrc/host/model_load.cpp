@@ -430,10 +430,14 @@ static void * model_load(const char * dir, const char * config_path, int max_ctx
         w.full = full[(size_t) i];
         if (sparkmv_model_set_layer(L.model, i, &w)) { err = vqg_decode_error(); return nullptr; }
     }
-    /* the model frees the weights from here on */
-    for (void * d : L.pending)
-        if (model_adopt(L.model, d)) { err = vqg_decode_error(); return nullptr; }
-    L.pending.clear();
+    /* the model frees the weights from here on: each buffer leaves the
+     * loader's list as soon as the model holds it, so a failure (or an
+     * allocation failure thrown by the handoff) part way frees each buffer
+     * exactly once, by whichever side holds it */
+    while (!L.pending.empty()) {
+        if (model_adopt(L.model, L.pending.back())) { err = vqg_decode_error(); return nullptr; }
+        L.pending.pop_back();
+    }
 
     /* The profile never fails a load (vq-model-gpu.cu:1097-1120): one that
      * is absent, not version 1, for another artifact or device, or that

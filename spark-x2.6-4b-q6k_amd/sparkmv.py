@@ -275,7 +275,8 @@ class Gguf:
     bytes come back as copies, so they outlive the handle."""
 
     def __init__(self, path):
-        self.h = lib().sparkmv_gguf_open(os.fsencode(path))
+        self._L = lib()   # kept for __del__, which must not use module globals at interpreter exit
+        self.h = self._L.sparkmv_gguf_open(os.fsencode(path))
         if not self.h:
             raise SparkmvError(f"gguf open: {last_error()}")
         self.version = lib().sparkmv_gguf_version(self.h)
@@ -292,7 +293,14 @@ class Gguf:
         self.close()
 
     def __del__(self):
-        self.close()
+        # only attributes of self: at interpreter exit the module's globals may be gone
+        L = getattr(self, "_L", None)
+        if getattr(self, "h", None) and L is not None:
+            try:
+                L.sparkmv_gguf_close(self.h)
+            except Exception:
+                pass
+            self.h = None
 
     def tensors(self):
         """[{name, dims (fastest first), dtype, offset, nbytes}] in file order;
@@ -368,7 +376,8 @@ class VqDir:
     norm sidecar as an f32 array [rows, cols]."""
 
     def __init__(self, path):
-        self.h = lib().sparkmv_manifest_open(os.fsencode(path))
+        self._L = lib()
+        self.h = self._L.sparkmv_manifest_open(os.fsencode(path))
         if not self.h:
             raise SparkmvError(f"manifest open: {last_error()}")
 
@@ -378,7 +387,14 @@ class VqDir:
             self.h = None
 
     def __del__(self):
-        self.close()
+        # only attributes of self: at interpreter exit the module's globals may be gone
+        L = getattr(self, "_L", None)
+        if getattr(self, "h", None) and L is not None:
+            try:
+                L.sparkmv_manifest_close(self.h)
+            except Exception:
+                pass
+            self.h = None
 
     def entries(self):
         out = []
@@ -592,7 +608,8 @@ class Model:
     def __init__(self, cfg, layers, head, final_norm):
         c = ModelCfg(**cfg)
         self.cfg = dict(cfg)
-        self.h = lib().sparkmv_model_create(ctypes.byref(c))
+        self._L = lib()
+        self.h = self._L.sparkmv_model_create(ctypes.byref(c))
         if not self.h:
             raise SparkmvError("model create: " + last_error())
         self.keep = [layers, head, final_norm]
@@ -620,7 +637,8 @@ class Model:
         the weights it uploaded. profile_note says what became of
         DIR/vq-tune.profile (a bad or foreign profile keeps the heuristic)."""
         self = cls.__new__(cls)
-        self.h = lib().sparkmv_model_load(os.fsencode(str(directory)), os.fsencode(str(config_path)), int(max_ctx),
+        self._L = lib()
+        self.h = self._L.sparkmv_model_load(os.fsencode(str(directory)), os.fsencode(str(config_path)), int(max_ctx),
                                           int(x_dtype), int(bool(apply_profile)))
         if not self.h:
             raise SparkmvError("model load: " + last_error())
@@ -631,8 +649,13 @@ class Model:
         return self
 
     def __del__(self):
-        if getattr(self, "h", None):
-            lib().sparkmv_model_destroy(self.h)
+        # only attributes of self: at interpreter exit the module's globals may be gone
+        L = getattr(self, "_L", None)
+        if getattr(self, "h", None) and L is not None:
+            try:
+                L.sparkmv_model_destroy(self.h)
+            except Exception:
+                pass
             self.h = None
 
     def forward(self, token, pos, logits, stream=None):
@@ -758,13 +781,19 @@ class Profile:
     geometry, trusted only for the artifact and device that measured it."""
 
     def __init__(self, path):
-        self.h = lib().sparkmv_profile_load(os.fsencode(path))
+        self._L = lib()
+        self.h = self._L.sparkmv_profile_load(os.fsencode(path))
         if not self.h:
             raise SparkmvError("profile load: " + last_error())
 
     def __del__(self):
-        if getattr(self, "h", None):
-            lib().sparkmv_profile_close(self.h)
+        # only attributes of self: at interpreter exit the module's globals may be gone
+        L = getattr(self, "_L", None)
+        if getattr(self, "h", None) and L is not None:
+            try:
+                L.sparkmv_profile_close(self.h)
+            except Exception:
+                pass
             self.h = None
 
     def trusted(self, artifact, gpu):
@@ -931,13 +960,19 @@ class Plan:
     replayed as one HIP graph. Holds references to every tensor it uses."""
 
     def __init__(self):
-        self.h = lib().sparkmv_plan_create()
+        self._L = lib()
+        self.h = self._L.sparkmv_plan_create()
         self.keep = []
         self.labels = []
 
     def __del__(self):
-        if getattr(self, "h", None):
-            lib().sparkmv_plan_destroy(self.h)
+        # only attributes of self: at interpreter exit the module's globals may be gone
+        L = getattr(self, "_L", None)
+        if getattr(self, "h", None) and L is not None:
+            try:
+                L.sparkmv_plan_destroy(self.h)
+            except Exception:
+                pass
             self.h = None
 
     def __len__(self):
@@ -1008,13 +1043,19 @@ class Chain:
     before it; holds references to every tensor it uses."""
 
     def __init__(self):
-        self.h = lib().sparkmv_chain_create()
+        self._L = lib()
+        self.h = self._L.sparkmv_chain_create()
         self.keep = []
         self.labels = []
 
     def __del__(self):
-        if getattr(self, "h", None):
-            lib().sparkmv_chain_destroy(self.h)
+        # only attributes of self: at interpreter exit the module's globals may be gone
+        L = getattr(self, "_L", None)
+        if getattr(self, "h", None) and L is not None:
+            try:
+                L.sparkmv_chain_destroy(self.h)
+            except Exception:
+                pass
             self.h = None
 
     def __len__(self):

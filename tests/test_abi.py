@@ -231,3 +231,16 @@ def test_chain_refusals(sm):
         assert sm.lib().sparkmv_chain_tune(h, 8, 8, 0) == 0
     finally:
         sm.lib().sparkmv_chain_destroy(h)
+
+
+def test_handles_are_released_at_interpreter_exit(sm):
+    """Objects still alive when the interpreter exits are destroyed without
+    an error: their destructors use only the library they captured, not
+    module globals that teardown may already have cleared."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, %r); import sparkmv as sm\n"
+            "keep = [sm.Plan(), sm.Chain(), sm.Plan()]\n" % os.path.dirname(sm.__file__))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "Exception ignored" not in r.stderr and "Error" not in r.stderr, r.stderr

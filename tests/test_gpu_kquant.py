@@ -23,7 +23,9 @@ def _dequant_ref(ref, kind, blocks, rows, cols):
     return ref.q6k_dequant(blocks, rows, cols) if kind == "q6_k" else ref.q8_0_dequant(blocks, rows, cols)
 
 
-SHAPES = {"q6_k": [(2560, 10240), (13, 512), (4, 256), (64, 2560)],
+# q6_k also at the Q6_K trunk's launch shapes: q + k + v + head gate stacked by
+# rows (6160 x 2560), gate + up stacked (20480 x 2560) and o (2560 x 4096)
+SHAPES = {"q6_k": [(2560, 10240), (13, 512), (4, 256), (64, 2560), (6160, 2560), (20480, 2560), (2560, 4096)],
           "q8_0": [(1024, 2560), (3, 32), (5, 96), (64, 2560), (7, 4096)]}
 
 

@@ -250,3 +250,46 @@ def test_live_reference_decoder(ref, sm, tmp_path):
     subprocess.run([ref.REF_DECODE, "dump", str(src), str(out)], check=True, stdout=subprocess.DEVNULL)
     want = np.fromfile(out, np.float32).reshape(21, 192)
     assert np.array_equal(ref.decode(data).view(np.uint32), want.view(np.uint32))
+
+
+def _torch_bf16_bits(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16).view(torch.int16).numpy() \
+        .view(np.uint16)
+
+
+def test_bf16_bits_matches_torch_rounding():
+    """The oracle's f32 -> bf16 rounding (chain_check.bf16_bits: round to
+    nearest, ties to even; NaN stays NaN) against torch's conversion, which
+    rounds the same way. Covers random values over the whole exponent range,
+    exact ties with an even and with an odd kept bit (both signs), values one
+    ulp either side of a tie, subnormals, the largest finite values (which
+    round to infinity), zeros and infinities, bit for bit; NaN inputs give
+    NaN in both. A mistake in the tie rule, the carry into the exponent or
+    the sign fails here."""
+    import chain_check as cc
+    rng = np.random.default_rng(0xBF16)
+    u = rng.integers(0, 1 << 32, 200000, dtype=np.uint64).astype(np.uint32)
+    finite = u[(u & 0x7F800000) != 0x7F800000]
+    hi = rng.integers(0, 1 << 16, 4096, dtype=np.uint64).astype(np.uint32) << 16
+    hi = hi[(hi & 0x7F800000) != 0x7F800000]
+    ties = np.concatenate([hi | 0x8000, hi | 0x7FFF, hi | 0x8001])            # tie, just below, just above
+    sub = np.concatenate([np.arange(1, 1 << 12, dtype=np.uint32), np.uint32(0x007FFFFF) - np.arange(4096, dtype=np.uint32),
+                          np.uint32(0x00008000) + np.arange(-3, 4, dtype=np.int64).astype(np.uint32)])
+    edge = np.array([0x00000000, 0x80000000, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0x7F7F7FFF, 0x7F800000, 0xFF800000,
+                     0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000, 0x00008000, 0x00018000], dtype=np.uint32)
+    vals = np.concatenate([finite, ties, sub, sub | 0x80000000, edge]).view(np.float32)
+    got = cc.bf16_bits(vals)
+    want = _torch_bf16_bits(vals)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, [(hex(int(vals.view(np.uint32)[i])), hex(int(got[i])), hex(int(want[i]))) for i in bad[:8]]
+    # ties go to the even neighbour: 1 + 2^-8 (kept bit even) stays 1, 1 + 3 * 2^-8 (odd) rounds up
+    assert cc.bf16_bits(np.float32([1 + 2 ** -8, 1 + 3 * 2 ** -8])).tolist() == [0x3F80, 0x3F82]
+    # the largest finite f32 rounds up to infinity, as torch's does
+    assert int(cc.bf16_bits(np.float32([3.4028235e38]))[0]) == 0x7F80
+    nans = np.array([0x7FC00000, 0xFFC00000, 0x7F800001, 0x7FFFFFFF, 0xFF800001], dtype=np.uint32).view(np.float32)
+    nb = cc.bf16_bits(nans)
+    assert np.all((nb & 0x7F80) == 0x7F80) and np.all((nb & 0x7F) != 0), [hex(int(v)) for v in nb]
+    assert int(nb[0]) == 0x7FC0
+    tn = _torch_bf16_bits(nans)   # torch's NaN bits differ by path (0x7FC0 or 0xFFFF): NaN either way
+    assert np.all((tn & 0x7F80) == 0x7F80) and np.all((tn & 0x7F) != 0)
