@@ -513,7 +513,9 @@ def bench_forward(args, sm, torch, dev):
     toks = np.random.default_rng(6).integers(0, args.head_rows, size=max_ctx)
     ev = lambda: torch.cuda.Event(enable_timing=True)
     if prompt:
-        return bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch)
+        hd = torch.from_numpy(head).to(dev)
+        make_f32 = lambda: sm.Model(dict(cfg, x_dtype=sm.X_F32), layers, hd, norm)  # noqa: E731  same weights
+        return bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch, make_f32)
     with torch.cuda.stream(stream):
         t0 = time.time()
         for p in range(P):
@@ -603,7 +605,7 @@ def bench_forward(args, sm, torch, dev):
     }
 
 
-def bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch):
+def bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch, make_f32=None):
     """prompt512: one 512-token prompt chunk through the whole model
     (sparkmv_model_forward_batch, the reference's forward_batch + tail_logits,
     vq-model-gpu.cu:858-953, over the 512-token chunks of :1161-1173): every
@@ -627,6 +629,46 @@ def bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch):
         torch.cuda.synchronize()
     ms = a.elapsed_time(b) / args.steps
     assert bool(torch.isfinite(logits).all()), "non-finite logits"
+    check = None
+    if args.check:
+        # The same 512 tokens one decode step at a time (the decode path,
+        # which the tests hold to the oracle), with bf16 activations as the
+        # chunk has and, on a second model over the same weights, with f32
+        # ones. The f32/bf16 gap is what bf16 activations alone move the
+        # logits by at this depth; the chunk (f16 x and folded stages in its
+        # GEMMs, besides bf16 activations) is held to twice that gap.
+        prompt_logits = logits.clone()
+        t = time.time()
+
+        def decode_logits(m):
+            out = torch.empty_like(logits)
+            m.rollback(0)
+            with torch.cuda.stream(stream):
+                for p, tok in enumerate(chunk):
+                    m.forward(tok, p, out, stream)
+            torch.cuda.synchronize()
+            m.rollback(0)
+            return out.double()
+
+        def rl2(a, b):
+            return float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+
+        dec16 = decode_logits(model)
+        m32 = make_f32()
+        m32.reserve(N)
+        dec32 = decode_logits(m32)
+        del m32
+        g = prompt_logits.double()
+        err, gap, err32 = rl2(g, dec16), rl2(dec16, dec32), rl2(g, dec32)
+        agree = int(torch.argmax(g)) == int(torch.argmax(dec16)) == int(torch.argmax(dec32))
+        log(f"  check ({time.time() - t:.1f} s): last logits vs 512 bf16 decode steps relL2 {err:.2e} "
+            f"(vs f32 decode steps {err32:.2e}; f32 vs bf16 decode {gap:.2e}), argmax agrees {agree}")
+        check = {"rel_l2_vs_bf16_decode": err, "rel_l2_vs_f32_decode": err32, "f32_vs_bf16_decode": gap,
+                 "argmax_agrees": agree,
+                 "method": "the chunk's last logits vs the same 512 tokens one decode step at a time "
+                           "(sparkmv_model_forward, which the tests hold to the oracle), bf16 activations; bar: "
+                           "twice the gap between the decode path's f32 and bf16 activations, argmax equal"}
+        assert err <= 2 * max(gap, 1e-3) and agree, f"prompt chunk vs the decode path: {check}"
     # matvec work: 2 flop per weight and token over the trunk, the head for one token
     weights = LAYERS * ((QD + 2 * KVD + NHEAD) * HIDDEN + HIDDEN * QD + 3 * FFN * HIDDEN)
     flop = 2.0 * weights * N + 2.0 * args.head_rows * HIDDEN
@@ -644,6 +686,7 @@ def bench_prompt(args, model, stream, logits, toks, mat_bytes, head, ev, torch):
         "tokens_per_s": round(N / (ms * 1e-3), 1),
         "matvec_tflops": round(flop / (ms * 1e-3) / 1e12, 1),
         "weight_bytes": int(mat_bytes + head.nbytes),
+        "check": check,
     }
 
 

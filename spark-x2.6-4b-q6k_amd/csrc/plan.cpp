@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <utility>
 #include <vector>
 
 #include "../../include/sparkmv.h"
@@ -34,9 +35,23 @@ struct PlanOp {
 struct Plan {
     std::vector<PlanOp> ops;
     std::vector<void *> slots;   /* each several-column op's shared-tile words */
+    std::vector<std::pair<void *, size_t>> unzeroed;   /* slot words not yet cleared (pointer, bytes) */
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
+
+/* Clear the slot words added since the last run, in stream order ahead of
+ * the ops that use them (outside any capture). Returns the number cleared. */
+static int zero_slots(Plan * p, hipStream_t s, int * cleared) {
+    *cleared = 0;
+    for (auto & q : p->unzeroed) {
+        hipError_t e = hipMemsetAsync(q.first, 0, q.second, s);
+        if (e != hipSuccess) return fail_hip("plan shared-tile words", e);
+        (*cleared)++;
+    }
+    p->unzeroed.clear();
+    return 0;
+}
 
 static int run_op(PlanOp & op, hipStream_t s) {
     if (op.kind == 0) {
@@ -98,19 +113,15 @@ int sparkmv_plan_add_vq(void * plan, const sparkmv_vq_matrix * mats, int nmat, i
     c.accumulate = accumulate ? 1 : 0;
     c.variant = variant;
     if (nmat == 1 && ncols > 1 && mats[0].rows > 0) {
-        /* zeroed words for workgroups that share a tile (the kernel leaves
-         * them zero); allocated here, so running the plan allocates nothing */
+        /* words for workgroups that share a tile (the kernel leaves them
+         * zero): allocated here, so running the plan allocates nothing, and
+         * cleared on the stream of the plan's next run or capture */
         const size_t n = (size_t) mats[0].rows * ncols;
         void * q = nullptr;
         hipError_t e = hipMalloc(&q, n * sizeof(uint64_t));
-        if (e == hipSuccess) e = hipMemset(q, 0, n * sizeof(uint64_t));
-        /* the zeros land before any stream's first launch of the plan */
-        if (e == hipSuccess) e = hipDeviceSynchronize();
-        if (e != hipSuccess) {
-            if (q) hipFree(q);
-            return fail_hip("plan shared-tile words", e);
-        }
+        if (e != hipSuccess) return fail_hip("plan shared-tile words", e);
         p->slots.push_back(q);
+        p->unzeroed.push_back({q, n * sizeof(uint64_t)});
         c.kslot = (uint64_t *) q;
         c.kslot_cap = (long) n;
     }
@@ -140,6 +151,8 @@ int sparkmv_plan_add_kquant(void * plan, int kind, const void * blocks, int rows
 int sparkmv_plan_run(void * plan, void * stream) {
     Plan * p = (Plan *) plan;
     if (!p) { set_error("plan is null"); return -1; }
+    int cleared = 0;
+    if (zero_slots(p, (hipStream_t) stream, &cleared)) return -1;
     for (size_t i = 0; i < p->ops.size(); i++)
         if (run_op(p->ops[i], (hipStream_t) stream)) return -1;
     return 0;
@@ -153,6 +166,14 @@ int sparkmv_plan_capture(void * plan, void * stream) {
     if (!stream) { set_error("a graph is captured on a created stream, not the null stream"); return -1; }
     hipStream_t s = (hipStream_t) stream;
     drop_graph(p);
+    /* slot words are cleared before the capture (no memset node in the
+     * graph), and waited for once, since the graph may replay on any stream */
+    int cleared = 0;
+    if (zero_slots(p, s, &cleared)) return -1;
+    if (cleared) {
+        hipError_t e0 = hipStreamSynchronize(s);
+        if (e0 != hipSuccess) return fail_hip("plan shared-tile words", e0);
+    }
     hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) return fail_hip("begin capture", e);
     int rc = 0;
@@ -248,7 +269,8 @@ int sparkmv_plan_time_ops(void * plan, void * stream, int iters, double * op_ms)
         }
     }
     for (size_t i = 0; i < n; i++) op_ms[i] = 0.0;
-    int rc = 0;
+    int cleared = 0;
+    int rc = zero_slots(p, s, &cleared);
     for (int it = 0; it < iters && !rc; it++) {
         for (size_t i = 0; i < n && !rc; i++) {
             g_launch_events.start = ev[2 * i];

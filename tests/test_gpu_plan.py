@@ -112,3 +112,58 @@ def test_plan_errors_and_empty_plan(sm, dev):
     assert "kind" in sm.last_error()
     assert L.sparkmv_plan_capture(plan.h, None) == -1
     assert "null stream" in sm.last_error()
+
+
+@pytest.mark.parametrize("rows", [2560, 2200, 2222])
+@pytest.mark.parametrize("acc", [False, True], ids=["overwrite", "accumulate"])
+def test_plan_shared_tiles_repeat_exactly(sm, ref, dev, rows, acc):
+    """Eight columns over 10240 columns with x read from global memory: a
+    single matrix whose whole tiles would leave most CUs idle takes shared
+    tiles in a plan (two workgroups meet through the plan's zeroed words).
+    Row counts of 2560 (the verify set's down), 2200 and 2222 (a ragged last
+    tile) put (tile, chunk) units over the workgroups so that some tiles
+    straddle two of them; below about 2048 rows the search keeps whole
+    tiles. Three runs from the same start
+    (eager, then a captured graph replayed twice) give identical bits, the
+    words returning to zero each time; each matches the oracle's decode
+    times x in f64, plus y0 when accumulating; and the same op launched
+    without a plan (no words: whole tiles only) agrees to within the f32
+    sums' reordering."""
+    import torch
+    cols, N = 10240, 8
+    h = sm.synth_container(0x5100 + rows, rows, cols)
+    M = sm.DeviceContainer(h, dev)
+    xb = sm.synth_bf16(0x5101, N * cols).reshape(N, cols)
+    xf = sm.bf16_to_f32(xb).reshape(N, cols).astype(np.float64)
+    x = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+    y0 = np.random.default_rng(rows).standard_normal((N, rows)).astype(np.float32)
+    y0t = torch.from_numpy(y0).to(dev)
+    y = y0t.clone()
+    plan = sm.Plan()
+    plan.add_vq([M], x, [y], ncols=N, accumulate=acc)
+    stream = torch.cuda.Stream(device=dev)
+    outs = []
+    with torch.cuda.stream(stream):
+        y.copy_(y0t)
+        plan.run(stream)
+        torch.cuda.synchronize()
+        outs.append(y.clone())
+        plan.capture(stream)
+        for _ in range(2):
+            y.copy_(y0t)
+            torch.cuda.synchronize()
+            plan.launch(stream)
+            torch.cuda.synchronize()
+            outs.append(y.clone())
+    for k, o in enumerate(outs[1:], 1):
+        assert torch.equal(o, outs[0]), f"run {k} differs from run 0"
+    want = xf @ ref.decode(h).astype(np.float64).T + (y0.astype(np.float64) if acc else 0.0)
+    err = rel_l2(outs[0].cpu().numpy(), want)
+    y2 = y0t.clone()
+    M.gemv(x, y2, ncols=N, accumulate=acc)
+    torch.cuda.synchronize()
+    err2 = rel_l2(outs[0].cpu().numpy(), y2.cpu().numpy())
+    print(f"rows {rows} accumulate {acc}: relL2 vs oracle {err:.2e}, vs the launch without words {err2:.2e}")
+    assert err <= TIGHT and err2 <= TIGHT
+    # the plan took shared tiles: its sums differ from whole tiles' in order
+    assert not torch.equal(outs[0], y2), "shared tiles were not used"

@@ -129,22 +129,25 @@ def test_forward_batch_against_oracle(sm, ref, dev, head_kind, xd):
         check_kv(model, oracle, dev, NTOK + 2, bar, f"head {head_kind} prompt")
 
 
+@pytest.mark.parametrize("xd", ["f32", "bf16"])
 @pytest.mark.parametrize("heads,kvh", [(4, 1), (8, 2)], ids=["kv1", "kv2"])
-def test_forward_batch_mfma_attention(sm, ref, dev, heads, kvh):
+def test_forward_batch_mfma_attention(sm, ref, dev, heads, kvh, xd):
     """Heads of 256 with 4 query heads per kv head (the reference model's
     shape) take the matrix-core prompt attention (16 tokens per workgroup,
     K and V through LDS 16 positions at a time). Chunks of 100 and 37
     tokens cross the 40-position window and tile boundaries mid-block; the
     last logits, the decode steps after and every KV row (each layer's rows
     depend on every token's attention output in the layers below) meet the
-    f32 prompt bar against the oracle."""
+    prompt bar against the oracle: 5e-3 with f32 activations, 2e-2 with
+    bf16 ones (the attention then writes only its bf16 output, the path the
+    real model and the 512-token bench take)."""
     import torch
     cfg = dict(LONG, head_dim=256, heads=heads, kv_heads=kvh)
-    model, oracle = build(sm, ref, dev, "q8_0", sm.X_F32, cfg)
+    model, oracle = build(sm, ref, dev, "q8_0", sm.X_F32 if xd == "f32" else sm.X_BF16, cfg)
     model.reserve(128)
     toks = tokens(139, seed=17)
     logits = torch.full((cfg["vocab"],), float("nan"), device=dev)
-    bar = 5e-3
+    bar = 5e-3 if xd == "f32" else 2e-2
     for lo, hi in ((0, 100), (100, 137)):
         want = None
         for p in range(lo, hi):
@@ -158,9 +161,9 @@ def test_forward_batch_mfma_attention(sm, ref, dev, heads, kvh):
         model.forward(toks[p], p, logits)
         torch.cuda.synchronize()
         err = rel_l2(logits.cpu().numpy(), oracle.forward(toks[p], p))
-        print(f"heads {heads}/{kvh}: decode at {p}, relL2 {err:.2e}")
+        print(f"heads {heads}/{kvh} x {xd}: decode at {p}, relL2 {err:.2e}")
         assert err <= bar
-    check_kv(model, oracle, dev, 139, bar, f"heads {heads}/{kvh} prompt", cfg)
+    check_kv(model, oracle, dev, 139, bar, f"heads {heads}/{kvh} x {xd} prompt", cfg)
 
 
 def test_forward_batch_short_chunk_is_exact(sm, ref, dev):
