@@ -14,7 +14,7 @@ are resident in HBM before timing starts.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--mode graph|eager]
                     [--workload decode-set|ffn-up|q6k-down|verify8|prefill512|forward|verify-block|
-                                decode-set-q6k|prompt512]
+                                decode-set-q6k|prompt512|decode-chain|startup]
 
 Prints one JSON line (rank 0). The metric is time per token (lower is
 better); achieved GB/s over the algorithmic bytes (container + bf16 x + f32 y
@@ -766,6 +766,37 @@ def bench_single(args, sm, torch, dev):
                          "bytes_per_launch": int(nbytes), "avg_launch_us": round(kern * 1e3, 3)}}
 
 
+def bench_startup(args, sm, torch, dev):
+    """startup: what one launch's fixed cost is made of, on the hot kernel's
+    launch shape (sparkmv_probe_startup): an empty kernel, the 64 KB codebook
+    staging alone, and plain reads of 8, 20 and 40 MB (about o, down and
+    gate+up) cold, with address translation warm (one dword per 4 KB page
+    read just before) and with the data warm (one dword per 64-byte line)."""
+    sizes = (8 << 20, 20 << 20, 40 << 20)
+    res = sm.probe_startup(sizes, reps=max(5, min(args.steps, 64)))
+    out = {"empty_kernel_us": round(res["empty"], 2), "empty_kernel_1wave_us": round(res["empty_1wave"], 2),
+           "empty_kernel_1wg_us": round(res["empty_1wg"], 2),
+           "empty_back_to_back_stream_us": round(res["empty_stream"], 2),
+           "empty_back_to_back_graph_us": round(res["empty_graph"], 2),
+           "stage_64k_us": round(res["stage_64k"], 2), "reads": {}}
+    for b in sizes:
+        r = res[b]
+        mb = b >> 20
+        out["reads"][f"{mb}MB"] = {k: round(v, 2) for k, v in r.items()}
+        out["reads"][f"{mb}MB"]["cold_gbps"] = round(b / (r["cold"] * 1e-6) / 1e9, 1)
+        log(f"  read {mb} MB: cold {r['cold']:.2f} us ({b / (r['cold'] * 1e-6) / 1e9:.0f} GB/s), translation warm "
+            f"{r['page_warm']:.2f} us, data warm {r['line_warm']:.2f} us")
+    log(f"  empty kernel {res['empty']:.2f} us ({res['empty_1wave']:.2f} with one wave per workgroup, "
+        f"{res['empty_1wg']:.2f} with one workgroup), 64 KB codebook staging {res['stage_64k']:.2f} us; "
+        f"back to back per launch: {res['empty_stream']:.2f} us on a stream, {res['empty_graph']:.2f} us in a graph")
+    return {"metric": "launch start-up split: kernel-exact us per launch on the hot kernel's shape",
+            "value": out["reads"]["20MB"]["cold"], "unit": "us (20 MB cold read)", "n_gpus": 1, "steps": args.steps,
+            "warmup": 0, "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "u32 reads",
+            "data": "synthetic", "config": {"workload": "startup", "grid": "one workgroup of 10 waves per CU",
+                                            "sizes_MB": [b >> 20 for b in sizes]},
+            "startup": out}
+
+
 def bench_prefill(args, sm, torch, dev):
     """prefill512: the prompt GEMM of one FFN pair, W 10240x2560 (up) and
     2560x10240 (down), VQ dim 4 nc 4096 2 stages, against 512 bf16 tokens.
@@ -856,7 +887,7 @@ def main():
     ap.add_argument("--mode", choices=["graph", "eager"], default="graph")
     ap.add_argument("--workload", default="decode-set",
                     choices=["decode-set", "verify8", "ffn-up", "q6k-down", "prefill512", "forward",
-                             "verify-block", "decode-set-q6k", "decode-chain", "prompt512"])
+                             "verify-block", "decode-set-q6k", "decode-chain", "prompt512", "startup"])
     ap.add_argument("--context", type=int, default=1024, help="forward: positions cached before the timed steps")
     ap.add_argument("--head-rows", type=int, default=VOCAB)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -894,6 +925,8 @@ def main():
             log(f"cpu baseline took {time.time() - t:.1f} s")
     elif args.workload == "prefill512":
         out = bench_prefill(args, sm, torch, dev)
+    elif args.workload == "startup":
+        out = bench_startup(args, sm, torch, dev)
     elif args.workload == "decode-set-q6k":
         out = bench_decode_set_q6k(args, sm, torch, dev)
     elif args.workload == "decode-chain":

@@ -324,6 +324,23 @@ int sparkmv_chain_trace(void * chain, uint32_t * buf, long words);
 /* The shape chosen for op i: MFMA parts S, K chunks C, macro steps per unit. */
 int sparkmv_chain_op_shape(void * chain, int i, int * S, int * C, int * msc);
 
+/* ---- launch start-up measurement ----
+ * No counterpart in the reference: a measurement of this build's launches,
+ * for the decode set's per-launch fixed cost. On the hot kernel's launch
+ * shape (one workgroup of 10 waves per CU), kernel-exact, medians of reps
+ * launches: out_us[0] an empty kernel, out_us[1] the same with one wave
+ * per workgroup, out_us[2] staging 64 KB of codebooks into LDS (L2 flushed
+ * before), then per size s (multiples of 16 bytes, 64 KB..1 GB) a plain read
+ * of sizes[s] bytes cold (out_us[3 + 3s]), after one dword per 4 KB page of
+ * it was read (address translation warm, data cold; out_us[4 + 3s]) and
+ * after one dword per 64-byte line was read (data warm; out_us[5 + 3s]);
+ * then, with n = nsizes, out_us[3 + 3n] an empty kernel of one workgroup of
+ * one wave, out_us[4 + 3n] and out_us[5 + 3n] the wall time per launch of 64
+ * empty full-shape launches back to back, eagerly and as one HIP graph
+ * (plain events around all 64). Allocates and frees its own buffers
+ * (largest size * reps + 640 MB); synchronizes the device. */
+int sparkmv_probe_startup(const size_t * sizes, int nsizes, int reps, double * out_us);
+
 /* ---- weight artifacts (host memory) ----
  * GGUF v2/v3 (ggml's layout), the reader of tools/dspark/src/gguf.rs:95-190
  * (Gguf::open, tensor_bytes, get_u64/get_f32/get_str/get_arr), extended to

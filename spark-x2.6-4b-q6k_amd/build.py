@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "lib", "libsparkmv.so")
 
-HIP_SOURCES = ["vq_kernels.hip", "kq_kernels.hip", "prefill.hip", "forward.hip", "chain.hip"]
+HIP_SOURCES = ["vq_kernels.hip", "kq_kernels.hip", "prefill.hip", "forward.hip", "chain.hip", "probe.hip"]
 CXX_SOURCES = ["abi.cpp", "plan.cpp", "host/vq_format.cpp", "host/synth.cpp", "host/artifacts.cpp", "host/profile.cpp",
                "host/model_load.cpp"]
 

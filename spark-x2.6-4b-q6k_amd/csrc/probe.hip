@@ -1,0 +1,268 @@
+/* probe.hip — what the fixed cost of one launch is made of (gfx950).
+ *
+ * A decode matvec reads 8-40 MB, which at 8 TB/s is 1-5 µs of transfer; the
+ * hot kernel's launches take 6.5-15 µs. These kernels split the difference,
+ * each on the hot kernel's launch shape (256 workgroups of 10 waves, one
+ * workgroup per CU) and timed kernel-exact (events carried by the dispatch):
+ *
+ *   probe_empty_kernel  nothing but its launch: dispatch of every workgroup
+ *                       and the end-of-kernel drain (also run with one wave
+ *                       per workgroup, to separate the dispatch's fixed part
+ *                       from the waves');
+ *   probe_stage_kernel  the hot kernel's prologue alone: 64 KB of codebooks
+ *                       (L2-resident after the first workgroup of each XCD)
+ *                       into LDS, then the barrier;
+ *   probe_read_kernel   a plain read of B bytes, each workgroup one
+ *                       contiguous slice, four 16-byte loads in flight per
+ *                       lane (the hot kernel reads its tiles' streams the
+ *                       same way);
+ *   probe_touch_kernel  one dword every `stride` bytes of a buffer: with a
+ *                       4 KB stride it warms address translation and almost
+ *                       no data (one 64-byte line per page); with a 64-byte
+ *                       stride it brings every line into the caches.
+ *
+ * The host entry times a read on a buffer no kernel has touched for the last
+ * 640 MB of traffic (cold: beyond the 256 MB memory-side cache and every
+ * XCD's L2), the same read right after a page touch of that buffer
+ * (translation warm, data cold) and right after a line touch (data warm).
+ * No counterpart in the reference: a measurement of this build's launches.
+ */
+#include "../../include/sparkmv.h"
+#include "common.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace sparkmv {
+
+constexpr int kProbeWaves = 10;
+constexpr int kProbeThreads = kProbeWaves * 64;
+
+/* no memory access at all: a wave starts and ends */
+__global__ __launch_bounds__(kProbeThreads) void probe_empty_kernel(uint32_t *) {}
+
+__global__ __launch_bounds__(kProbeThreads) void probe_stage_kernel(const uint4 * cb, uint32_t * sink) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int n = 65536 / 16;
+    constexpr int per = (n + kProbeThreads - 1) / kProbeThreads;
+    uint4 v[per];
+#pragma unroll
+    for (int k = 0; k < per; k++) v[k] = cb[min(k * kProbeThreads + (int) threadIdx.x, n - 1)];
+#pragma unroll
+    for (int k = 0; k < per; k++) {
+        const int i = k * kProbeThreads + (int) threadIdx.x;
+        if (i < n) ((uint4 *) lds)[i] = v[k];
+    }
+    __syncthreads();
+    const uint4 w = ((const uint4 *) lds)[(threadIdx.x * 37u) % n];
+    if ((w.x ^ w.y ^ w.z ^ w.w) == 0x9e3779b9u) sink[blockIdx.x] = 1u;
+}
+
+__global__ __launch_bounds__(kProbeThreads) void probe_read_kernel(const uint4 * p, size_t n16, uint32_t * sink) {
+    const size_t lo = n16 * blockIdx.x / gridDim.x, hi = n16 * (blockIdx.x + 1) / gridDim.x;
+    uint32_t acc = 0;
+    size_t i = lo + threadIdx.x;
+    for (; i + 3 * kProbeThreads < hi; i += 4 * kProbeThreads) {
+        const uint4 a = p[i], b = p[i + kProbeThreads], c = p[i + 2 * kProbeThreads], d = p[i + 3 * kProbeThreads];
+        acc ^= a.x ^ b.y ^ c.z ^ d.w;
+    }
+    for (; i < hi; i += kProbeThreads) acc ^= p[i].x;
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(kProbeThreads) void probe_touch_kernel(const uint32_t * p, size_t nwords, size_t stride,
+                                                                    uint32_t * sink) {
+    uint32_t acc = 0;
+    for (size_t i = ((size_t) blockIdx.x * blockDim.x + threadIdx.x) * stride; i < nwords;
+         i += (size_t) gridDim.x * blockDim.x * stride)
+        acc ^= p[i];
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+}  // namespace sparkmv
+
+using namespace sparkmv;
+
+namespace {
+
+struct Timer {
+    hipEvent_t a = nullptr, b = nullptr;
+    Timer() {
+        (void) hipEventCreate(&a);
+        (void) hipEventCreate(&b);
+    }
+    ~Timer() {
+        if (a) (void) hipEventDestroy(a);
+        if (b) (void) hipEventDestroy(b);
+    }
+    /* arm the next hot-path launch to carry the events */
+    void arm() {
+        g_launch_events.start = a;
+        g_launch_events.stop = b;
+    }
+    double us() {
+        g_launch_events = LaunchEvents();
+        if (hipEventSynchronize(b) != hipSuccess) return -1.0;
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return -1.0;
+        return 1000.0 * ms;
+    }
+};
+
+double median(std::vector<double> v) {
+    std::sort(v.begin(), v.end());
+    return v.empty() ? 0.0 : v[v.size() / 2];
+}
+
+}  // namespace
+
+extern "C" {
+
+int sparkmv_probe_startup(const size_t * sizes, int nsizes, int reps, double * out_us) {
+    if (!sizes || nsizes < 1 || nsizes > 8 || reps < 3 || reps > 64 || !out_us) {
+        set_error("probe: 1..8 sizes, 3..64 repetitions and an output array");
+        return -1;
+    }
+    for (int s = 0; s < nsizes; s++)
+        if (sizes[s] < 65536 || sizes[s] > ((size_t) 1 << 30) || sizes[s] % 16) {
+            set_error("probe: sizes are multiples of 16 bytes from 64 KB to 1 GB, not %zu", sizes[s]);
+            return -1;
+        }
+    const int G = cu_count();
+    const size_t pool = (size_t) 640 << 20;   /* more than the memory-side cache and every L2 together */
+    size_t big = 65536;
+    for (int s = 0; s < nsizes; s++) big = std::max(big, sizes[s]);
+    /* targets first, then a separate flush region: reading the whole region
+     * leaves none of a target in any cache */
+    const size_t targets = big * (size_t) reps, total = targets + pool;
+    uint8_t * buf = nullptr;
+    uint32_t * sink = nullptr;
+    hipError_t e = hipMalloc((void **) &buf, total);
+    if (e != hipSuccess) return fail_hip("probe buffer", e);
+    e = hipMalloc((void **) &sink, 4 * (size_t) G);
+    if (e == hipSuccess) e = hipMemset(sink, 0, 4 * (size_t) G);
+    if (e == hipSuccess) e = hipMemset(buf, 1, total);
+    if (e == hipSuccess) e = hipFuncSetAttribute((const void *) probe_stage_kernel,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void) hipFree(buf);
+        if (sink) (void) hipFree(sink);
+        return fail_hip("probe setup", e);
+    }
+    hipStream_t st = nullptr;
+    Timer t;
+    const dim3 grid(G), block(kProbeThreads);
+    int rc = 0;
+    /* flush: one pass over the flush region evicts every target from the caches */
+    auto flush = [&]() {
+        launch_kernel(probe_read_kernel, grid, block, 0, st, (const uint4 *) (buf + targets), pool / 16, sink);
+    };
+    std::vector<double> v;
+    /* empty launches */
+    for (int r = 0; r < reps && !rc; r++) {
+        t.arm();
+        launch_kernel(probe_empty_kernel, grid, block, 0, st, sink);
+        v.push_back(t.us());
+    }
+    out_us[0] = median(v);
+    v.clear();
+    for (int r = 0; r < reps && !rc; r++) {
+        t.arm();
+        launch_kernel(probe_empty_kernel, grid, dim3(64), 0, st, sink);
+        v.push_back(t.us());
+    }
+    out_us[1] = median(v);
+    /* one workgroup of one wave */
+    v.clear();
+    for (int r = 0; r < reps && !rc; r++) {
+        t.arm();
+        launch_kernel(probe_empty_kernel, dim3(1), dim3(64), 0, st, sink);
+        v.push_back(t.us());
+    }
+    out_us[3 + 3 * nsizes] = median(v);
+    /* 64 empty launches of the full shape back to back on one stream, eagerly
+     * and as one captured graph: wall time per launch between two plain
+     * events (no per-dispatch event) */
+    {
+        hipStream_t cs = nullptr;
+        hipGraph_t g = nullptr;
+        hipGraphExec_t gx = nullptr;
+        e = hipStreamCreate(&cs);
+        const int K = 64;
+        auto wall = [&](bool graph) -> double {
+            std::vector<double> w;
+            for (int r = 0; r < 5; r++) {
+                if (hipEventRecord(t.a, cs) != hipSuccess) return -1.0;
+                if (graph) {
+                    if (hipGraphLaunch(gx, cs) != hipSuccess) return -1.0;
+                } else {
+                    for (int k = 0; k < K; k++) hipLaunchKernelGGL(probe_empty_kernel, grid, block, 0, cs, sink);
+                }
+                if (hipEventRecord(t.b, cs) != hipSuccess || hipEventSynchronize(t.b) != hipSuccess) return -1.0;
+                float ms = 0.f;
+                if (hipEventElapsedTime(&ms, t.a, t.b) != hipSuccess) return -1.0;
+                w.push_back(1000.0 * ms / K);
+            }
+            return median(w);
+        };
+        if (e == hipSuccess) out_us[4 + 3 * nsizes] = wall(false);
+        if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            for (int k = 0; k < K; k++) hipLaunchKernelGGL(probe_empty_kernel, grid, block, 0, cs, sink);
+            e = hipStreamEndCapture(cs, &g);
+        }
+        if (e == hipSuccess) e = hipGraphInstantiate(&gx, g, nullptr, nullptr, 0);
+        if (e == hipSuccess) {
+            (void) hipGraphLaunch(gx, cs);   /* first replay uploads the graph */
+            (void) hipStreamSynchronize(cs);
+            out_us[5 + 3 * nsizes] = wall(true);
+        }
+        if (gx) (void) hipGraphExecDestroy(gx);
+        if (g) (void) hipGraphDestroy(g);
+        if (cs) (void) hipStreamDestroy(cs);
+        if (e != hipSuccess) rc = fail_hip("probe back-to-back launches", e);
+    }
+    /* staging alone, codebooks cold in L2 each time (flushed before) */
+    v.clear();
+    for (int r = 0; r < reps && !rc; r++) {
+        flush();
+        t.arm();
+        launch_kernel(probe_stage_kernel, grid, block, 65536, st, (const uint4 *) (buf + (size_t) r * 65536), sink);
+        v.push_back(t.us());
+    }
+    out_us[2] = median(v);
+    for (int s = 0; s < nsizes && !rc; s++) {
+        const size_t B = sizes[s];
+        std::vector<double> cold, page, line;
+        for (int r = 0; r < reps; r++) {
+            const uint8_t * p = buf + (size_t) r * B;
+            flush();
+            t.arm();
+            launch_kernel(probe_read_kernel, grid, block, 0, st, (const uint4 *) p, B / 16, sink);
+            cold.push_back(t.us());
+            flush();
+            launch_kernel(probe_touch_kernel, grid, block, 0, st, (const uint32_t *) p, B / 4, (size_t) 1024, sink);
+            t.arm();
+            launch_kernel(probe_read_kernel, grid, block, 0, st, (const uint4 *) p, B / 16, sink);
+            page.push_back(t.us());
+            flush();
+            launch_kernel(probe_touch_kernel, grid, block, 0, st, (const uint32_t *) p, B / 4, (size_t) 16, sink);
+            t.arm();
+            launch_kernel(probe_read_kernel, grid, block, 0, st, (const uint4 *) p, B / 16, sink);
+            line.push_back(t.us());
+        }
+        out_us[3 + 3 * s] = median(cold);
+        out_us[4 + 3 * s] = median(page);
+        out_us[5 + 3 * s] = median(line);
+    }
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) rc = fail_hip("probe", e);
+    (void) hipFree(buf);
+    (void) hipFree(sink);
+    for (int k = 0; k < 6 + 3 * nsizes; k++)
+        if (out_us[k] < 0) { set_error("probe: a timing event failed"); rc = -1; }
+    return rc;
+}
+
+}  // extern "C"

@@ -148,6 +148,7 @@ SIGNATURES = {
     "sparkmv_chain_status": (_I, [_P]),
     "sparkmv_chain_op_shape": (_I, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "sparkmv_chain_trace": (_I, [_P, _P, ctypes.c_long]),
+    "sparkmv_probe_startup": (_I, [ctypes.POINTER(_S), _I, _I, _D]),
     "sparkmv_gguf_open": (_P, [ctypes.c_char_p]),
     "sparkmv_gguf_close": (None, [_P]),
     "sparkmv_gguf_version": (_I, [_P]),
@@ -1128,6 +1129,22 @@ class Chain:
         check(lib().sparkmv_chain_op_shape(self.h, i, ctypes.byref(S), ctypes.byref(C), ctypes.byref(msc)),
               "chain shape")
         return S.value, C.value, msc.value
+
+
+def probe_startup(sizes=(8 << 20, 20 << 20, 40 << 20), reps=20):
+    """Launch start-up split (sparkmv_probe_startup), kernel-exact medians
+    in µs: {"empty", "empty_1wave", "empty_1wg", "empty_stream",
+    "empty_graph", "stage_64k", sizes[i]: {"cold", "page_warm",
+    "line_warm"}}."""
+    n = len(sizes)
+    sz = (_S * n)(*sizes)
+    out = (ctypes.c_double * (6 + 3 * n))()
+    check(lib().sparkmv_probe_startup(sz, n, int(reps), out), "probe startup")
+    res = {"empty": out[0], "empty_1wave": out[1], "stage_64k": out[2], "empty_1wg": out[3 + 3 * n],
+           "empty_stream": out[4 + 3 * n], "empty_graph": out[5 + 3 * n]}
+    for i, b in enumerate(sizes):
+        res[int(b)] = {"cold": out[3 + 3 * i], "page_warm": out[4 + 3 * i], "line_warm": out[5 + 3 * i]}
+    return res
 
 
 # The decode token's matvecs in the order the forward issues them
