@@ -21,13 +21,7 @@ import sparkref as ref
 F32 = np.float32
 
 
-def bf16_bits(x):
-    """f32 -> bf16 bits, round to nearest even; NaN -> quiet NaN."""
-    u = np.ascontiguousarray(x, dtype=F32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
-    nan = (u & 0x7FFFFFFF) > 0x7F800000
-    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint32)
-    return r.astype(np.uint16)
+bf16_bits = fw.bf16_bits   # f32 -> bf16 bits, round to nearest even; NaN -> quiet NaN
 
 
 def bf16_f32(bits):

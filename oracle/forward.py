@@ -20,6 +20,14 @@ with the same helpers:
 The matrices are given as f32 arrays (the oracle's bit-exact decode of the
 VQ containers or Q8_0 blocks). Sums run in numpy's order, not the Rust
 dot's 8-lane order, so results agree to f32 rounding, not bit for bit.
+
+With x_bf16 the restatement also rounds, to bf16 (nearest, ties to even),
+exactly the values a matvec reads when the GPU forward runs on bf16
+activations: the normed input of qkv and the head gate, the gated attention
+output (the out matvec's input), the normed input of gate and up, gelu(gate)
+* up (down's input) and the final norm (the head's input). The residual,
+the KV cache, the gate and every sum stay f32, as on the GPU. This mode is
+this build's arithmetic, not the reference's (which is f32 throughout).
 """
 import math
 
@@ -27,6 +35,21 @@ import numpy as np
 from scipy.special import erf
 
 F32 = np.float32
+
+
+def bf16_bits(x):
+    """f32 -> bf16 bits, round to nearest even; NaN -> quiet NaN."""
+    u = np.ascontiguousarray(x, dtype=F32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint32)
+    return r.astype(np.uint16)
+
+
+def bf16_round(x):
+    """x rounded to bf16 (nearest, ties to even), as f32 values."""
+    x = np.asarray(x, F32)
+    return (bf16_bits(x.ravel()).astype(np.uint32) << 16).view(F32).reshape(x.shape)
 
 
 def rms_norm(x, w, eps):
@@ -77,10 +100,11 @@ class Forward:
     """One model's decode state: cfg as sparkmv_model_cfg's fields (dict),
     layers a list of dicts of f32 arrays (in_norm, post_norm, qkv, attn_gate,
     out, gate, up, down) plus full (bool), embed [vocab, hidden] f32, norm
-    [hidden] f32."""
+    [hidden] f32; x_bf16 rounds every matvec's input to bf16."""
 
-    def __init__(self, cfg, layers, embed, norm):
+    def __init__(self, cfg, layers, embed, norm, x_bf16=False):
         self.c = cfg
+        self.q = bf16_round if x_bf16 else (lambda v: v)   # a matvec's input
         self.layers = layers
         self.embed = embed
         self.norm = norm
@@ -108,7 +132,7 @@ class Forward:
             theta = c["rope_full_theta"] if full else c["rope_slide_theta"]
             partial = c["rope_full_partial"] if full else c["rope_slide_partial"]
             dim, cos, sin = rope_table(pos, hd, theta, partial)
-            xn = rms_norm(h, L["in_norm"], c["eps"])
+            xn = self.q(rms_norm(h, L["in_norm"], c["eps"]))
             qkv = (L["qkv"] @ xn).astype(F32)
             gate = (L["attn_gate"] @ xn).astype(F32)
             for hh in range(heads):
@@ -130,9 +154,9 @@ class Forward:
                 e = np.exp(sc - sc.max()).astype(F32)
                 p = (e * (F32(1.0) / F32(e.sum(dtype=F32)))).astype(F32)
                 attn[hh * hd:(hh + 1) * hd] = (p @ V[:, kv * hd:(kv + 1) * hd]).astype(F32) * g[hh]
-            h = (h + (L["out"] @ attn).astype(F32)).astype(F32)
-            xn = rms_norm(h, L["post_norm"], c["eps"])
+            h = (h + (L["out"] @ self.q(attn)).astype(F32)).astype(F32)
+            xn = self.q(rms_norm(h, L["post_norm"], c["eps"]))
             act = (gelu((L["gate"] @ xn).astype(F32)) * (L["up"] @ xn).astype(F32)).astype(F32)
-            h = (h + (L["down"] @ act).astype(F32)).astype(F32)
-        xn = rms_norm(h, self.norm, c["eps"])
+            h = (h + (L["down"] @ self.q(act)).astype(F32)).astype(F32)
+        xn = self.q(rms_norm(h, self.norm, c["eps"]))
         return (self.embed @ xn).astype(F32)

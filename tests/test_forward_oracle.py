@@ -42,11 +42,17 @@ def weights(seed, cfg=CFG, full=FULL):
     return layers, embed, norm
 
 
-def torch_forward(cfg, layers, embed, norm, tokens):
-    """The same model from torch's own routines, in f64; logits per step."""
+def torch_forward(cfg, layers, embed, norm, tokens, bf16=(), slip=None):
+    """The same model from torch's own routines, in f64; logits per step.
+    bf16: the matvec inputs to round through torch.bfloat16 ("in_norm",
+    "attn", "post_norm", "act", "final"); slip: a deliberate mistake, for
+    the test that shows the formulation tells it apart."""
     import torch
     import torch.nn.functional as F
     dt = torch.float64
+
+    def R(name, x):
+        return x.to(torch.float32).to(torch.bfloat16).to(dt) if name in bf16 else x
     T = lambda a: torch.tensor(np.asarray(a, np.float64), dtype=dt)
     hd, heads, kvh, hid = cfg["head_dim"], cfg["heads"], cfg["kv_heads"], cfg["hidden"]
     qd, kvd = heads * hd, kvh * hd
@@ -63,7 +69,7 @@ def torch_forward(cfg, layers, embed, norm, tokens):
             partial = cfg["rope_full_partial"] if full else cfg["rope_slide_partial"]
             dim = fw.rope_dim(hd, partial)
             half = dim // 2
-            xn = F.rms_norm(h, (hid,), weight=L["in_norm"], eps=cfg["eps"])
+            xn = R("in_norm", F.rms_norm(h, (hid,), weight=L["in_norm"], eps=cfg["eps"]))
             qkv = L["qkv"] @ xn
             g = torch.sigmoid(L["attn_gate"] @ xn)
             q = qkv[:qd].reshape(heads, hd).clone()
@@ -81,10 +87,12 @@ def torch_forward(cfg, layers, embed, norm, tokens):
             Ks = torch.stack(K[li][start:], 0).repeat_interleave(heads // kvh, dim=1).transpose(0, 1)
             Vs = torch.stack(V[li][start:], 0).repeat_interleave(heads // kvh, dim=1).transpose(0, 1)
             o = F.scaled_dot_product_attention(q[:, None, :], Ks.contiguous(), Vs.contiguous())[:, 0, :]
-            h = h + L["out"] @ (o * g[:, None]).reshape(-1)
-            xn = F.rms_norm(h, (hid,), weight=L["post_norm"], eps=cfg["eps"])
-            h = h + L["down"] @ (F.gelu(L["gate"] @ xn, approximate="none") * (L["up"] @ xn))
-        out.append((E @ F.rms_norm(h, (hid,), weight=Nf, eps=cfg["eps"])).numpy())
+            h = h + L["out"] @ R("attn", (o * g[:, None]).reshape(-1))
+            if slip == "round_residual":
+                h = R("in_norm", h)
+            xn = R("post_norm", F.rms_norm(h, (hid,), weight=L["post_norm"], eps=cfg["eps"]))
+            h = h + L["down"] @ R("act", F.gelu(L["gate"] @ xn, approximate="none") * (L["up"] @ xn))
+        out.append((E @ R("final", F.rms_norm(h, (hid,), weight=Nf, eps=cfg["eps"]))).numpy())
     return out
 
 
@@ -196,3 +204,34 @@ def test_single_position_attention_is_gated_value():
     hd, heads, kvh = cfg["head_dim"], cfg["heads"], cfg["kv_heads"]
     v = qkv[heads * hd + kvh * hd:]
     assert np.array_equal(f.kv_v[0][0], v.astype(np.float32))
+
+
+BF16_POINTS = ("in_norm", "attn", "post_norm", "act", "final")
+
+
+def test_bf16_oracle_against_torch_routines():
+    """The oracle's bf16 mode (every matvec input rounded to bf16, nothing
+    else) against the torch f64 formulation with the same five inputs cast
+    through torch.bfloat16. The two round values computed in f32 and in
+    f64, so an element near a rounding boundary may land on the other bf16
+    neighbour; the bar allows a few such (5e-4), while each wrong placement
+    below moves the logits by more than four times the bar."""
+    layers, embed, norm = weights(2)
+    tokens = [3, 17, 41, 8, 8, 29, 0]
+    f = fw.Forward(CFG, layers, embed, norm, x_bf16=True)
+    got = [f.forward(t, p) for p, t in enumerate(tokens)]
+    want = torch_forward(CFG, layers, embed, norm, tokens, bf16=BF16_POINTS)
+    worst = max(rel_l2(g, w) for g, w in zip(got, want))
+    print(f"bf16 oracle vs torch bf16 formulation: worst relL2 {worst:.2e}")
+    assert worst <= 5e-4
+    wrong = {"no rounding": torch_forward(CFG, layers, embed, norm, tokens),
+             "attn not rounded": torch_forward(CFG, layers, embed, norm, tokens,
+                                               bf16=tuple(p for p in BF16_POINTS if p != "attn")),
+             "act not rounded": torch_forward(CFG, layers, embed, norm, tokens,
+                                              bf16=tuple(p for p in BF16_POINTS if p != "act")),
+             "residual rounded too": torch_forward(CFG, layers, embed, norm, tokens, bf16=BF16_POINTS,
+                                                   slip="round_residual")}
+    for name, w in wrong.items():
+        d = max(rel_l2(g, ww) for g, ww in zip(got, w))
+        print(f"  {name}: relL2 {d:.2e}")
+        assert d > 2e-3, name

@@ -8,7 +8,9 @@ that is Q8_0 blocks or a VQ container. Tokens run past the window.
 Bars: with f32 activations into the matvecs (the reference's arithmetic) the
 logits of every step meet 1e-5 relative L2 (measured 7e-7) and the KV cache
 1e-5. With bf16 activations (rounded at each matvec's input, as the decode
-benchmark runs) the logits meet 2e-2 (measured 6e-3).
+benchmark runs) the oracle rounds at the same five inputs (forward.py's
+x_bf16 mode) and the logits and KV cache meet BF16_BAR against it; against
+the reference's f32 arithmetic they meet 2e-2 (measured 6e-3).
 """
 import numpy as np
 import pytest
@@ -22,6 +24,16 @@ CFG = dict(hidden=256, layers=3, heads=4, kv_heads=2, head_dim=64, intermediate=
            rope_slide_partial=1.0, max_ctx=16)
 FULL = [False, True, False]
 TOKENS = [5, 17, 3, 250, 42, 7, 17]
+# bf16 activations against the oracle's bf16 mode. The GPU's f32 values and
+# the oracle's differ in their last bits (sums in another order), so a value
+# within that distance of a bf16 rounding boundary rounds to the other
+# neighbour on one side: such a step differs by about 1e-4..3e-3, and over a
+# run the difference persists through the KV cache. A run is held to the
+# bound of those flips; test_forward_bf16_step_by_step isolates each step
+# (the oracle continues from the GPU's own KV rows), where most steps meet
+# 1e-5.
+BF16_RUN_BAR = 5e-3
+BF16_BAR = 1e-5
 
 
 def rel_l2(a, b):
@@ -63,7 +75,7 @@ def build(sm, ref, dev, head_kind, x_dtype, cfg=None):
         head = sm.DeviceContainer(data, dev)
     cfg = dict(c, x_dtype=x_dtype, dim=4, nc=4096, nstages=2, v3=1)
     model = sm.Model(cfg, dev_layers, head, torch.from_numpy(norm).to(dev))
-    oracle = fw.Forward(c, host_layers, embed.astype(np.float32), norm)
+    oracle = fw.Forward(c, host_layers, embed.astype(np.float32), norm, x_bf16=x_dtype == sm.X_BF16)
     return model, oracle
 
 
@@ -73,18 +85,21 @@ def test_forward_against_oracle(sm, ref, dev, head_kind, xd):
     import torch
     x_dtype = sm.X_F32 if xd == "f32" else sm.X_BF16
     model, oracle = build(sm, ref, dev, head_kind, x_dtype)
+    f32_oracle = fw.Forward(oracle.c, oracle.layers, oracle.embed, oracle.norm)
     logits = torch.full((CFG["vocab"],), float("nan"), device=dev)
-    bar = 1e-5 if xd == "f32" else 2e-2
+    bar = 1e-5 if xd == "f32" else BF16_RUN_BAR
     worst = 0.0
     for pos, tok in enumerate(TOKENS):
         model.forward(tok, pos, logits)
         torch.cuda.synchronize()
         want = oracle.forward(tok, pos)
-        err = rel_l2(logits.cpu().numpy(), want)
+        got = logits.cpu().numpy()
+        err = rel_l2(got, want)
+        err32 = rel_l2(got, f32_oracle.forward(tok, pos))
         worst = max(worst, err)
-        print(f"head {head_kind} x {xd} pos {pos} token {tok}: logits relL2 {err:.2e}")
-        assert err <= bar
-    if xd == "f32":
+        print(f"head {head_kind} x {xd} pos {pos} token {tok}: logits relL2 {err:.2e} (vs f32 arithmetic {err32:.2e})")
+        assert err <= bar and err32 <= (1e-5 if xd == "f32" else 2e-2)
+    if True:
         # the KV cache rows, copied out of the model's buffer device to device
         import ctypes
         hip = ctypes.CDLL("libamdhip64.so")
@@ -97,7 +112,7 @@ def test_forward_against_oracle(sm, ref, dev, head_kind, xd):
                                      ctypes.c_size_t(n * kvd * 4), ctypes.c_int(3)) == 0   # device to device
                 err = rel_l2(buf.cpu().numpy(), want[:n])
                 print(f"layer {li} cache relL2 {err:.2e}")
-                assert err <= 1e-5, li
+                assert err <= bar, li
     print(f"head {head_kind} x {xd}: worst relL2 {worst:.2e}")
 
 
@@ -196,9 +211,9 @@ def test_verify_block_and_rollback(sm, ref, dev, head_kind, xd):
     only the prefix and the 2 kept tokens."""
     import torch
     x_dtype = sm.X_F32 if xd == "f32" else sm.X_BF16
-    bar = 1e-5 if xd == "f32" else 2e-2
+    bar = 1e-5 if xd == "f32" else BF16_RUN_BAR
     model, oracle = build(sm, ref, dev, head_kind, x_dtype)
-    kept = fw.Forward(oracle.c, oracle.layers, oracle.embed, oracle.norm)
+    kept = fw.Forward(oracle.c, oracle.layers, oracle.embed, oracle.norm, x_bf16=xd == "bf16")
     prefix, block = [5, 17, 3], [250, 42, 7, 17, 99, 1, 300, 12]
     one = torch.empty(CFG["vocab"], device=dev)
     for p, t in enumerate(prefix):
@@ -256,3 +271,46 @@ def test_forward_wider_heads(sm, ref, dev, hd, heads, kvh):
         err = rel_l2(got[i], oracle.forward(t, 4 + i))
         print(f"hd {hd} block row {i}: relL2 {err:.2e}")
         assert err <= 1e-5
+
+
+def _kv_rows(model, dev, li, n, kvd):
+    """The first n rows of layer li's K and V cache, copied device to device."""
+    import ctypes
+    import torch
+    hip = ctypes.CDLL("libamdhip64.so")
+    out = []
+    for ptr in model.kv(li):
+        buf = torch.empty((n, kvd), dtype=torch.float32, device=dev)
+        assert hip.hipMemcpy(ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(ptr), ctypes.c_size_t(n * kvd * 4),
+                             ctypes.c_int(3)) == 0
+        out.append(buf.cpu().numpy())
+    return out
+
+
+@pytest.mark.parametrize("head_kind", ["q8_0", "vq"])
+def test_forward_bf16_step_by_step(sm, ref, dev, head_kind):
+    """bf16 activations, each step on its own: before every step the
+    oracle's KV cache takes the GPU's rows, so a bf16 rounding flip in an
+    earlier step does not carry over, and each step compares one token's
+    arithmetic. Most steps meet 1e-5 against the oracle's bf16 mode; the
+    rest (a value within its last bits of a rounding boundary) stay under
+    the flip bound. 16 tokens, past the window."""
+    import torch
+    model, oracle = build(sm, ref, dev, head_kind, sm.X_BF16)
+    kvd = CFG["kv_heads"] * CFG["head_dim"]
+    toks = [int(t) for t in np.random.default_rng(21).integers(0, CFG["vocab"], CFG["max_ctx"])]
+    logits = torch.full((CFG["vocab"],), float("nan"), device=dev)
+    errs = []
+    for pos, tok in enumerate(toks):
+        if pos:
+            for li in range(CFG["layers"]):
+                k, v = _kv_rows(model, dev, li, pos, kvd)
+                oracle.kv_k[li][:pos] = k
+                oracle.kv_v[li][:pos] = v
+        model.forward(tok, pos, logits)
+        torch.cuda.synchronize()
+        errs.append(rel_l2(logits.cpu().numpy(), oracle.forward(tok, pos)))
+    errs = np.array(errs)
+    print(f"head {head_kind}: per-step relL2 vs the bf16 oracle {np.array2string(errs, precision=1)}")
+    assert np.mean(errs <= BF16_BAR) >= 0.75, errs
+    assert errs.max() <= BF16_RUN_BAR, errs
