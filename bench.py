@@ -483,7 +483,9 @@ def bench_forward(args, sm, torch, dev):
     cfg = dict(hidden=HIDDEN, layers=LAYERS, heads=NHEAD, kv_heads=KVD // (QD // NHEAD), head_dim=QD // NHEAD,
                intermediate=FFN, vocab=args.head_rows, eps=1e-6, sliding_window=FW_WINDOW, rope_full_theta=5.0e6,
                rope_full_partial=0.25, rope_slide_theta=1.0e4, rope_slide_partial=1.0, max_ctx=max_ctx,
-               x_dtype=sm.X_BF16, dim=VQ["dim"], nc=VQ["nc"], nstages=VQ["nstages"], v3=VQ["v3"])
+               x_dtype=sm.X_F32 if args.fw_x == "f32" else sm.X_BF16, dim=VQ["dim"], nc=VQ["nc"],
+               nstages=VQ["nstages"], v3=VQ["v3"])
+    xdesc = "f32 x (the reference's precision: hi + lo f16 halves)" if args.fw_x == "f32" else "bf16 x"
     shapes = [("qkv", QD + 2 * KVD, HIDDEN), ("attn_gate", NHEAD, HIDDEN), ("out", HIDDEN, QD),
               ("gate", FFN, HIDDEN), ("up", FFN, HIDDEN), ("down", HIDDEN, FFN)]
     t0 = time.time()
@@ -551,7 +553,7 @@ def bench_forward(args, sm, torch, dev):
                 "metric": "speculative verify block us/step (8 tokens, whole model, tied Q8_0 head)",
                 "value": round(vms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
                 "warmup": args.warmup, "ms_per_step": round(vms, 4), "higher_is_better": False, "scaling": "weak",
-                "vs_baseline": None, "dtype": "f16xf16->f32 matvecs (bf16 x), f32 elementwise, f64 norm sums",
+                "vs_baseline": None, "dtype": f"f16xf16->f32 matvecs ({xdesc}), f32 elementwise, f64 norm sums",
                 "data": "synthetic (seeded, random-init weights of the real shapes)",
                 "config": {"workload": f"verify block of 8 tokens at context {P4}", "layers": LAYERS,
                            "hidden": HIDDEN, "ffn": FFN, "heads": NHEAD, "sliding_window": FW_WINDOW,
@@ -591,7 +593,7 @@ def bench_forward(args, sm, torch, dev):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16xf16->f32 matvecs (bf16 x), f32 elementwise, f64 norm sums",
+        "dtype": f"f16xf16->f32 matvecs ({xdesc}), f32 elementwise, f64 norm sums",
         "data": "synthetic (seeded, random-init weights of the real shapes)",
         "config": {"workload": "decode forward, one token per step at context " + str(P), "layers": LAYERS,
                    "hidden": HIDDEN, "ffn": FFN, "heads": NHEAD, "kv_heads": cfg["kv_heads"],
@@ -771,7 +773,9 @@ def bench_startup(args, sm, torch, dev):
     launch shape (sparkmv_probe_startup): an empty kernel, the 64 KB codebook
     staging alone, and plain reads of 8, 20 and 40 MB (about o, down and
     gate+up) cold, with address translation warm (one dword per 4 KB page
-    read just before) and with the data warm (one dword per 64-byte line)."""
+    read just before) and with the data warm (one dword per 64-byte line);
+    then what a dependent op costs inside one launch instead
+    (sparkmv_probe_handoff), three ways."""
     sizes = (8 << 20, 20 << 20, 40 << 20)
     res = sm.probe_startup(sizes, reps=max(5, min(args.steps, 64)))
     out = {"empty_kernel_us": round(res["empty"], 2), "empty_kernel_1wave_us": round(res["empty_1wave"], 2),
@@ -786,6 +790,10 @@ def bench_startup(args, sm, torch, dev):
         out["reads"][f"{mb}MB"]["cold_gbps"] = round(b / (r["cold"] * 1e-6) / 1e9, 1)
         log(f"  read {mb} MB: cold {r['cold']:.2f} us ({b / (r['cold'] * 1e-6) / 1e9:.0f} GB/s), translation warm "
             f"{r['page_warm']:.2f} us, data warm {r['line_warm']:.2f} us")
+    hand = sm.probe_handoff((1280, 2560, 5120))
+    out["handoff_us_per_op"] = {k: {str(n): round(v, 2) for n, v in d.items()} for k, d in hand.items()}
+    for k, d in hand.items():
+        log(f"  dependent handoff, {k}: " + ", ".join(f"{n} words {v:.2f} us" for n, v in d.items()))
     log(f"  empty kernel {res['empty']:.2f} us ({res['empty_1wave']:.2f} with one wave per workgroup, "
         f"{res['empty_1wg']:.2f} with one workgroup), 64 KB codebook staging {res['stage_64k']:.2f} us; "
         f"back to back per launch: {res['empty_stream']:.2f} us on a stream, {res['empty_graph']:.2f} us in a graph")
@@ -896,6 +904,8 @@ def main():
     ap.add_argument("--chain-units", type=int, default=0,
                     help="decode-chain: units per workgroup aimed for (0: the chain's cost model)")
     ap.add_argument("--chain-trace", action="store_true", help="decode-chain: one more launch with a phase trace")
+    ap.add_argument("--fw-x", choices=["bf16", "f32"], default="bf16",
+                    help="forward / verify-block: the matvecs' activations (f32 is the reference's precision)")
     ap.add_argument("--chain-trace-out", default=None, metavar="NPY", help="decode-chain: also save the raw trace")
     ap.add_argument("--no-check", dest="check", action="store_false",
                     help="skip the oracle check of the timed outputs")

@@ -340,6 +340,15 @@ int sparkmv_chain_op_shape(void * chain, int i, int * S, int * C, int * msc);
  * (plain events around all 64). Allocates and frees its own buffers
  * (largest size * reps + 640 MB); synchronizes the device. */
 int sparkmv_probe_startup(const size_t * sizes, int nsizes, int reps, double * out_us);
+/* The cost of one dependent handoff over every workgroup (one per CU), the
+ * decode chain's per-op wait, three ways: mode 0 words carrying their epoch
+ * (each reader reloads the words not yet current; the chain's protocol), 1
+ * the same behind one sentinel word per producer, 2 an agent-scope fence and
+ * an atomic counter per op, polled before reading. For each word count
+ * nwords[i] (256..5120, words an op's reader loads), out_us[mode * nn + i] =
+ * µs per op of a 400-op chain minus a 1-op chain, best of 5. No counterpart
+ * in the reference. Needs the device to itself; synchronizes it. */
+int sparkmv_probe_handoff(const int * nwords, int nn, double * out_us);
 
 /* ---- weight artifacts (host memory) ----
  * GGUF v2/v3 (ggml's layout), the reader of tools/dspark/src/gguf.rs:95-190

@@ -79,6 +79,99 @@ __global__ __launch_bounds__(kProbeThreads) void probe_touch_kernel(const uint32
     if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
 }
 
+/* A chain of K dependent "ops" over all workgroups, each op moving n words:
+ * every workgroup reads all n words the previous op wrote, sums them, and
+ * writes its 1/G of this op's n words. Three ways to know the words are
+ * there: (0) each word carries its epoch in its upper half and a reader
+ * reloads the words whose epoch is not yet current; (1) the same words, but
+ * wave 0 first waits on one word of each producer; (2) plain words, each
+ * producer's stores released by an agent-scope fence and counted by an
+ * atomic per op, which wave 0 polls before anyone reads. Every wait is
+ * bounded (past kProbeSpin polls the workgroup sets *err and waits no more).
+ * out[0] is the last op's sum in workgroup 0, which the host checks. */
+constexpr int kProbeMaxWords = 10;              /* words per thread */
+constexpr uint32_t kProbeSpin = 1u << 18;
+
+template <int MODE>
+__global__ __launch_bounds__(512) void probe_handoff_kernel(uint64_t * buf, uint32_t * ctr, int n, int K,
+                                                            uint32_t base, uint32_t * err, uint32_t * out) {
+    __shared__ uint32_t red[8];
+    const int tid = threadIdx.x, G = gridDim.x, wg = blockIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t s = 0;
+    bool dead = false;
+    for (int op = 0; op < K; op++) {
+        if (op > 0) {
+            const uint64_t * src = buf + (size_t) (op - 1) * n;
+            const uint32_t want = base + (uint32_t) op;
+            if (MODE == 1 && wave == 0 && !dead) {
+                uint32_t spins = 0;
+                while (true) {
+                    bool ok = true;
+                    for (int k = 0; k < 4; k++) {
+                        const int p = lane + 64 * k;
+                        const int lo = (int) ((long) p * n / G), hi = (int) ((long) (p + 1) * n / G);
+                        if (p < G && hi > lo &&
+                            (uint32_t) (__hip_atomic_load(src + hi - 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) != want)
+                            ok = false;
+                    }
+                    if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+                    if (++spins > kProbeSpin) { if (lane == 0) atomicOr(err, 1u); dead = true; break; }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            if (MODE == 2 && wave == 0 && !dead) {
+                uint32_t spins = 0;
+                while (__hip_atomic_load(ctr + op - 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (uint32_t) G) {
+                    if (++spins > kProbeSpin) { if (lane == 0) atomicOr(err, 1u); dead = true; break; }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            if (MODE != 0) __syncthreads();
+            const int cnt = tid < n ? (n - tid + 511) / 512 : 0;
+            uint64_t v[kProbeMaxWords];
+#pragma unroll
+            for (int k = 0; k < kProbeMaxWords; k++)
+                if (k < cnt) v[k] = __hip_atomic_load(src + tid + k * 512, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint32_t spins = 0;
+            while (!dead) {
+                bool ok = true;
+#pragma unroll
+                for (int k = 0; k < kProbeMaxWords; k++)
+                    if (k < cnt && (uint32_t) (v[k] >> 32) != want) ok = false;
+                if (ok) break;
+                if (++spins > kProbeSpin) { atomicOr(err, 2u); dead = true; break; }
+                __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+                for (int k = 0; k < kProbeMaxWords; k++)
+                    if (k < cnt && (uint32_t) (v[k] >> 32) != want)
+                        v[k] = __hip_atomic_load(src + tid + k * 512, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            uint32_t part = 0;
+#pragma unroll
+            for (int k = 0; k < kProbeMaxWords; k++)
+                if (k < cnt) part += (uint32_t) v[k];
+            for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+            if (lane == 0) red[wave] = part;
+            __syncthreads();
+            s = 0;
+            for (int w = 0; w < 8; w++) s += red[w];
+            __syncthreads();
+        }
+        const int lo = (int) ((long) wg * n / G), hi = (int) ((long) (wg + 1) * n / G);
+        uint64_t * dst = buf + (size_t) op * n;
+        const uint32_t ep = base + (uint32_t) op + 1u;
+        if (lo + tid < hi)
+            __hip_atomic_store(dst + lo + tid, ((uint64_t) ep << 32) | (uint32_t) (s * 31u + (uint32_t) (lo + tid)),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (MODE == 2) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __syncthreads();
+            if (tid == 0) __hip_atomic_fetch_add(ctr + op, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (wg == 0 && tid == 0) out[0] = s;
+}
+
 }  // namespace sparkmv
 
 using namespace sparkmv;
@@ -262,6 +355,77 @@ int sparkmv_probe_startup(const size_t * sizes, int nsizes, int reps, double * o
     (void) hipFree(sink);
     for (int k = 0; k < 6 + 3 * nsizes; k++)
         if (out_us[k] < 0) { set_error("probe: a timing event failed"); rc = -1; }
+    return rc;
+}
+
+/* Dependent handoffs over every workgroup (see probe_handoff_kernel): for
+ * each mode (0 epoch-carrying words, 1 the same behind a per-producer
+ * sentinel, 2 fence + counter) and each word count in nwords (up to 5120),
+ * the µs per dependent op of a 400-op launch minus a 1-op launch, best of 5:
+ * out_us[mode * nn + i]. The chain's result is checked against its closed
+ * form; -1 on a mismatch or a wait that gave up. Needs the device to itself
+ * (one workgroup per CU, all resident). */
+int sparkmv_probe_handoff(const int * nwords, int nn, double * out_us) {
+    if (!nwords || nn < 1 || nn > 8 || !out_us) { set_error("probe handoff: 1..8 word counts and an output array"); return -1; }
+    for (int i = 0; i < nn; i++)
+        if (nwords[i] < 256 || nwords[i] > 512 * kProbeMaxWords) {
+            set_error("probe handoff: word counts are 256..%d, not %d", 512 * kProbeMaxWords, nwords[i]);
+            return -1;
+        }
+    const int G = cu_count(), K = 400;
+    uint64_t * buf = nullptr;
+    uint32_t *ctr = nullptr, *err = nullptr, *out = nullptr;
+    const size_t nbuf = (size_t) K * 512 * kProbeMaxWords;
+    hipError_t e = hipMalloc((void **) &buf, nbuf * 8);
+    if (e == hipSuccess) e = hipMalloc((void **) &ctr, 4 * (size_t) K);
+    if (e == hipSuccess) e = hipMalloc((void **) &err, 4);
+    if (e == hipSuccess) e = hipMalloc((void **) &out, 4);
+    if (e == hipSuccess) e = hipMemset(buf, 0, nbuf * 8);
+    if (e == hipSuccess) e = hipMemset(err, 0, 4);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    int rc = e == hipSuccess ? 0 : fail_hip("probe handoff setup", e);
+    uint32_t base = 1;
+    Timer t;
+    auto run = [&](int mode, int n, int k) -> double {
+        if (hipMemset(ctr, 0, 4 * (size_t) K) != hipSuccess) return -1.0;
+        if (hipEventRecord(t.a, nullptr) != hipSuccess) return -1.0;
+        const size_t lds = 96 * 1024;   /* one workgroup per CU */
+        if (mode == 0) hipLaunchKernelGGL(probe_handoff_kernel<0>, dim3(G), dim3(512), lds, nullptr, buf, ctr, n, k, base, err, out);
+        if (mode == 1) hipLaunchKernelGGL(probe_handoff_kernel<1>, dim3(G), dim3(512), lds, nullptr, buf, ctr, n, k, base, err, out);
+        if (mode == 2) hipLaunchKernelGGL(probe_handoff_kernel<2>, dim3(G), dim3(512), lds, nullptr, buf, ctr, n, k, base, err, out);
+        if (hipGetLastError() != hipSuccess || hipEventRecord(t.b, nullptr) != hipSuccess ||
+            hipEventSynchronize(t.b) != hipSuccess)
+            return -1.0;
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, t.a, t.b) != hipSuccess) return -1.0;
+        uint32_t h[2] = {0, 0};
+        if (hipMemcpy(h, out, 4, hipMemcpyDeviceToHost) != hipSuccess || hipMemcpy(h + 1, err, 4, hipMemcpyDeviceToHost) != hipSuccess)
+            return -1.0;
+        uint32_t want = 0;
+        for (int op = 1; op < k; op++) want = (uint32_t) n * 31u * want + (uint32_t) ((uint64_t) n * (n - 1) / 2);
+        base += (uint32_t) k + 1u;
+        if (h[1] || h[0] != want) return -2.0;
+        return 1000.0 * ms;
+    };
+    for (int mode = 0; mode < 3 && !rc; mode++)
+        for (int i = 0; i < nn && !rc; i++) {
+            const int n = nwords[i];
+            double best = 1e30, best1 = 1e30;
+            for (int r = 0; r < 5 && !rc; r++) {
+                const double a = run(mode, n, K), b = run(mode, n, 1);
+                if (a < 0 || b < 0) {
+                    rc = -1;
+                    set_error(a == -2.0 || b == -2.0 ? "probe handoff: a chain's result or wait failed" : "probe handoff: a launch failed");
+                }
+                best = std::min(best, a);
+                best1 = std::min(best1, b);
+            }
+            out_us[mode * nn + i] = (best - best1) / (K - 1);
+        }
+    (void) hipFree(buf);
+    (void) hipFree(ctr);
+    (void) hipFree(err);
+    (void) hipFree(out);
     return rc;
 }
 

@@ -149,6 +149,7 @@ SIGNATURES = {
     "sparkmv_chain_op_shape": (_I, [_P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "sparkmv_chain_trace": (_I, [_P, _P, ctypes.c_long]),
     "sparkmv_probe_startup": (_I, [ctypes.POINTER(_S), _I, _I, _D]),
+    "sparkmv_probe_handoff": (_I, [ctypes.POINTER(_I), _I, _D]),
     "sparkmv_gguf_open": (_P, [ctypes.c_char_p]),
     "sparkmv_gguf_close": (None, [_P]),
     "sparkmv_gguf_version": (_I, [_P]),
@@ -1145,6 +1146,17 @@ def probe_startup(sizes=(8 << 20, 20 << 20, 40 << 20), reps=20):
     for i, b in enumerate(sizes):
         res[int(b)] = {"cold": out[3 + 3 * i], "page_warm": out[4 + 3 * i], "line_warm": out[5 + 3 * i]}
     return res
+
+
+def probe_handoff(nwords=(1280, 2560, 5120)):
+    """µs per dependent op over every workgroup (sparkmv_probe_handoff):
+    {"epoch_words" | "sentinel" | "fence_counter": {n: us}}."""
+    n = len(nwords)
+    arr = (_I * n)(*nwords)
+    out = (ctypes.c_double * (3 * n))()
+    check(lib().sparkmv_probe_handoff(arr, n, out), "probe handoff")
+    return {name: {int(w): out[m * n + i] for i, w in enumerate(nwords)}
+            for m, name in enumerate(("epoch_words", "sentinel", "fence_counter"))}
 
 
 # The decode token's matvecs in the order the forward issues them
