@@ -214,7 +214,7 @@ int sparkmv_vq_prefill(const void * const * stages, int nstages, int dim, int nc
  * exceed it fails with a message saying how many bytes it needs. Every call
  * on one GPU shares that GPU's array: calls that overlap on one GPU (on
  * different streams, or from different threads) race. The first call on a
- * device looks the array's address up once. */
+ * device looks the array's address up once, under a lock. */
 int sparkmv_vq_prefill_noalloc(const void * const * stages, int nstages, int dim, int nc, int rows, int cols, int v3,
                                const void * x, int x_dtype, int ldx, int ntok, float * y, int ldy,
                                int accumulate, void * stream);

@@ -398,6 +398,17 @@ __global__ __launch_bounds__(W * 64) void vq_chain_kernel(const ChainOp * __rest
                 for (int k = 0; k < NXK; k++) xw[k] = xp[min(k * NT + tid, nxw - 1)];
             }
         }
+        /* the norm's weights with x (they do not depend on it), so that no
+         * load falls between x's arrival and its staging; a norm without
+         * weights (a null pointer) multiplies by 1 */
+        float nv[NXK];
+#pragma unroll
+        for (int k = 0; k < NXK; k++) nv[k] = 1.0f;
+        if (stages_x && O.xmode == kXNorm && O.nw) {
+            const gptr<const float> nwp = gpin(O.nw);
+#pragma unroll
+            for (int k = 0; k < NXK; k++) nv[k] = nwp[min(k * NT + tid, nxw - 1)];
+        }
         stamp(i, 7);
 
         /* cursor B: the next op's first steps */
@@ -464,13 +475,14 @@ __global__ __launch_bounds__(W * 64) void vq_chain_kernel(const ChainOp * __rest
          * constants now, so no wait for them falls after the steps, whose
          * refills of the next op's index words are then in flight */
         asm volatile("" : "+v"(gr[0]), "+v"(gr[1]), "+v"(gr[2]), "+v"(gr[3]), "+v"(yword), "+v"(yplain));
+#pragma unroll
+        for (int k = 0; k < NXK; k++) asm volatile("" : "+v"(nv[k]));
         const float g00 = chain_f16((uint16_t) gr[0]), g01 = chain_f16((uint16_t) gr[1]);
         const float g10 = chain_f16((uint16_t) gr[2]), g11 = chain_f16((uint16_t) gr[3]);
         int xk = 0;
         uint32_t xb[NXK];   /* bf16 per word (f32 sources) or bf16 pairs */
         if (stages_x) {
             const int xmode = pin(O.xmode);
-            const gptr<const float> nw = xmode == kXNorm ? gpin(O.nw) : nullptr;
             const gptr<uint16_t> xo = wg == 0 ? gpin(O.xout) : nullptr;
             float inv = 1.0f;
             if (xmode == kXNorm) {
@@ -481,9 +493,6 @@ __global__ __launch_bounds__(W * 64) void vq_chain_kernel(const ChainOp * __rest
             }
             uint32_t xm = 0;
             if (f32v) {
-                float nv[NXK];
-#pragma unroll
-                for (int k = 0; k < NXK; k++) nv[k] = nw ? nw[min(k * NT + tid, nxw - 1)] : 1.0f;
 #pragma unroll
                 for (int k = 0; k < NXK; k++) {
                     const int wi = k * NT + tid;

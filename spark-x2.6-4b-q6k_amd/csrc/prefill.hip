@@ -24,6 +24,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 namespace sparkmv {
 
@@ -777,10 +778,12 @@ static __device__ __align__(256) float scratch[kPrefillScratchBytes / sizeof(flo
 
 int prefill_scratch(void ** ptr) {
     static void * addr[64] = {};
+    static std::mutex mu;   /* the first calls on a device may come from several threads */
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail_hip("get device", e);
     if (dev < 0 || dev >= 64) { set_error("device %d is outside the scratch table", dev); return -1; }
+    std::lock_guard<std::mutex> hold(mu);
     if (!addr[dev]) {
         void * p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
@@ -796,10 +799,12 @@ int prefill_scratch(void ** ptr) {
  * kept between calls), one per device */
 static int cw_workspace(size_t bytes, hipStream_t s, void ** out) {
     static hipMemPool_t pools[64] = {};
+    static std::mutex mu;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail_hip("get device", e);
     if (dev < 0 || dev >= 64) { set_error("device %d is outside the pool table", dev); return -1; }
+    std::unique_lock<std::mutex> hold(mu);
     if (!pools[dev]) {
         hipMemPoolProps props;
         memset(&props, 0, sizeof props);
@@ -814,7 +819,9 @@ static int cw_workspace(size_t bytes, hipStream_t s, void ** out) {
         if (e != hipSuccess) return fail_hip("memory pool attribute", e);
         pools[dev] = p;
     }
-    e = hipMallocFromPoolAsync(out, bytes, pools[dev], s);
+    hipMemPool_t pool = pools[dev];
+    hold.unlock();
+    e = hipMallocFromPoolAsync(out, bytes, pool, s);
     return e == hipSuccess ? 0 : fail_hip("split workspace", e);
 }
 
