@@ -774,8 +774,9 @@ def bench_startup(args, sm, torch, dev):
     staging alone, and plain reads of 8, 20 and 40 MB (about o, down and
     gate+up) cold, with address translation warm (one dword per 4 KB page
     read just before) and with the data warm (one dword per 64-byte line);
-    then what a dependent op costs inside one launch instead
-    (sparkmv_probe_handoff), three ways."""
+    then the decode set's 145 launches as plain reads of their byte counts in
+    one graph (sparkmv_probe_read_chain), and what a dependent op costs
+    inside one launch instead (sparkmv_probe_handoff), three ways."""
     sizes = (8 << 20, 20 << 20, 40 << 20)
     res = sm.probe_startup(sizes, reps=max(5, min(args.steps, 64)))
     out = {"empty_kernel_us": round(res["empty"], 2), "empty_kernel_1wave_us": round(res["empty_1wave"], 2),
@@ -790,6 +791,22 @@ def bench_startup(args, sm, torch, dev):
         out["reads"][f"{mb}MB"]["cold_gbps"] = round(b / (r["cold"] * 1e-6) / 1e9, 1)
         log(f"  read {mb} MB: cold {r['cold']:.2f} us ({b / (r['cold'] * 1e-6) / 1e9:.0f} GB/s), translation warm "
             f"{r['page_warm']:.2f} us, data warm {r['line_warm']:.2f} us")
+    # the decode set's 145 launches as plain reads of the same byte counts
+    # (one layer's containers give every layer's sizes), back to back in one
+    # graph: the floor of one launch per matvec with no compute
+    hosts = gen_layer(sm, 0)
+    layer = []
+    for grp in range(4):
+        idx = [i for i, m in enumerate(LAYER_MATS) if m[3] == grp]
+        layer.append(sum(algorithmic_bytes_vq(hosts[i].nbytes, LAYER_MATS[i][1], LAYER_MATS[i][2]) for i in idx))
+    head = VOCAB * (HIDDEN // 32) * 34 + 2 * HIDDEN + 4 * VOCAB
+    chain = layer * LAYERS + [head]
+    rc = sm.probe_read_chain(chain, reps=max(5, min(args.steps, 64)))
+    out["read_chain"] = {"launches": len(chain), "bytes": int(sum(chain)), "per_layer_bytes": layer, "head_bytes": head,
+                         "graph_us": round(rc["graph_us"], 1), "stream_us": round(rc["stream_us"], 1),
+                         "graph_gbps": round(sum(chain) / (rc["graph_us"] * 1e-6) / 1e9, 1)}
+    log(f"  the decode set's {len(chain)} launches as plain reads ({sum(chain) / 1e9:.3f} GB): "
+        f"{rc['graph_us']:.1f} us per graph replay, {rc['stream_us']:.1f} us eager")
     hand = sm.probe_handoff((1280, 2560, 5120))
     out["handoff_us_per_op"] = {k: {str(n): round(v, 2) for n, v in d.items()} for k, d in hand.items()}
     for k, d in hand.items():

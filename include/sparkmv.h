@@ -273,10 +273,15 @@ int sparkmv_plan_op_kernel(void * plan, int i, int * variant, int * threads);
 /* ---- decode chain: the per-token matvec chain as ONE persistent launch ----
  * Replaces the launch-by-launch chain of tools/vq/gpu/vq-model-gpu.cu:776-835
  * (gemv calls :795-833; rms_norm :364-380, gelu-mul :404-414 between them)
- * with one launch of one workgroup per CU that walks the op list. An op
- * that waits (wait = 1) reads only what every earlier op has published:
- * the dependency between matvecs is a device-scope flag per workgroup,
- * polled with bounded waits. Each op's input transform runs inside its
+ * with one launch of one workgroup per CU that walks the op list. Every
+ * output that a later op of the chain reads (found at build time by matching
+ * pointers) is also published as 8-byte words {payload, epoch}, each written
+ * with one agent-scope store; the reader's load of its words is its wait (it
+ * reloads the words whose epoch is not yet current, with a bounded spin). So
+ * every read of chain-produced data, x or addend, waits for exactly its own
+ * words, and `wait` is accepted and ignored. An input that only partly
+ * overlaps an earlier op's output, or an output over an earlier op's
+ * external input, is refused at build. Each op's input transform runs inside its
  * staging: x_mode 0 takes bf16 x as is, 1 rounds f32 x to bf16, 2 applies
  * rms_norm to f32 x (f64 sum of squares, tools/vq-runtime/src/model.rs:236-245;
  * norm_w may be NULL for weight 1) and rounds to bf16. Each matrix writes
@@ -285,7 +290,7 @@ int sparkmv_plan_op_kernel(void * plan, int i, int * variant, int * threads);
  * and act[r] = bf16(gelu(y0[r]) * y1[r]) with exact-erf gelu (model.rs:253-258).
  * x_out, when set, receives the staged bf16 x (the op's actual input).
  * Geometry: DQV3, dim 4, two stages, 12-bit indices (an even nc of 2050..4096), columns a multiple
- * of 128 up to 16384, 4-byte aligned stages. A chain needs the device to
+ * of 128 up to 12288 (bf16 x) or 6144 (f32 x, norm), 4-byte aligned stages. A chain needs the device to
  * itself while it runs (every workgroup resident at once); the launch is
  * asynchronous and can be captured into a HIP graph. */
 typedef struct {
@@ -310,8 +315,8 @@ int sparkmv_chain_add_vq(void * chain, const sparkmv_chain_matrix * mats, int nm
 int sparkmv_chain_add_norm(void * chain, const float * x, int n, const float * norm_w, float eps, uint16_t * out,
                            int wait);
 int sparkmv_chain_launch(void * chain, void * stream);
-/* 0, or -1 if a wait of any launch so far gave up (flags are then cleared);
- * synchronizes the device. */
+/* 0, or -1 if a wait of any launch so far gave up (the error word is then
+ * cleared); synchronizes the device. */
 int sparkmv_chain_status(void * chain);
 /* Phase trace of later launches into buf (device memory, NULL = off): per
  * workgroup w and op i, buf[(w * ops + i) * 10 + k] holds the 100 MHz clock
@@ -349,6 +354,13 @@ int sparkmv_probe_startup(const size_t * sizes, int nsizes, int reps, double * o
  * µs per op of a 400-op chain minus a 1-op chain, best of 5. No counterpart
  * in the reference. Needs the device to itself; synchronizes it. */
 int sparkmv_probe_handoff(const int * nwords, int nn, double * out_us);
+/* The floor of one launch per matvec with no compute: n plain reads of
+ * sizes[i] bytes (4 KB..1 GB each, 16 GB in all), each from its own region,
+ * on the hot kernel's launch shape, back to back as one captured HIP graph
+ * (out_us[0], µs per replay) and eagerly on a stream (out_us[1], µs per
+ * pass), medians of reps (3..64). No counterpart in the reference.
+ * Allocates and frees its own buffer; synchronizes the device. */
+int sparkmv_probe_read_chain(const size_t * sizes, int n, int reps, double * out_us);
 
 /* ---- weight artifacts (host memory) ----
  * GGUF v2/v3 (ggml's layout), the reader of tools/dspark/src/gguf.rs:95-190

@@ -429,4 +429,87 @@ int sparkmv_probe_handoff(const int * nwords, int nn, double * out_us) {
     return rc;
 }
 
+/* The floor of one launch per matvec: n plain reads (probe_read_kernel on
+ * the hot kernel's launch shape) of sizes[i] bytes each, every read its own
+ * region of one buffer, back to back as one captured HIP graph and eagerly
+ * on a stream. out_us[0] = µs per graph replay, out_us[1] = µs per eager
+ * pass (wall time between two plain events, median of reps). With the
+ * decode set's byte counts (3.27 GB, beyond the 256 MB memory-side cache)
+ * every replay reads cold, as a token does. */
+int sparkmv_probe_read_chain(const size_t * sizes, int n, int reps, double * out_us) {
+    if (!sizes || n < 1 || n > 1024 || reps < 3 || reps > 64 || !out_us) {
+        set_error("probe read chain: 1..1024 sizes, 3..64 repetitions and an output array");
+        return -1;
+    }
+    std::vector<size_t> off(n + 1, 0);
+    for (int i = 0; i < n; i++) {
+        if (sizes[i] < 4096 || sizes[i] > ((size_t) 1 << 30)) {
+            set_error("probe read chain: sizes from 4 KB to 1 GB, not %zu", sizes[i]);
+            return -1;
+        }
+        off[i + 1] = off[i] + ((sizes[i] + 255) & ~(size_t) 255);
+    }
+    if (off[n] > ((size_t) 16 << 30)) { set_error("probe read chain: more than 16 GB in all"); return -1; }
+    const int G = cu_count();
+    uint8_t * buf = nullptr;
+    uint32_t * sink = nullptr;
+    hipStream_t cs = nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t gx = nullptr;
+    hipError_t e = hipMalloc((void **) &buf, off[n]);
+    if (e == hipSuccess) e = hipMalloc((void **) &sink, 4 * (size_t) G);
+    if (e == hipSuccess) e = hipMemset(sink, 0, 4 * (size_t) G);
+    if (e == hipSuccess) e = hipMemset(buf, 1, off[n]);
+    if (e == hipSuccess) e = hipStreamCreate(&cs);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    const dim3 grid(G), block(kProbeThreads);
+    auto pass = [&]() {
+        for (int i = 0; i < n; i++)
+            hipLaunchKernelGGL(probe_read_kernel, grid, block, 0, cs, (const uint4 *) (buf + off[i]), sizes[i] / 16,
+                               sink);
+    };
+    if (e == hipSuccess) e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        pass();
+        e = hipStreamEndCapture(cs, &g);
+    }
+    if (e == hipSuccess) e = hipGraphInstantiate(&gx, g, nullptr, nullptr, 0);
+    int rc = 0;
+    if (e == hipSuccess) {
+        Timer t;
+        auto wall = [&](bool graph) -> double {
+            std::vector<double> w;
+            if (graph) (void) hipGraphLaunch(gx, cs);   /* the first replay uploads the graph */
+            else pass();
+            if (hipStreamSynchronize(cs) != hipSuccess) return -1.0;
+            for (int r = 0; r < reps; r++) {
+                if (hipEventRecord(t.a, cs) != hipSuccess) return -1.0;
+                if (graph) {
+                    if (hipGraphLaunch(gx, cs) != hipSuccess) return -1.0;
+                } else {
+                    pass();
+                }
+                if (hipEventRecord(t.b, cs) != hipSuccess || hipEventSynchronize(t.b) != hipSuccess) return -1.0;
+                float ms = 0.f;
+                if (hipEventElapsedTime(&ms, t.a, t.b) != hipSuccess) return -1.0;
+                w.push_back(1000.0 * ms);
+            }
+            return median(w);
+        };
+        out_us[0] = wall(true);
+        out_us[1] = wall(false);
+        if (out_us[0] < 0 || out_us[1] < 0) { set_error("probe read chain: a timing event failed"); rc = -1; }
+    } else {
+        rc = fail_hip("probe read chain setup", e);
+    }
+    if (gx) (void) hipGraphExecDestroy(gx);
+    if (g) (void) hipGraphDestroy(g);
+    if (cs) (void) hipStreamDestroy(cs);
+    e = hipDeviceSynchronize();
+    if (!rc && e != hipSuccess) rc = fail_hip("probe read chain", e);
+    if (buf) (void) hipFree(buf);
+    if (sink) (void) hipFree(sink);
+    return rc;
+}
+
 }  // extern "C"

@@ -150,6 +150,7 @@ SIGNATURES = {
     "sparkmv_chain_trace": (_I, [_P, _P, ctypes.c_long]),
     "sparkmv_probe_startup": (_I, [ctypes.POINTER(_S), _I, _I, _D]),
     "sparkmv_probe_handoff": (_I, [ctypes.POINTER(_I), _I, _D]),
+    "sparkmv_probe_read_chain": (_I, [ctypes.POINTER(ctypes.c_size_t), _I, _I, _D]),
     "sparkmv_gguf_open": (_P, [ctypes.c_char_p]),
     "sparkmv_gguf_close": (None, [_P]),
     "sparkmv_gguf_version": (_I, [_P]),
@@ -1157,6 +1158,17 @@ def probe_handoff(nwords=(1280, 2560, 5120)):
     check(lib().sparkmv_probe_handoff(arr, n, out), "probe handoff")
     return {name: {int(w): out[m * n + i] for i, w in enumerate(nwords)}
             for m, name in enumerate(("epoch_words", "sentinel", "fence_counter"))}
+
+
+def probe_read_chain(sizes, reps=10):
+    """The floor of one launch per matvec with no compute
+    (sparkmv_probe_read_chain): plain reads of the given byte counts back to
+    back, {"graph_us": per replay, "stream_us": per eager pass}."""
+    n = len(sizes)
+    arr = (ctypes.c_size_t * n)(*sizes)
+    out = (ctypes.c_double * 2)()
+    check(lib().sparkmv_probe_read_chain(arr, n, reps, out), "probe read chain")
+    return {"graph_us": out[0], "stream_us": out[1]}
 
 
 # The decode token's matvecs in the order the forward issues them
