@@ -422,6 +422,52 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
 #pragma unroll
             for (int k = 0; k < KS; k++)
                 ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+    } else if constexpr (MSC > 0 && XF32) {
+        /* One 16-byte aligned f32 activation column of at most 16 * blockDim
+         * columns, each value split into f16 hi + lo (hi in the column's
+         * slot, lo in the next one), and an even codebook of at most KS
+         * chunks per thread and stage, staged as in the bf16 form below. */
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
+        constexpr int KX = 4;                      /* 16-byte x chunks (4 columns) per thread */
+        constexpr int KS = 5;
+        const int xq = A.cols >> 2;
+        u4v cv[NST][KS];
+        u4v xv[KX];
+#pragma unroll
+        for (int s = 0; s < NST; s++)
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+                cv[s][k] = ((const u4a *) (stp[s] + 24))[min(k * bd + tid, n16 - 1)];
+#pragma unroll
+        for (int k = 0; k < KX; k++) xv[k] = ((const u4v *) A.x)[min(k * bd + tid, xq - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        point(first);
+        ld_gains(first);
+        ld_head();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < NST; s++)
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+                ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+#pragma unroll
+        for (int k = 0; k < KX; k++) {
+            const int e = 4 * min(k * bd + tid, xq - 1);
+            const int off = 264 * (e >> 7) + 2 * (e & 127);
+            h4 hi4, lo4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float f = __uint_as_float(xv[k][j]);
+                hi4[j] = (_Float16) f;
+                lo4[j] = (_Float16) (f - (float) hi4[j]);
+                xm = max(xm, xr_mag_f32w(xv[k][j]));
+            }
+            *(h4 *) (lx + off) = hi4;
+            *(h4 *) (lx + A.xstride + off) = lo4;
+        }
     } else if constexpr (MSC > 0) {
         /* One 16-byte aligned activation column of at most 16 * blockDim
          * columns and an even codebook of at most KS chunks per thread and
@@ -1170,6 +1216,16 @@ static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, 
             case 10: if (!EXT) return launch_fast_t<NST, 0, EXT, EXT ? 0 : 10>(A, grid, threads, lds, s); break;
             default: break;
         }
+    } else if (!mc) {
+        /* f32 x, one column: the trunk's unit lengths run straight-line too
+         * (x as hi + lo f16 in LDS, two MFMAs per step) */
+        switch (MS) {
+            case 2: return launch_fast_t<NST, 1, EXT, 2>(A, grid, threads, lds, s);
+            case 5: return launch_fast_t<NST, 1, EXT, 5>(A, grid, threads, lds, s);
+            case 8: return launch_fast_t<NST, 1, EXT, 8>(A, grid, threads, lds, s);
+            case 10: if (!EXT) return launch_fast_t<NST, 1, EXT, EXT ? 0 : 10>(A, grid, threads, lds, s); break;
+            default: break;
+        }
     }
     return launch_fast_t<NST, XF32, EXT, 0>(A, grid, threads, lds, s);
 }
@@ -1246,15 +1302,16 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     }
     const int threads = sh.W * 64;
     A.threads = threads;
-    /* The straight-line kernels take bf16 x and an even codebook. One column
-     * is staged in one branch-free pass and reduced within a wave: 16-byte
-     * aligned x of at most 16 * threads values, one wave per tile, at most 5
-     * codebook chunks per thread and stage. Several columns are staged by
-     * loops before the index words are requested. */
+    /* The straight-line kernels take an even codebook, and bf16 x or one
+     * column of f32 x. One column is staged in one branch-free pass and
+     * reduced within a wave: 16-byte aligned x of at most 16 * threads
+     * values, one wave per tile, at most 5 codebook chunks per thread and
+     * stage. Several bf16 columns are staged by loops before the index words
+     * are requested. */
     const int n16 = c.nc * 8 / 16;
     const int one_col = sh.C == 1 && !((uintptr_t) A.x & 15u) && n16 <= 5 * threads && part.cols <= 16 * threads;
     const int multi_col = c.ncol > 1 && !((uintptr_t) A.x & 15u) && c.ldx % 8 == 0 && n16 <= 5 * threads;
-    const int straight = !c.xf32 && c.nc % 2 == 0 && (c.ncol > 1 ? multi_col : one_col);
+    const int straight = (!c.xf32 || c.ncol == 1) && c.nc % 2 == 0 && (c.ncol > 1 ? multi_col : one_col);
     const int MS = sh.xg ? A.M / sh.S / sh.C : straight ? A.M / sh.S / sh.C : 0;
     /* the multi-column kernels: x from global memory (2) or staged in LDS (1;
      * MS without its own instantiation runs their ring form); any other

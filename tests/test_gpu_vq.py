@@ -506,3 +506,35 @@ def test_full_size_ffn_up(sm, ref, dev):
     out = torch.zeros(rows, cols, device=dev)
     dc.dequant(out)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), W.view(np.uint32))
+
+
+TRUNK_F32 = [
+    # (matrix rows, ...), cols: the decode layer's launches with f32 x
+    ((4096, 1024, 1024, 16), 2560),   # q + k + v + head gate, one launch
+    ((2560,), 4096),                  # o
+    ((10240, 10240), 2560),           # gate + up, one launch
+    ((10240,), 2560),                 # gate alone
+    ((2560,), 10240),                 # down
+]
+
+
+@pytest.mark.parametrize("shapes,cols", TRUNK_F32, ids=["qkvg", "o", "gate_up", "gate", "down"])
+def test_f32_x_at_trunk_shapes(sm, ref, dev, shapes, cols):
+    """f32 activations (the reference's arithmetic: x split into f16 hi + lo,
+    two MFMAs per step) at the decode layer's real launch shapes, whose
+    one-column shapes run the straight-line units of 2, 5 and 10 macro
+    steps; every row against the oracle's decode times x in f64, within
+    1e-5, with y filled with NaN first so every row must be written."""
+    import torch
+    datas = [sm.synth_container(0xF320 + 7 * i + cols, r, cols) for i, r in enumerate(shapes)]
+    mats = [sm.DeviceContainer(d, dev) for d in datas]
+    xt, xf = _x(sm, 0xF32 + cols, 1, cols, True)
+    ys = [torch.full((1, max(shapes)), float("nan"), device=dev) for _ in shapes]
+    print(f"f32 x: rows {shapes} x {cols}", flush=True)
+    sm.gemv_multi(mats, xt, ys)
+    torch.cuda.synchronize()
+    for d, y, r in zip(datas, ys, shapes):
+        W = ref.decode(d).astype(np.float64)
+        err = rel_l2(y[0, :r].cpu().numpy(), W @ xf[0].astype(np.float64))
+        print(f"  {r} rows: relL2 {err:.2e}")
+        assert err <= TIGHT, (r, err)
