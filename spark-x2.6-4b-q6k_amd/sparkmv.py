@@ -150,7 +150,7 @@ SIGNATURES = {
     "sparkmv_chain_trace": (_I, [_P, _P, ctypes.c_long]),
     "sparkmv_probe_startup": (_I, [ctypes.POINTER(_S), _I, _I, _D]),
     "sparkmv_probe_handoff": (_I, [ctypes.POINTER(_I), _I, _D]),
-    "sparkmv_probe_read_chain": (_I, [ctypes.POINTER(ctypes.c_size_t), _I, _I, _D]),
+    "sparkmv_probe_read_chain": (_I, [ctypes.POINTER(_S), _I, _I, _D]),
     "sparkmv_gguf_open": (_P, [ctypes.c_char_p]),
     "sparkmv_gguf_close": (None, [_P]),
     "sparkmv_gguf_version": (_I, [_P]),

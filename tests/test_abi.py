@@ -233,6 +233,33 @@ def test_chain_refusals(sm):
         sm.lib().sparkmv_chain_destroy(h)
 
 
+def test_probe_refusals(sm):
+    """The measurement entries refuse what they cannot time before any device
+    call: too many or too few sizes, sizes outside their range, repetitions
+    outside 3..64, word counts outside 256..5120, and a missing output."""
+    import ctypes
+    L = sm.lib()
+    out = (ctypes.c_double * 64)()
+
+    def sizes(*v):
+        return (ctypes.c_size_t * len(v))(*v)
+
+    def words(*v):
+        return (ctypes.c_int * len(v))(*v)
+
+    for call, msg in ((lambda: L.sparkmv_probe_startup(sizes(1 << 20), 1, 2, out), "3..64 repetitions"),
+                      (lambda: L.sparkmv_probe_startup(sizes(1000), 1, 5, out), "from 64 KB to 1 GB"),
+                      (lambda: L.sparkmv_probe_startup(sizes(1 << 20), 1, 5, None), "output array"),
+                      (lambda: L.sparkmv_probe_read_chain(sizes(1 << 20), 0, 5, out), "1..1024 sizes"),
+                      (lambda: L.sparkmv_probe_read_chain(sizes(100), 1, 5, out), "from 4 KB to 1 GB"),
+                      (lambda: L.sparkmv_probe_read_chain(sizes(1 << 20), 1, 99, out), "3..64 repetitions"),
+                      (lambda: L.sparkmv_probe_read_chain(sizes(1 << 30, 1 << 30, 1 << 30), 3, 5, None), "output array"),
+                      (lambda: L.sparkmv_probe_handoff(words(2560), 0, out), "1..8 word counts"),
+                      (lambda: L.sparkmv_probe_handoff(words(100), 1, out), "256")):
+        assert call() == -1, msg
+        assert msg in sm.last_error(), (msg, sm.last_error())
+
+
 def test_handles_are_released_at_interpreter_exit(sm):
     """Objects still alive when the interpreter exits are destroyed without
     an error: their destructors use only the library they captured, not
