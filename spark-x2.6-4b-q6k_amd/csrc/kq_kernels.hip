@@ -523,33 +523,90 @@ __device__ __forceinline__ void lds_stream(const uint8_t * lds_base, uint32_t of
  * are a multiple of 4 bytes and at least 1 KB long, blocks 4-byte aligned
  * (the host checks). Every column gets the same arithmetic whatever the
  * column count. */
+/* One 32-weight unit u of the Q6_K row at LDS byte offset row (ggml's
+ * block_q6_K: ql, qh, scales, d), against ncol activation columns staged
+ * as f16 from LDS offset xoff: acc[n] += d * scale * (q . x) over its four
+ * 8-weight groups, in group order. */
 template <int NC, int XF32>
+__device__ __forceinline__ void q6k_unit(const uint8_t * lds, uint32_t row, int u, uint32_t xoff, int xst, int ncol,
+                                         float * acc) {
+    const int sb = u >> 3, h = (u >> 2) & 1, l0 = 8 * (u & 3);
+    const uint32_t blk = row + (uint32_t) sb * 210u;
+    uint32_t qa[2], qb[2], qc[2], scw[2], dw[1];
+    lds_stream<2>(lds, blk + 64 * h + l0, qa);
+    lds_stream<2>(lds, blk + 64 * h + 32 + l0, qb);
+    lds_stream<2>(lds, blk + 128 + 32 * h + l0, qc);
+    lds_stream<2>(lds, blk + 192 + 8 * h, scw);
+    lds_stream<1>(lds, blk + 208, dw);
+    const float d = kq_f16((uint16_t) dw[0]);
+    const int e0 = 256 * sb + 128 * h + l0;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int sci = (l0 >> 4) + 2 * g;
+        const float dsc = d * (float) (int) (int8_t) (scw[sci >> 2] >> (8 * (sci & 3)));
+        kq_h2 qv[4];
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const uint32_t lo = ((g & 1 ? qb[w] : qa[w]) >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
+            const uint32_t hi = ((qc[w] >> (2 * g)) & 0x03030303u) << 4;
+            bytes_to_h2(lo | hi, (_Float16) 1056.0f, qv[2 * w], qv[2 * w + 1]);
+        }
+        const int e = e0 + 32 * g;
+        const int xo = (e >> 5) * 72 + (e >> 7) * 8 + 2 * (e & 31);
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            if (n < ncol) {
+                const uint8_t * xp = lds + xoff + n * xst + xo;
+                float sacc = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 2; w++) {
+                    const kq_h4 xv = *(const kq_h4 *) (xp + 8 * w);
+                    sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xv[0], xv[1]}, sacc, false);
+                    sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xv[2], xv[3]}, sacc, false);
+                    if (XF32) {
+                        const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * w);
+                        sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xl[0], xl[1]}, sacc, false);
+                        sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xl[2], xl[3]}, sacc, false);
+                    }
+                }
+                acc[n] += dsc * sacc;
+            }
+        }
+    }
+}
+
+template <int NC, int XF32, int RPV>
 __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * blocks, int rows, int cols,
                                                                 const void * x, int ldx, int ncol, float * y, int ldy,
                                                                 int accumulate, int rpw) {
+    constexpr int rpv = RPV;
     typedef __attribute__((address_space(3))) void lds_void;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int bpr = cols / 256, units = 8 * bpr, xst = (cols / 32) * 72 + (cols / 128) * 8;
     const uint32_t rowbytes = (uint32_t) bpr * 210;
-    const int xw = (blockDim.x >> 6) - rpw;                    /* waves rpw .. stage x */
+    const int nrw = (rpw + rpv - 1) / rpv;                     /* waves with rows; waves nrw .. stage x */
+    const int xw = (blockDim.x >> 6) - nrw;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = blockIdx.x * rpw, nrow = min(rpw, rows - row0);
+    const int wr0 = wv * rpv, wnr = min(rpv, nrow - wr0);     /* this wave's first row in the workgroup, its row count */
     const uint32_t xoff = (uint32_t) ((rpw * rowbytes + 15) & ~15u);
-    const uint32_t reg = (uint32_t) wv * rowbytes;            /* this wave's row, a byte offset in LDS */
+    const uint32_t reg = (uint32_t) wr0 * rowbytes;           /* this wave's rows, a byte offset in LDS */
     uint32_t * xr = (uint32_t *) (lds + xoff + xr_off((XF32 ? 2 : 1) * ncol * xst));
     uint32_t xm = 0;
-    if (wv >= rpw) {
+    if (wv >= nrw) {
         /* x: the x waves' loads, LDS stores and range flags, complete
          * before the barrier */
-        xm = kq_stage_x_by<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst, threadIdx.x - 64 * rpw, 64 * xw);
+        xm = kq_stage_x_by<XF32, 1>(lds + xoff, x, ldx, ncol, cols, xst, threadIdx.x - 64 * nrw, 64 * xw);
         xr_note_f16(xr, xm);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    } else if (wv < nrow) {
-        const uint8_t * src = blocks + (size_t) (row0 + wv) * rowbytes;
-        const int nchunk = (int) ((rowbytes + 1023) >> 10);
+    } else if (wnr > 0) {
+        /* the wave's rows are contiguous, in memory and in LDS */
+        const uint32_t bytes = (uint32_t) wnr * rowbytes;
+        const uint8_t * src = blocks + (size_t) (row0 + wr0) * rowbytes;
+        const int nchunk = (int) ((bytes + 1023) >> 10);
         for (int b = 0; b < nchunk; b++) {
-            const uint32_t o = min((uint32_t) b * 1024u, rowbytes - 1024u);   /* the last chunk overlaps its neighbour */
+            const uint32_t o = min((uint32_t) b * 1024u, bytes - 1024u);   /* the last chunk overlaps its neighbour */
             __builtin_amdgcn_global_load_lds((const void *) (src + o + 16 * lane), (lds_void *) (lds + reg + o), 16, 0, 0);
         }
     }
@@ -558,66 +615,32 @@ __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * b
      * its row copy here. */
     asm volatile("s_barrier" ::: "memory");
     /* every wave takes the (uniform) range decision before any leaves */
-    const int xk = kq_x_range<XF32, 1>(lds + xoff, xr, x, ldx, ncol, cols, xst, rpw);
-    if (wv >= nrow) return;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* this wave's row */
+    const int xk = kq_x_range<XF32, 1>(lds + xoff, xr, x, ldx, ncol, cols, xst, nrw);
+    if (wnr <= 0) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* this wave's rows */
+    /* rpv rows per wave, each on L = 64 / rpv lanes; the lane l of its row's
+     * L takes units l, l + L, ..., k = rpv * units / 64 of them (the host
+     * picks rpv so that k is whole), so every lane has the same work. With
+     * one row per wave that is units lane, lane + 64, ... */
+    constexpr int L = 64 / RPV;
+    const int k = RPV * units / 64;
+    const int rl = lane / L, ul = lane - rl * L;
+    const bool live = rl < wnr;
+    const uint32_t rreg = reg + (uint32_t) (live ? rl : 0) * rowbytes;
     float acc[NC];
 #pragma unroll
     for (int n = 0; n < NC; n++) acc[n] = 0.0f;
-    for (int u = lane; u < units; u += 64) {
-        const int sb = u >> 3, h = (u >> 2) & 1, l0 = 8 * (u & 3);
-        const uint32_t blk = reg + (uint32_t) sb * 210u;
-        uint32_t qa[2], qb[2], qc[2], scw[2], dw[1];
-        lds_stream<2>(lds, blk + 64 * h + l0, qa);
-        lds_stream<2>(lds, blk + 64 * h + 32 + l0, qb);
-        lds_stream<2>(lds, blk + 128 + 32 * h + l0, qc);
-        lds_stream<2>(lds, blk + 192 + 8 * h, scw);
-        lds_stream<1>(lds, blk + 208, dw);
-        const float d = kq_f16((uint16_t) dw[0]);
-        const int e0 = 256 * sb + 128 * h + l0;
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int sci = (l0 >> 4) + 2 * g;
-            const float dsc = d * (float) (int) (int8_t) (scw[sci >> 2] >> (8 * (sci & 3)));
-            kq_h2 qv[4];
-#pragma unroll
-            for (int w = 0; w < 2; w++) {
-                const uint32_t lo = ((g & 1 ? qb[w] : qa[w]) >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
-                const uint32_t hi = ((qc[w] >> (2 * g)) & 0x03030303u) << 4;
-                bytes_to_h2(lo | hi, (_Float16) 1056.0f, qv[2 * w], qv[2 * w + 1]);
-            }
-            const int e = e0 + 32 * g;
-            const int xo = (e >> 5) * 72 + (e >> 7) * 8 + 2 * (e & 31);
-#pragma unroll
-            for (int n = 0; n < NC; n++) {
-                if (n < ncol) {
-                    const uint8_t * xp = lds + xoff + n * xst + xo;
-                    float sacc = 0.0f;
-#pragma unroll
-                    for (int w = 0; w < 2; w++) {
-                        const kq_h4 xv = *(const kq_h4 *) (xp + 8 * w);
-                        sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xv[0], xv[1]}, sacc, false);
-                        sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xv[2], xv[3]}, sacc, false);
-                        if (XF32) {
-                            const kq_h4 xl = *(const kq_h4 *) (xp + ncol * xst + 8 * w);
-                            sacc = __builtin_amdgcn_fdot2(qv[2 * w], kq_h2{xl[0], xl[1]}, sacc, false);
-                            sacc = __builtin_amdgcn_fdot2(qv[2 * w + 1], kq_h2{xl[2], xl[3]}, sacc, false);
-                        }
-                    }
-                    acc[n] += dsc * sacc;
-                }
-            }
-        }
-    }
+    if (live)
+        for (int i = 0; i < k; i++) q6k_unit<NC, XF32>(lds, rreg, ul + L * i, xoff, xst, ncol, acc);
 #pragma unroll
     for (int n = 0; n < NC; n++) {
         if (n < ncol) {
             float v = acc[n];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            for (int o = L >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
             v = xr_unscale(v, xk);
-            if (lane == 0) {
-                float * yp = y + (size_t) n * ldy + row0 + wv;
+            if (live && lane == rl * L) {
+                float * yp = y + (size_t) n * ldy + row0 + wr0 + rl;
                 *yp = (accumulate ? *yp : 0.0f) + v;
             }
         }
@@ -626,28 +649,53 @@ __global__ __launch_bounds__(1024) void q6k_gemv_staged_kernel(const uint8_t * b
 
 static inline const uint8_t * bp_in(const void * p) { return (const uint8_t *) p; }
 
+/* Rows per wave of the staged kernel: the fewest that give its 64 lanes a
+ * whole, equal number of 32-weight units (8 per 256 columns): 4 rows of
+ * 2560 columns (80 units each, 5 per lane), 1 of 4096 or 10240. */
+static int q6k_rows_per_wave(int cols) {
+    const int units = 8 * (cols / 256);
+    int g = 64;
+    while (units % g) g >>= 1;
+    return 64 / g;
+}
+
+template <int NC, int XF32, int RPV>
+static int kq_q6k_staged_k(const uint8_t * bp, int rows, int cols, const void * x, int ldx, int ncol, float * y,
+                           int ldy, int accumulate, int rpw, size_t lds, hipStream_t s) {
+    static size_t opted = 0;
+    const void * fn = (const void *) q6k_gemv_staged_kernel<NC, XF32, RPV>;
+    if (lds > 65536 && lds > opted) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return fail_hip("LDS opt-in for the staged Q6_K kernel", e);
+        opted = lds;
+    }
+    /* x waves: enough for one batch of eight 16-byte groups per lane, within 16 waves */
+    const int nrw = (rpw + RPV - 1) / RPV;
+    int xw = (ncol * cols + 4095) / 4096;
+    xw = xw < 1 ? 1 : (xw > 16 - nrw ? 16 - nrw : xw);
+    const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block((unsigned) (64 * (nrw + xw)));
+    launch_kernel(q6k_gemv_staged_kernel<NC, XF32, RPV>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y,
+                  ldy, accumulate, rpw);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail_hip("staged Q6_K launch", e);
+}
+
+template <int NC, int XF32>
+static int kq_q6k_staged_r(const uint8_t * bp, int rows, int cols, const void * x, int ldx, int ncol, float * y,
+                           int ldy, int accumulate, int rpw, size_t lds, hipStream_t s) {
+    switch (q6k_rows_per_wave(cols)) {
+        case 1: return kq_q6k_staged_k<NC, XF32, 1>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
+        case 2: return kq_q6k_staged_k<NC, XF32, 2>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
+        default: return kq_q6k_staged_k<NC, XF32, 4>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
+    }
+}
+
 template <int XF32>
 static int kq_q6k_staged_t(const uint8_t * bp, int rows, int cols, const void * x, int ldx, int ncol, float * y,
                            int ldy, int accumulate, int rpw, size_t lds, hipStream_t s) {
-    static size_t opted[3] = {0, 0, 0};
-    const int slot = ncol == 1 ? 0 : (ncol <= 4 ? 1 : 2);
-    const void * fn = slot == 0 ? (const void *) q6k_gemv_staged_kernel<1, XF32>
-                    : slot == 1 ? (const void *) q6k_gemv_staged_kernel<4, XF32>
-                                : (const void *) q6k_gemv_staged_kernel<16, XF32>;
-    if (lds > 65536 && lds > opted[slot]) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
-        if (e != hipSuccess) return fail_hip("LDS opt-in for the staged Q6_K kernel", e);
-        opted[slot] = lds;
-    }
-    /* x waves: enough for one batch of eight 16-byte groups per lane, within 16 waves */
-    int xw = (ncol * cols + 4095) / 4096;
-    xw = xw < 1 ? 1 : (xw > 16 - rpw ? 16 - rpw : xw);
-    const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block((unsigned) (64 * (rpw + xw)));
-    if (slot == 0) launch_kernel(q6k_gemv_staged_kernel<1, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw);
-    else if (slot == 1) launch_kernel(q6k_gemv_staged_kernel<4, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw);
-    else launch_kernel(q6k_gemv_staged_kernel<16, XF32>, grid, block, (uint32_t) lds, s, bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw);
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? 0 : fail_hip("staged Q6_K launch", e);
+    if (ncol == 1) return kq_q6k_staged_r<1, XF32>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
+    if (ncol <= 4) return kq_q6k_staged_r<4, XF32>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
+    return kq_q6k_staged_r<16, XF32>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
 }
 
 static int kq_q6k_staged(const uint8_t * bp, int rows, int cols, const void * x, int xf32, int ldx, int ncol, float * y,
@@ -694,9 +742,11 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
          * stages x, the rows' blocks and x within LDS */
         const size_t rowbytes = (size_t) (cols / 256) * 210;
         const size_t xbytes = (size_t) (xf32 ? 2 : 1) * ncol * ((cols / 32) * 72 + (cols / 128) * 8) + kXrBytes;
+        const int rpv = q6k_rows_per_wave(cols);
         int rpw = (rows + cu_count() - 1) / cu_count();
         rpw = rpw < 2 ? 2 : (rpw > 12 ? 12 : rpw);
-        while (rpw > 2 && ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes > 160 * 1024) rpw--;
+        rpw = (rpw + rpv - 1) / rpv * rpv;
+        while (rpw > rpv && ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes > 160 * 1024) rpw -= rpv;
         const size_t slds = ((rpw * rowbytes + 15) & ~(size_t) 15) + xbytes;
         if (slds <= 160 * 1024) {
             return kq_q6k_staged(bp_in(blocks), rows, cols, x, xf32, ldx, ncol, y, ldy, accumulate, rpw, slds, s);
