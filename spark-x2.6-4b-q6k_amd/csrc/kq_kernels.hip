@@ -10,9 +10,14 @@
  * integer factor at most 11 more), so the dequant kernels are bit-exact and the
  * GEMVs only round in the f32 accumulation.
  *
- * GEMV mapping: 16 lanes per row (a wave covers 4 rows), each lane a run of
- * blocks (Q8_0) or superblock halves (Q6_K) spaced 16 apart; partial sums meet
- * in a 16-lane butterfly. Blocks are 2-byte aligned, so a lane reads the
+ * Q8_0 runs on the matrix cores (q8_0_mfma_kernel) wherever rows are whole
+ * 512-column chunks in a 16-byte aligned buffer, for every column count, so
+ * the columns of a speculative verify equal one-column launches bit for bit;
+ * other shapes take the dot2 kernels below, again for every column count.
+ *
+ * Dot2 GEMV mapping: 16 lanes per row (a wave covers 4 rows), each lane a run
+ * of blocks (Q8_0) or superblock halves (Q6_K) spaced 16 apart; partial sums
+ * meet in a 16-lane butterfly. Blocks are 2-byte aligned, so a lane reads the
  * dword-aligned window around its bytes with dwordx4 loads and realigns with
  * v_alignbit; the window never leaves the block except where the next
  * block's bytes follow, and the buffer's final block reads only its own bytes.
@@ -21,6 +26,8 @@
 #include "xrange.h"
 
 #include <string.h>
+
+#include <atomic>
 
 namespace sparkmv {
 
@@ -53,6 +60,20 @@ __device__ __forceinline__ void load_stream(const uint8_t * addr, uint32_t * out
     if (sh && last_ok) w[N] = p[N];
     else if (sh) w[N] = (uint32_t) *(gu16 *) (p + N);
     else w[N] = 0;
+#pragma unroll
+    for (int k = 0; k < N; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+}
+
+/* N dwords of LDS bytes from byte `off` of the shared array (2-byte
+ * aligned): the covering aligned dwords, funnel-shifted. Offsets from the
+ * array itself keep the reads in the LDS address space. */
+template <int N>
+__device__ __forceinline__ void lds_stream(const uint8_t * lds_base, uint32_t off, uint32_t * out) {
+    const uint32_t * p = (const uint32_t *) (lds_base + (off & ~3u));
+    const uint32_t sh = (off & 3u) * 8u;
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int k = 0; k <= N; k++) w[k] = p[k];
 #pragma unroll
     for (int k = 0; k < N; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
 }
@@ -92,8 +113,9 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t w, _Float16 bias, kq_h2 & l
  * memory latencies rather than one per element; otherwise one element per
  * thread and step. PADU adds 8 bytes after every 4 slots (128 columns): the
  * Q6_K kernels' lanes read 128-column units, and the pad puts neighbouring
- * units on different LDS banks. */
-template <int XF32, int PADU = 0>
+ * units on different LDS banks. FLAT instead stores each column's values
+ * contiguously (column k at byte 2k of its xst-byte row). */
+template <int XF32, int PADU = 0, int FLAT = 0>
 __device__ __forceinline__ uint32_t kq_stage_x_by(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst,
                                                   int tid, int nthr) {
     typedef uint32_t u4a __attribute__((ext_vector_type(4), aligned(4)));
@@ -118,7 +140,7 @@ __device__ __forceinline__ uint32_t kq_stage_x_by(uint8_t * lds, const void * x,
 #pragma unroll
             for (int k = 0; k < KB; k++) {
                 const int n = gi[k] / ng, e = 8 * (gi[k] - n * ng);
-                const int off = (e >> 5) * 72 + (PADU ? (e >> 7) * 8 : 0) + 2 * (e & 31);
+                const int off = FLAT ? 2 * e : (e >> 5) * 72 + (PADU ? (e >> 7) * 8 : 0) + 2 * (e & 31);
                 float f[8];
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
@@ -158,7 +180,7 @@ __device__ __forceinline__ uint32_t kq_stage_x_by(uint8_t * lds, const void * x,
         const float v = kq_x(x, XF32, (size_t) n * ldx + k);
         const _Float16 hi = (_Float16) v;
         m = max(m, (uint32_t) __builtin_bit_cast(uint16_t, hi) & 0x7fffu);
-        const int off = (k >> 5) * 72 + (PADU ? (k >> 7) * 8 : 0) + 2 * (k & 31);
+        const int off = FLAT ? 2 * k : (k >> 5) * 72 + (PADU ? (k >> 7) * 8 : 0) + 2 * (k & 31);
         *(_Float16 *) (lds + n * xst + off) = hi;
         if (XF32) *(_Float16 *) (lds + (ncol + n) * xst + off) = (_Float16) (v - (float) hi);
     }
@@ -166,9 +188,9 @@ __device__ __forceinline__ uint32_t kq_stage_x_by(uint8_t * lds, const void * x,
 }
 
 /* The whole workgroup stages x. */
-template <int XF32, int PADU = 0>
+template <int XF32, int PADU = 0, int FLAT = 0>
 __device__ __forceinline__ uint32_t kq_stage_x(uint8_t * lds, const void * x, int ldx, int ncol, int cols, int xst) {
-    return kq_stage_x_by<XF32, PADU>(lds, x, ldx, ncol, cols, xst, (int) threadIdx.x, (int) blockDim.x);
+    return kq_stage_x_by<XF32, PADU, FLAT>(lds, x, ldx, ncol, cols, xst, (int) threadIdx.x, (int) blockDim.x);
 }
 
 /* After the staging barrier, every thread of the workgroup: when the staged
@@ -176,7 +198,7 @@ __device__ __forceinline__ uint32_t kq_stage_x(uint8_t * lds, const void * x, in
  * finite |x| (x read again) and, unless that is in range, stage x again as
  * x * 2^-k (one element per thread and step, the same layout) and return k;
  * otherwise return 0 with x as staged. */
-template <int XF32, int PADU = 0>
+template <int XF32, int PADU = 0, int FLAT = 0>
 __device__ __forceinline__ int kq_x_range(uint8_t * lds, uint32_t * xr, const void * x, int ldx, int ncol, int cols,
                                           int xst, int first = 0) {
     if (!xr_out_lanes(xr[threadIdx.x & 15u], first)) return 0;
@@ -191,7 +213,7 @@ __device__ __forceinline__ int kq_x_range(uint8_t * lds, uint32_t * xr, const vo
         const int n = e / cols, c = e - n * cols;
         const float v = __builtin_ldexpf(kq_x(x, XF32, (size_t) n * ldx + c), -k);
         const _Float16 hi = (_Float16) v;
-        const int off = (c >> 5) * 72 + (PADU ? (c >> 7) * 8 : 0) + 2 * (c & 31);
+        const int off = FLAT ? 2 * c : (c >> 5) * 72 + (PADU ? (c >> 7) * 8 : 0) + 2 * (c & 31);
         *(_Float16 *) (lds + n * xst + off) = hi;
         if (XF32) *(_Float16 *) (lds + (ncol + n) * xst + off) = (_Float16) (v - (float) hi);
     }
@@ -298,6 +320,129 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const uint8_t * blocks, 
                         *yp = (accumulate ? *yp : 0.0f) + v;
                     }
                 }
+            }
+        }
+    }
+}
+
+/* Q8_0 on the matrix cores (v_mfma_f32_16x16x32_f16), every column count.
+ * A wave owns tiles of 16 rows; per 32-weight block it forms
+ *   D = A B from zero, A[i][k] = x[i][k] as f16 (activation columns past
+ *   ncol zero), B[k][j] = q(row j, weight k) (exact in f16),
+ * and then acc[i][j] = fma(d(row j), D[i][j], acc[i][j]), blocks in row
+ * order. Row i of D depends on row i of A alone, so each column of a
+ * several-column launch equals a one-column launch bit for bit.
+ * Rows stream through LDS in chunks of 16 blocks: a chunk (16 rows x 544
+ * bytes) is loaded with coalesced 16-byte loads into registers PD chunks
+ * ahead, stored into the wave's own LDS slot (rows 560 bytes apart, so the
+ * lanes' fragment reads hit distinct banks) and read back in MFMA layout:
+ * lane (m, g) = m + 16 g takes weights 8g .. 8g + 7 of the block, of row m
+ * (B) and of activation column m (A); D[i][j] lands in lane j + 16 (i / 4),
+ * so a lane scales its four sums by one row's d. x is staged once per
+ * workgroup as f16, each column contiguous. Only the x staging uses a
+ * barrier: the waves then run on their own. */
+constexpr int kQ8Chunk = 16;                  /* blocks per chunk */
+constexpr int kQ8PR = kQ8Chunk * 34 / 16;     /* 16-byte pieces per row of a chunk */
+/* LDS bytes per row of a chunk slot: the row's 544 bytes and a pad, so
+ * that the 16 rows' fragment reads spread over the banks */
+constexpr int kQ8Row = 560;
+constexpr int kQ8Slot = 16 * kQ8Row;
+
+template <int NC, int XF32, int PD>
+__global__ __launch_bounds__(PD == 1 ? 1024 : 512) void q8_0_mfma_kernel(const uint8_t * blocks, int rows, int cols,
+                                                                        const void * x, int ldx, int ncol, float * y,
+                                                                        int ldy, int accumulate) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int bpr = cols / 32, nch = bpr / kQ8Chunk;
+    const size_t rowbytes = (size_t) bpr * 34;
+    const int xs = 2 * cols + 16;                                /* LDS bytes per staged column */
+    const uint32_t xbytes = (uint32_t) ((XF32 ? 2 : 1) * ncol * xs);
+    const int nwv = blockDim.x >> 6;
+    uint32_t * xr = (uint32_t *) (lds + xr_off(xbytes + (uint32_t) nwv * kQ8Slot));
+    const uint32_t xm = kq_stage_x<XF32, 0, 1>(lds, x, ldx, ncol, cols, xs);
+    xr_note_f16(xr, xm);
+    __syncthreads();
+    const int xk = kq_x_range<XF32, 0, 1>(lds, xr, x, ldx, ncol, cols, xs);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m = lane & 15, g = lane >> 4;
+    const uint32_t slot = xbytes + (uint32_t) wave * kQ8Slot;
+    const int ntiles = (rows + 15) >> 4, nw = gridDim.x * nwv, w0 = blockIdx.x * nwv + wave;
+    const int S = (w0 < ntiles ? (ntiles - 1 - w0) / nw + 1 : 0) * nch;   /* chunks this wave streams */
+    /* piece p = 64 k + lane of a chunk: row p / kQ8PR of the tile, 16 bytes at 16 (p % kQ8PR) */
+    constexpr int NP = (16 * kQ8PR + 63) / 64;
+    const bool plast = 64 * (NP - 1) + lane < 16 * kQ8PR;
+    u4 R[PD][NP];
+    auto load = [&](int s, int b) {
+        const int tile = w0 + (s / nch) * nw, c = s - (s / nch) * nch;
+        const uint8_t * base = blocks + (size_t) c * (kQ8Chunk * 34);
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            const int p = 64 * k + lane, pr = p / kQ8PR;
+            if (k < NP - 1 || plast) {
+                const int row = min(16 * tile + pr, rows - 1);
+                R[b][k] = *(const u4 *) (base + (size_t) row * rowbytes + 16 * (p - kQ8PR * pr));
+            }
+        }
+    };
+    auto put = [&](int b) {
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            const int p = 64 * k + lane, pr = p / kQ8PR;
+            if (k < NP - 1 || plast) *(u4 *) (lds + slot + (uint32_t) pr * kQ8Row + 16u * (p - kQ8PR * pr)) = R[b][k];
+        }
+    };
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool xcol = NC == 1 ? m == 0 : m < ncol;
+    auto compute = [&](int s) {
+        const int tile = w0 + (s / nch) * nw, c = s - (s / nch) * nch;
+        const uint32_t wrow = slot + (uint32_t) m * kQ8Row;
+#pragma unroll 4
+        for (int bb = 0; bb < kQ8Chunk; bb++) {
+            uint32_t qw[2];
+            lds_stream<2>(lds, wrow + 34u * bb + 2u + 8u * g, qw);
+            kq_h2 w0h, w1h, w2h, w3h;
+            bytes_to_h2(qw[0] ^ 0x80808080u, (_Float16) 1152.0f, w0h, w1h);
+            bytes_to_h2(qw[1] ^ 0x80808080u, (_Float16) 1152.0f, w2h, w3h);
+            const h8 B = {w0h[0], w0h[1], w1h[0], w1h[1], w2h[0], w2h[1], w3h[0], w3h[1]};
+            const uint32_t xo = (uint32_t) m * xs + 2u * (32u * (kQ8Chunk * c + bb) + 8u * g);
+            h8 A = {};
+            if (xcol) A = *(const h8 *) (lds + xo);
+            f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            if (XF32) {
+                h8 Al = {};
+                if (xcol) Al = *(const h8 *) (lds + (uint32_t) ncol * xs + xo);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B, D, 0, 0, 0);
+            }
+            const float d = kq_f16(*(const uint16_t *) (lds + wrow + 34u * bb));
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = __builtin_fmaf(d, D[e], acc[e]);
+        }
+        if (c == nch - 1) {
+            const int row = 16 * tile + m;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int n = 4 * g + e;
+                if ((NC == 1 ? n == 0 : n < ncol) && row < rows) {
+                    float * yp = y + (size_t) n * ldy + row;
+                    *yp = (accumulate ? *yp : 0.0f) + xr_unscale(acc[e], xk);
+                }
+                acc[e] = 0.0f;
+            }
+        }
+    };
+#pragma unroll
+    for (int b = 0; b < PD; b++)
+        if (b < S) load(b, b);
+    for (int s = 0; s < S; s += PD) {
+#pragma unroll
+        for (int b = 0; b < PD; b++) {
+            if (s + b < S) {
+                put(b);
+                if (s + b + PD < S) load(s + b + PD, b);
+                compute(s + b);
             }
         }
     }
@@ -497,19 +642,6 @@ __global__ __launch_bounds__(256) void q6k_gemv_wide_kernel(const uint8_t * bloc
     }
 }
 
-/* N dwords of LDS bytes from byte `off` of the shared array (2-byte
- * aligned): the covering aligned dwords, funnel-shifted. Offsets from the
- * array itself keep the reads in the LDS address space. */
-template <int N>
-__device__ __forceinline__ void lds_stream(const uint8_t * lds_base, uint32_t off, uint32_t * out) {
-    const uint32_t * p = (const uint32_t *) (lds_base + (off & ~3u));
-    const uint32_t sh = (off & 3u) * 8u;
-    uint32_t w[N + 1];
-#pragma unroll
-    for (int k = 0; k <= N; k++) w[k] = p[k];
-#pragma unroll
-    for (int k = 0; k < N; k++) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
-}
 
 /* Q6_K, staged form. Compute waves each own one row: a wave copies its row
  * into its own LDS region by 1 KB direct-to-LDS loads and then works it,
@@ -704,6 +836,69 @@ static int kq_q6k_staged(const uint8_t * bp, int rows, int cols, const void * x,
                 : kq_q6k_staged_t<0>(bp, rows, cols, x, ldx, ncol, y, ldy, accumulate, rpw, lds, s);
 }
 
+/* The matrix-core Q8_0 kernel: rows of whole 16-block chunks (cols a multiple
+ * of 512) from a 16-byte aligned buffer. Waves per workgroup: as many
+ * 8960-byte row slots as fit beside x, in fours, at most 16; one workgroup
+ * per CU, each wave a strided share of the 16-row tiles. Returns 1 when the
+ * shape does not fit it. */
+template <int NC, int XF32, int PD>
+static int kq_q8_mfma_k(const uint8_t * bp, int rows, int cols, const void * x, int ldx, int ncol, float * y, int ldy,
+                        int accumulate, int nwv, int persist, size_t lds, hipStream_t s) {
+    static std::atomic<size_t> opted{0};
+    const void * fn = (const void *) q8_0_mfma_kernel<NC, XF32, PD>;
+    if (lds > 65536 && lds > opted.load()) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
+        if (e != hipSuccess) return fail_hip("LDS opt-in for the matrix-core Q8_0 kernel", e);
+        opted.store(lds);
+    }
+    const int ntiles = (rows + 15) / 16;
+    int grid = (ntiles + nwv - 1) / nwv;
+    if (persist && grid > cu_count()) grid = cu_count();
+    launch_kernel(q8_0_mfma_kernel<NC, XF32, PD>, dim3((unsigned) grid), dim3((unsigned) (64 * nwv)), (uint32_t) lds, s,
+                  bp, rows, cols, x, ldx, ncol, y, ldy, accumulate);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail_hip("matrix-core Q8_0 launch", e);
+}
+
+/* The matrix-core Q8_0 GEMV for rows of whole 16-block chunks (cols a
+ * multiple of 512) in a 16-byte aligned buffer; returns 1 when the shape
+ * does not fit it. Columns per launch: as many as fit LDS beside four row
+ * slots; a shape where one column does not fit never takes this kernel, and
+ * wider launches go in groups, so every column count of a shape gets the
+ * same arithmetic. Launch shapes (measured on the 151936 x 2560 head):
+ *  - one column: eight waves per workgroup, one 16-row tile per wave, the
+ *    next chunk's loads in flight (80.5 us; whole-grid persistent waves
+ *    82.5-84.5, two tiles per wave 91.6, two chunks ahead 85);
+ *  - several columns: at most one workgroup of eight waves per CU, each
+ *    wave a strided share of the tiles, two chunks ahead (8 columns: 91-92
+ *    us; one tile per wave would stage 41 KB of x per tile). */
+static int kq_q8_mfma(const uint8_t * bp, int rows, int cols, const void * x, int xf32, int ldx, int ncol, float * y,
+                      int ldy, int accumulate, hipStream_t s) {
+    if (cols % (32 * kQ8Chunk) || ((uintptr_t) bp & 15u)) return 1;
+    const size_t xcol = (size_t) (xf32 ? 2 : 1) * (2 * cols + 16);
+    const size_t room = 160 * 1024 - kXrBytes - 16;
+    if (xcol + 4 * (size_t) kQ8Slot > room) return 1;
+    const int gmax = (int) ((room - 4 * (size_t) kQ8Slot) / xcol);
+    for (int n0 = 0; n0 < ncol; n0 += gmax) {
+        const int nc = ncol - n0 < gmax ? ncol - n0 : gmax;
+        const size_t xbytes = (size_t) nc * xcol;
+        int nwv = (int) ((room - xbytes) / kQ8Slot);
+        nwv = nwv > 8 ? 8 : nwv & ~3;
+        const size_t lds = xr_off((uint32_t) (xbytes + (size_t) nwv * kQ8Slot)) + kXrBytes;
+        const void * xg = (const uint8_t *) x + (size_t) n0 * ldx * (xf32 ? 4 : 2);
+        float * yg = y + (size_t) n0 * ldy;
+        int rc;
+        if (nc == 1)
+            rc = xf32 ? kq_q8_mfma_k<1, 1, 1>(bp, rows, cols, xg, ldx, nc, yg, ldy, accumulate, nwv, 0, lds, s)
+                      : kq_q8_mfma_k<1, 0, 1>(bp, rows, cols, xg, ldx, nc, yg, ldy, accumulate, nwv, 0, lds, s);
+        else
+            rc = xf32 ? kq_q8_mfma_k<16, 1, 2>(bp, rows, cols, xg, ldx, nc, yg, ldy, accumulate, nwv, 1, lds, s)
+                      : kq_q8_mfma_k<16, 0, 2>(bp, rows, cols, xg, ldx, nc, yg, ldy, accumulate, nwv, 1, lds, s);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void * x, int xf32, int ldx, int ncol,
                    float * y, int ldy, int accumulate, hipStream_t s) {
     const int blk = kind == 6 ? 256 : 32;
@@ -716,6 +911,11 @@ int kq_gemv_launch(int kind, const void * blocks, int rows, int cols, const void
     if (((uintptr_t) blocks) & 1) { set_error("k-quant blocks must be 2-byte aligned"); return -1; }
     if (ncol < 1 || ncol > kMaxCols) { set_error("column count %d is outside 1..%d", ncol, kMaxCols); return -1; }
     if (ncol > 1 && (ldx < cols || ldy < rows)) { set_error("ldx/ldy below the matrix extent"); return -1; }
+    if (kind == 8) {
+        /* the matrix cores where the shape allows (any column count) */
+        const int mr = kq_q8_mfma((const uint8_t *) blocks, rows, cols, x, xf32, ldx, ncol, y, ldy, accumulate, s);
+        if (mr != 1) return mr;
+    }
     const int threads = 256;
     const int rows_per_block = (threads / 64) * 4;
     /* Q6_K slots carry 8 bytes of pad per 128 columns */

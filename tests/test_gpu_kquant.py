@@ -26,7 +26,7 @@ def _dequant_ref(ref, kind, blocks, rows, cols):
 # q6_k also at the Q6_K trunk's launch shapes: q + k + v + head gate stacked by
 # rows (6160 x 2560), gate + up stacked (20480 x 2560) and o (2560 x 4096)
 SHAPES = {"q6_k": [(2560, 10240), (13, 512), (4, 256), (64, 2560), (6160, 2560), (20480, 2560), (2560, 4096)],
-          "q8_0": [(1024, 2560), (3, 32), (5, 96), (64, 2560), (7, 4096)]}
+          "q8_0": [(1024, 2560), (3, 32), (5, 96), (64, 2560), (7, 4096), (5, 512), (40, 1536)]}
 
 
 @pytest.mark.parametrize("kind,shape", [(k, s) for k in SHAPES for s in SHAPES[k]])
@@ -112,11 +112,44 @@ def test_q8_0_sixteen_columns(sm, ref, dev):
     xt = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
     y = torch.full((ncol, rows), float("nan"), device=dev)
     sm.kquant_gemv("q8_0", db, rows, cols, xt, y, ncols=ncol)
-    y1 = torch.full((1, rows), float("nan"), device=dev)
-    sm.kquant_gemv("q8_0", db, rows, cols, xt[5:6].contiguous(), y1)
     torch.cuda.synchronize()
     assert rel_l2(y.cpu().numpy(), xf.astype(np.float64) @ W.T) <= TIGHT
-    assert np.array_equal(y[5].cpu().numpy().view(np.uint32), y1[0].cpu().numpy().view(np.uint32))
+    # x of 16 columns does not fit beside the row slots: the launch goes in
+    # column groups, and every column still equals a one-column launch
+    for n in range(ncol):
+        y1 = torch.full((1, rows), float("nan"), device=dev)
+        sm.kquant_gemv("q8_0", db, rows, cols, xt[n:n + 1].contiguous(), y1)
+        torch.cuda.synchronize()
+        assert np.array_equal(y[n].cpu().numpy().view(np.uint32), y1[0].cpu().numpy().view(np.uint32)), n
+
+
+@pytest.mark.parametrize("ncol,xdt", [(3, "bf16"), (5, "f32")])
+def test_q8_0_columns_equal_single_launches(sm, ref, dev, ncol, xdt):
+    """Fewer columns than the kernel's width (3 of 16 B-operand rows), and f32
+    x (its hi and lo halves, two matrix-core products per block): every
+    column bit-equal to a one-column launch and within 1e-5 of the oracle.
+    Rows not a multiple of 16 leave the last tile partial."""
+    import torch
+    rows, cols = 300, 2560
+    blocks = sm.synth_q8_0(51, rows, cols)
+    W = ref.q8_0_dequant(blocks, rows, cols).astype(np.float64)
+    db = torch.from_numpy(blocks).to(dev)
+    if xdt == "bf16":
+        xb = sm.synth_bf16(52, ncol * cols).reshape(ncol, cols)
+        xf = sm.bf16_to_f32(xb).reshape(ncol, cols)
+        xt = torch.from_numpy(xb.view(np.int16).copy()).to(dev)
+    else:
+        xf = np.random.default_rng(53).standard_normal((ncol, cols)).astype(np.float32)
+        xt = torch.from_numpy(xf).to(dev)
+    y = torch.full((ncol, rows), float("nan"), device=dev)
+    sm.kquant_gemv("q8_0", db, rows, cols, xt, y, ncols=ncol)
+    torch.cuda.synchronize()
+    assert rel_l2(y.cpu().numpy(), xf.astype(np.float64) @ W.T) <= TIGHT
+    for n in range(ncol):
+        y1 = torch.full((1, rows), float("nan"), device=dev)
+        sm.kquant_gemv("q8_0", db, rows, cols, xt[n:n + 1].contiguous(), y1)
+        torch.cuda.synchronize()
+        assert np.array_equal(y[n].cpu().numpy().view(np.uint32), y1[0].cpu().numpy().view(np.uint32)), n
 
 
 def test_kquant_errors(sm, dev):
