@@ -28,6 +28,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <type_traits>
 
 namespace sparkmv {
 
@@ -395,30 +396,59 @@ __global__ __launch_bounds__(PD == 1 ? 1024 : 512) void q8_0_mfma_kernel(const u
         }
     };
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    const bool xcol = NC == 1 ? m == 0 : m < ncol;
+    const bool xact = NC == 1 ? m == 0 : m < ncol;
+    /* the A operand of lanes past the columns stays zero: they never load */
+    h8 A = {}, Al = {};
     auto compute = [&](int s) {
         const int tile = w0 + (s / nch) * nw, c = s - (s / nch) * nch;
-        const uint32_t wrow = slot + (uint32_t) m * kQ8Row;
-#pragma unroll 4
-        for (int bb = 0; bb < kQ8Chunk; bb++) {
+        const uint32_t wrow = slot + (uint32_t) m * kQ8Row;   /* 16-byte aligned */
+        /* blocks 4i .. 4i + 3 of the chunk start 136 bytes apart from a lane
+         * base that is a multiple of 8, so each block's quant bytes 8g .. 8g
+         * + 7 sit 2, 4, 2 and 0 bytes past a dword: 3, 2, 3 and 2 dword
+         * reads, and a fixed shift */
+        auto frag = [&](const uint32_t * pw, auto J, uint32_t * q) {
+            constexpr int j = decltype(J)::value;
+            if constexpr (j == 0 || j == 2) {
+                constexpr int o = j == 0 ? 0 : 17;
+                const uint32_t a = pw[o], b = pw[o + 1], c2 = pw[o + 2];
+                q[0] = __builtin_amdgcn_alignbit(b, a, 16);
+                q[1] = __builtin_amdgcn_alignbit(c2, b, 16);
+            } else {
+                constexpr int o = j == 1 ? 9 : 26;
+                q[0] = pw[o];
+                q[1] = pw[o + 1];
+            }
+        };
+        auto block = [&](const uint32_t * pw, int bb, auto J) {
             uint32_t qw[2];
-            lds_stream<2>(lds, wrow + 34u * bb + 2u + 8u * g, qw);
+            frag(pw, J, qw);
             kq_h2 w0h, w1h, w2h, w3h;
             bytes_to_h2(qw[0] ^ 0x80808080u, (_Float16) 1152.0f, w0h, w1h);
             bytes_to_h2(qw[1] ^ 0x80808080u, (_Float16) 1152.0f, w2h, w3h);
             const h8 B = {w0h[0], w0h[1], w1h[0], w1h[1], w2h[0], w2h[1], w3h[0], w3h[1]};
             const uint32_t xo = (uint32_t) m * xs + 2u * (32u * (kQ8Chunk * c + bb) + 8u * g);
-            h8 A = {};
-            if (xcol) A = *(const h8 *) (lds + xo);
+            if (xact) A = *(const h8 *) (lds + xo);
             f4 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             if (XF32) {
-                h8 Al = {};
-                if (xcol) Al = *(const h8 *) (lds + (uint32_t) ncol * xs + xo);
+                if (xact) Al = *(const h8 *) (lds + (uint32_t) ncol * xs + xo);
                 D = __builtin_amdgcn_mfma_f32_16x16x32_f16(Al, B, D, 0, 0, 0);
             }
-            const float d = kq_f16(*(const uint16_t *) (lds + wrow + 34u * bb));
+            const float d = kq_f16(*(const uint16_t *) (lds + wrow + 34u * (uint32_t) bb));
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[e] = __builtin_fmaf(d, D[e], acc[e]);
+        };
+        static_assert(kQ8Chunk % 4 == 0, "chunks of whole block quads");
+#pragma unroll 1
+        for (int b4 = 0; b4 < kQ8Chunk; b4 += 4) {
+            /* the lane's dword base, its 8-byte alignment hidden so that the
+             * reads stay dword reads (wider unaligned LDS reads measured slower) */
+            uint32_t pb = wrow + 8u * g + 34u * (uint32_t) b4;
+            asm volatile("" : "+v"(pb));
+            const uint32_t * pw = (const uint32_t *) (lds + pb);
+            block(pw, b4, std::integral_constant<int, 0>{});
+            block(pw, b4 + 1, std::integral_constant<int, 1>{});
+            block(pw, b4 + 2, std::integral_constant<int, 2>{});
+            block(pw, b4 + 3, std::integral_constant<int, 3>{});
         }
         if (c == nch - 1) {
             const int row = 16 * tile + m;
@@ -867,11 +897,12 @@ static int kq_q8_mfma_k(const uint8_t * bp, int rows, int cols, const void * x, 
  * wider launches go in groups, so every column count of a shape gets the
  * same arithmetic. Launch shapes (measured on the 151936 x 2560 head):
  *  - one column: eight waves per workgroup, one 16-row tile per wave, the
- *    next chunk's loads in flight (80.5 us; whole-grid persistent waves
- *    82.5-84.5, two tiles per wave 91.6, two chunks ahead 85);
+ *    next chunk's loads in flight (78.0-78.5 us; before the block quads,
+ *    80.5 against whole-grid persistent waves 82.5-84.5, two tiles per wave
+ *    91.6 and two chunks ahead 85);
  *  - several columns: at most one workgroup of eight waves per CU, each
- *    wave a strided share of the tiles, two chunks ahead (8 columns: 91-92
- *    us; one tile per wave would stage 41 KB of x per tile). */
+ *    wave a strided share of the tiles, two chunks ahead (8 columns:
+ *    88.4-89.2 us; one tile per wave would stage 41 KB of x per tile). */
 static int kq_q8_mfma(const uint8_t * bp, int rows, int cols, const void * x, int xf32, int ldx, int ncol, float * y,
                       int ldy, int accumulate, hipStream_t s) {
     if (cols % (32 * kQ8Chunk) || ((uintptr_t) bp & 15u)) return 1;
