@@ -29,6 +29,8 @@
 #include <hip/hip_fp16.h>
 #include <string.h>
 
+#include <atomic>
+
 namespace sparkmv {
 
 
@@ -112,6 +114,8 @@ constexpr int kFastMats = 4;
 constexpr int kFastXg = 1;
 
 constexpr int kRedStride = 16 * 17;   /* floats per wave of the LDS reduction area */
+/* LDS stride between the stages' codebooks for 12-bit indices (nc <= 4096) */
+constexpr uint32_t kCbStride12 = 32768;
 
 /* f32 -> bf16 bits, round to nearest even (a NaN stays a NaN) */
 __device__ __forceinline__ uint32_t bf16_rne(float f) {
@@ -143,11 +147,17 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * streaming 40 MB) measured best with two. */
     constexpr int kLook = MSC >= 10 ? 2 : 3;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    /* cbb: bytes of one stage's codebook; cbs: their stride in LDS. The
+     * several-column kernels with 12-bit indices (nc <= 4096) use a fixed
+     * 32 KB, so the second stage's gathers take their offset as an
+     * immediate; the one-column kernels keep cbb (their code is sensitive
+     * to the change: 0.1-0.25 us per launch slower, measured) */
     const uint32_t cbb = (uint32_t) A.nc * 8u;
-    uint8_t * lx = lds + NST * cbb;
+    const uint32_t cbs = (EXT || !MC) ? cbb : kCbStride12;
+    uint8_t * lx = lds + NST * cbs;
     float * red = (float *) (lx + (XF32 ? 2 : 1) * A.ncol * A.xstride);
     /* the x range flags, after the reduction area */
-    uint32_t * xr = (uint32_t *) (lds + xr_off(NST * cbb + (XF32 ? 2 : 1) * A.ncol * A.xstride +
+    uint32_t * xr = (uint32_t *) (lds + xr_off(NST * cbs + (XF32 ? 2 : 1) * A.ncol * A.xstride +
                                                (A.threads >> 6) * kRedStride * 4));
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m16 = lane & 15, q = lane >> 4;
@@ -260,7 +270,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
     };
     auto cb_store = [&](int i, const uint32_t * v) {
         const int s = NST > 1 && i >= n16 ? 1 : 0;
-        uint32_t * dst = (uint32_t *) (lds + s * cbb) + 4 * (i - s * n16);
+        uint32_t * dst = (uint32_t *) (lds + s * cbs) + 4 * (i - s * n16);
         dst[0] = v[0]; dst[1] = v[1]; dst[2] = v[2]; dst[3] = v[3];
     };
     auto x_load = [&](int n, int k) -> uint32_t {
@@ -311,7 +321,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
             for (int s = 0; s < NST; s++)
 #pragma unroll
                 for (int k = 0; k < KS; k++)
-                    ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+                    ((u4v *) (lds + s * cbs))[min(k * bd + tid, n16 - 1)] = cv[s][k];
         }
         const int xq = A.cols >> 3, nx = XG ? 0 : ncol * xq;
         for (int base = 0; base < nx; base += KXM * bd) {
@@ -421,7 +431,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         for (int s = 0; s < NST; s++)
 #pragma unroll
             for (int k = 0; k < KS; k++)
-                ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+                ((u4v *) (lds + s * cbs))[min(k * bd + tid, n16 - 1)] = cv[s][k];
     } else if constexpr (MSC > 0 && XF32) {
         /* One 16-byte aligned f32 activation column of at most 16 * blockDim
          * columns, each value split into f16 hi + lo (hi in the column's
@@ -452,7 +462,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         for (int s = 0; s < NST; s++)
 #pragma unroll
             for (int k = 0; k < KS; k++)
-                ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+                ((u4v *) (lds + s * cbs))[min(k * bd + tid, n16 - 1)] = cv[s][k];
 #pragma unroll
         for (int k = 0; k < KX; k++) {
             const int e = 4 * min(k * bd + tid, xq - 1);
@@ -505,7 +515,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         for (int s = 0; s < NST; s++)
 #pragma unroll
             for (int k = 0; k < KS; k++)
-                ((u4v *) (lds + s * cbb))[min(k * bd + tid, n16 - 1)] = cv[s][k];
+                ((u4v *) (lds + s * cbs))[min(k * bd + tid, n16 - 1)] = cv[s][k];
 #pragma unroll
         for (int k = 0; k < KX; k++) {
             const int i = k * bd + tid;
@@ -559,7 +569,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
     }
     if (MSC == 0 && (cbb & 8u) && tid < 2 * NST) {   /* an odd codebook: the last codeword of each stage */
         const int s = tid >> 1, k = tid & 1;
-        ((uint32_t *) (lds + s * cbb))[4 * n16 + k] = ((const uint32_t *) ((s ? stp[NST - 1] : stp[0]) + 24))[4 * n16 + k];
+        ((uint32_t *) (lds + s * cbs))[4 * n16 + k] = ((const uint32_t *) ((s ? stp[NST - 1] : stp[0]) + 24))[4 * n16 + k];
     }
     if constexpr (XG == 0) xr_note(xr, XF32 ? xm : xr_bf16_max(xm2));
     __syncthreads();
@@ -606,7 +616,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
             if (MSC > 0) {
 #pragma unroll
                 for (int u = 0; u < D; u++) {
-                    mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * u, xbl + 264 * u, acc, 1.0f, xm);
+                    mstep<NST, XF32, EXT, XG, 0, MC != 0>(w[u], lds, cbs, xb + 264 * u, xbl + 264 * u, acc, 1.0f, xm);
                     if (u + kLook < D) ld(w[u + kLook], u + kLook);
                     /* keep step u + kLook's loads here: left to itself the
                      * scheduler sinks them to just before their step, which
@@ -619,7 +629,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
 #pragma unroll
                     for (int u = 0; u < D; u++) {
                         if (ms0 + u < MS)
-                            mstep<NST, XF32, EXT, XG>(w[u], lds, cbb, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc,
+                            mstep<NST, XF32, EXT, XG, 0, MC != 0>(w[u], lds, cbs, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc,
                                                       1.0f, xm);
                         if (MS > D) ld(w[u], ms0 + u + D);
                     }
@@ -678,7 +688,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                         for (int u = 0; u < MS; u++) {
                             Words<NST, EXT, XG> W1;
                             load_words<NST, EXT, XG>(W1, rp, pp, xgp, u);
-                            mstep<NST, XF32, EXT, XG, 1>(W1, lds, cbb, xb, xbl, acc, sc);
+                            mstep<NST, XF32, EXT, XG, 1, MC != 0>(W1, lds, cbs, xb, xbl, acc, sc);
                         }
                     }
                 }
@@ -975,7 +985,20 @@ static int aligned4(const void * p) { return ((uintptr_t) p & 3u) == 0; }
 template <int NST, int XF32, int EXT, int MSC, int MC = 0, int XN = 0>
 static int launch_fast_t(const FastArgs & A, int grid, int threads, size_t lds, hipStream_t s) {
     static size_t opted = 0;
+    static std::atomic<int> checked{0};
     const void * fn = (const void *) vq_mfma_kernel<NST, XF32, EXT, MSC, MC, XN>;
+    if (!checked.load()) {
+        /* the codeword gathers address LDS from 0: no static LDS may precede
+         * the dynamic array */
+        hipFuncAttributes fa;
+        hipError_t e = hipFuncGetAttributes(&fa, fn);
+        if (e != hipSuccess) return fail_hip("VQ block kernel attributes", e);
+        if (fa.sharedSizeBytes != 0) {
+            set_error("the VQ block kernel has %zu bytes of static LDS; its gathers assume none", fa.sharedSizeBytes);
+            return -1;
+        }
+        checked.store(1);
+    }
     if (lds > 65536 && lds > opted) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return fail_hip("LDS opt-in for the VQ block kernel", e);
@@ -1001,8 +1024,15 @@ struct FastShape {
  * values and 8 of pad) and 8 more between columns. */
 static int fast_xstride(int cols, int S) { (void) S; return 264 * (cols / 128) + 8; }
 
+/* LDS bytes per stage codebook in the block kernel: a fixed 32 KB in the
+ * several-column kernels with 12-bit indices (nc <= 4096), else nc * 8 (a
+ * several-column call that runs the generic kernel gets the 32 KB too, more
+ * than it uses) */
+static size_t fast_cbs(int nc, int ncol) { return nc > 4096 || ncol == 1 ? (size_t) nc * 8 : kCbStride12; }
+
 static size_t fast_lds(const VqCall & c, int nst, int S, int W, int xg = 0) {
-    return (size_t) nst * c.nc * 8 + (xg ? 0 : (size_t) (c.xf32 ? 2 : 1) * c.ncol * fast_xstride(c.cols, S)) +
+    return (size_t) nst * fast_cbs(c.nc, c.ncol) +
+           (xg ? 0 : (size_t) (c.xf32 ? 2 : 1) * c.ncol * fast_xstride(c.cols, S)) +
            (size_t) W * kRedStride * 4 + kXrBytes;
 }
 

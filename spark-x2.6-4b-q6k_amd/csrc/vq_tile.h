@@ -72,10 +72,10 @@ __device__ __forceinline__ void load_words(Words<NST, EXT, XG> & W, const uint8_
  * of the step (8 B reads, 8 * NST codeword gathers) is issued before the
  * first MFMA, so the gathers' latency overlaps. */
 template <int T, int NST, int EXT, int XG>
-__device__ __forceinline__ uint32_t step_addr(const Words<NST, EXT, XG> & W, int s, uint32_t cbb) {
+__device__ __forceinline__ uint32_t step_addr(const Words<NST, EXT, XG> & W, int s, uint32_t cbs) {
     uint32_t a = cw_addr<T>(W.w[s][0], W.w[s][1], W.w[s][2]);
     if (EXT) a |= (W.pb[s] << (15 - T)) & 0x8000u;
-    return (uint32_t) s * cbb + a;
+    return (uint32_t) s * cbs + a;
 }
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -85,21 +85,38 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
  * integers; an infinity or NaN is larger than any finite value), from which
  * the caller finds units of small x. SCX: x is multiplied by sc (a power of
  * two) before it is converted. */
-template <int NST, int XF32, int EXT, int XG = 0, int SCX = 0>
-__device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8_t * lds, uint32_t cbb,
+/* A codeword at LDS byte address a. The codebooks sit at the start of the
+ * kernel's dynamic LDS, which begins at address 0 (the kernels that call this
+ * have no static LDS; their launcher checks), so the address is the gather's
+ * own offset: no base is added, and a constant stage offset goes into the
+ * instruction's offset field. */
+__device__ __forceinline__ h4 cw_read(uint32_t a) {
+    typedef const __attribute__((address_space(3))) h4 lds_h4;
+    return *(lds_h4 *) (size_t) a;
+}
+
+/* cbs: LDS bytes from one stage's codebook to the next (a constant in the
+ * several-column 12-bit kernels, so the second stage's offset is an
+ * immediate). ABS: gather by absolute LDS address (cw_read); otherwise from
+ * the array `lds` (a base add per gather). The several-column kernels gather
+ * by absolute address (verify step 2087 -> 2060 us); the one-column kernels
+ * measured slower that way and keep the base add. */
+template <int NST, int XF32, int EXT, int XG = 0, int SCX = 0, int ABS = 0>
+__device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8_t * lds, uint32_t cbs,
                                       const uint8_t * xb, const uint8_t * xbl, f4 * acc, float sc = 1.0f,
                                       u16x2 * xm = nullptr) {
     h4 cw[8][NST], b[8], bl[8];
+    auto rd = [&](uint32_t a) -> h4 { return ABS ? cw_read(a) : *(const h4 *) (lds + a); };
 #pragma unroll
     for (int s = 0; s < NST; s++) {
-        cw[0][s] = *(const h4 *) (lds + step_addr<0, NST, EXT, XG>(W, s, cbb));
-        cw[1][s] = *(const h4 *) (lds + step_addr<1, NST, EXT, XG>(W, s, cbb));
-        cw[2][s] = *(const h4 *) (lds + step_addr<2, NST, EXT, XG>(W, s, cbb));
-        cw[3][s] = *(const h4 *) (lds + step_addr<3, NST, EXT, XG>(W, s, cbb));
-        cw[4][s] = *(const h4 *) (lds + step_addr<4, NST, EXT, XG>(W, s, cbb));
-        cw[5][s] = *(const h4 *) (lds + step_addr<5, NST, EXT, XG>(W, s, cbb));
-        cw[6][s] = *(const h4 *) (lds + step_addr<6, NST, EXT, XG>(W, s, cbb));
-        cw[7][s] = *(const h4 *) (lds + step_addr<7, NST, EXT, XG>(W, s, cbb));
+        cw[0][s] = rd(step_addr<0, NST, EXT, XG>(W, s, cbs));
+        cw[1][s] = rd(step_addr<1, NST, EXT, XG>(W, s, cbs));
+        cw[2][s] = rd(step_addr<2, NST, EXT, XG>(W, s, cbs));
+        cw[3][s] = rd(step_addr<3, NST, EXT, XG>(W, s, cbs));
+        cw[4][s] = rd(step_addr<4, NST, EXT, XG>(W, s, cbs));
+        cw[5][s] = rd(step_addr<5, NST, EXT, XG>(W, s, cbs));
+        cw[6][s] = rd(step_addr<6, NST, EXT, XG>(W, s, cbs));
+        cw[7][s] = rd(step_addr<7, NST, EXT, XG>(W, s, cbs));
     }
 #pragma unroll
     for (int t = 0; t < 8; t++) {
