@@ -1,12 +1,14 @@
 /* vq_tile.h — the MFMA tile primitives of the dim-4 DQV3 GEMV kernels (device
  * code only): 12-bit field addresses, the index words of one macro step, and
- * one macro step of codeword gathers and v_mfma_f32_16x16x16_f16.
+ * one macro step of codeword gathers and matrix-core products.
  *
  * A macro step is 32 indices (128 columns) of a row: lane quarter q of a wave
  * reads the 12 bytes that hold indices 8q .. 8q + 7, gathers their raw f16
- * codewords from the LDS codebook straight into the A operand, and takes the
- * matching activations as the B operand. Codeword times activation is exact
- * in f16 x f16 -> f32; only the f32 accumulation rounds. */
+ * codewords from the LDS codebook straight into the A operand (two per
+ * v_mfma_f32_16x16x32_f16, or one per v_mfma_f32_16x16x16_f16 when x comes
+ * from global memory), and takes the matching activations as the B operand.
+ * Codeword times activation is exact in f16 x f16 -> f32; only the f32
+ * accumulation rounds. */
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -139,12 +141,36 @@ __device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8
             if (XF32) bl[t] = *(const h4 *) (xbl + 8 * t);
         }
     }
+    /* With x in LDS, k-slots t and t + 1 go into one
+     * v_mfma_f32_16x16x32_f16: a lane's A holds its two codewords and B the
+     * matching two quads of x (the same pairing on both sides). On gfx950 it
+     * issues in about the time of one 16x16x16 (31 against 30 cycles,
+     * measured), so a step takes half the matrix-core time: decode set
+     * 1571-1578 -> 1554-1565 us, N = 8 gate+up 16.9 -> 16.65 us. The
+     * x-from-global kernels keep 16x16x16: paired, they spill at their
+     * register cap and lost 0.3-0.9 us per launch. */
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    if constexpr (XG != 0) {
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
+        for (int t = 0; t < 8; t++) {
+#pragma unroll
+            for (int s = 0; s < NST; s++) {
+                acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw[t][s], b[t], acc[s], 0, 0, 0);
+                if (XF32) acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw[t][s], bl[t], acc[s], 0, 0, 0);
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t += 2) {
+        const h8 bp = __builtin_shufflevector(b[t], b[t + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+        h8 blp;
+        if (XF32) blp = __builtin_shufflevector(bl[t], bl[t + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int s = 0; s < NST; s++) {
-            acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw[t][s], b[t], acc[s], 0, 0, 0);
-            if (XF32) acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(cw[t][s], bl[t], acc[s], 0, 0, 0);
+            const h8 ap = __builtin_shufflevector(cw[t][s], cw[t + 1][s], 0, 1, 2, 3, 4, 5, 6, 7);
+            acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, bp, acc[s], 0, 0, 0);
+            if (XF32) acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap, blp, acc[s], 0, 0, 0);
         }
     }
 }
