@@ -143,9 +143,12 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
     /* straight-line units keep at most kLook macro steps of index words in
      * flight per wave: with every step requested up front the memory system
      * serves some CUs' words last, and those CUs then do their whole unit
-     * after the stream has ended. Ten-step units (gate+up: 10 waves per CU
-     * streaming 40 MB) measured best with two. */
-    constexpr int kLook = MSC >= 10 ? 2 : 3;
+     * after the stream has ended. Two measured best wherever x is in LDS
+     * (one column: q+k+v+g 7.6 -> 7.4 us, down 9.7 -> 9.2 us against three;
+     * one step ahead lost 0.2-0.8 us). The x-from-global kernels also carry
+     * each step's x in the same loads and keep three below ten-step units
+     * (N = 8 down 14.8 -> 15.8 us with two). */
+    constexpr int kLook = (MSC >= 10 || !XG) ? 2 : 3;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     /* cbb: bytes of one stage's codebook; cbs: their stride in LDS. The
      * several-column kernels with 12-bit indices (nc <= 4096) use a fixed
