@@ -150,13 +150,11 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * (N = 8 down 14.8 -> 15.8 us with two). */
     constexpr int kLook = (MSC >= 10 || !XG) ? 2 : 3;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    /* cbb: bytes of one stage's codebook; cbs: their stride in LDS. The
-     * several-column kernels with 12-bit indices (nc <= 4096) use a fixed
-     * 32 KB, so the second stage's gathers take their offset as an
-     * immediate; the one-column kernels keep cbb (their code is sensitive
-     * to the change: 0.1-0.25 us per launch slower, measured) */
+    /* cbb: bytes of one stage's codebook; cbs: their stride in LDS, a fixed
+     * 32 KB for 12-bit indices (nc <= 4096), so the second stage's gathers
+     * take their offset as an immediate */
     const uint32_t cbb = (uint32_t) A.nc * 8u;
-    const uint32_t cbs = (EXT || !MC) ? cbb : kCbStride12;
+    const uint32_t cbs = EXT ? cbb : kCbStride12;
     uint8_t * lx = lds + NST * cbs;
     float * red = (float *) (lx + (XF32 ? 2 : 1) * A.ncol * A.xstride);
     /* the x range flags, after the reduction area */
@@ -619,7 +617,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
             if (MSC > 0) {
 #pragma unroll
                 for (int u = 0; u < D; u++) {
-                    mstep<NST, XF32, EXT, XG, 0, MC != 0>(w[u], lds, cbs, xb + 264 * u, xbl + 264 * u, acc, 1.0f, xm);
+                    mstep<NST, XF32, EXT, XG, 0>(w[u], cbs, xb + 264 * u, xbl + 264 * u, acc, 1.0f, xm);
                     if (u + kLook < D) ld(w[u + kLook], u + kLook);
                     /* keep step u + kLook's loads here: left to itself the
                      * scheduler sinks them to just before their step, which
@@ -632,7 +630,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
 #pragma unroll
                     for (int u = 0; u < D; u++) {
                         if (ms0 + u < MS)
-                            mstep<NST, XF32, EXT, XG, 0, MC != 0>(w[u], lds, cbs, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc,
+                            mstep<NST, XF32, EXT, XG, 0>(w[u], cbs, xb + 264 * (ms0 + u), xbl + 264 * (ms0 + u), acc,
                                                       1.0f, xm);
                         if (MS > D) ld(w[u], ms0 + u + D);
                     }
@@ -691,7 +689,7 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                         for (int u = 0; u < MS; u++) {
                             Words<NST, EXT, XG> W1;
                             load_words<NST, EXT, XG>(W1, rp, pp, xgp, u);
-                            mstep<NST, XF32, EXT, XG, 1, MC != 0>(W1, lds, cbs, xb, xbl, acc, sc);
+                            mstep<NST, XF32, EXT, XG, 1>(W1, cbs, xb, xbl, acc, sc);
                         }
                     }
                 }
@@ -1027,14 +1025,13 @@ struct FastShape {
  * values and 8 of pad) and 8 more between columns. */
 static int fast_xstride(int cols, int S) { (void) S; return 264 * (cols / 128) + 8; }
 
-/* LDS bytes per stage codebook in the block kernel: a fixed 32 KB in the
- * several-column kernels with 12-bit indices (nc <= 4096), else nc * 8 (a
- * several-column call that runs the generic kernel gets the 32 KB too, more
- * than it uses) */
-static size_t fast_cbs(int nc, int ncol) { return nc > 4096 || ncol == 1 ? (size_t) nc * 8 : kCbStride12; }
+/* LDS bytes per stage codebook in the block kernel: a fixed 32 KB for
+ * 12-bit indices (nc <= 4096; a smaller codebook leaves the rest unused),
+ * else nc * 8 */
+static size_t fast_cbs(int nc) { return nc > 4096 ? (size_t) nc * 8 : kCbStride12; }
 
 static size_t fast_lds(const VqCall & c, int nst, int S, int W, int xg = 0) {
-    return (size_t) nst * fast_cbs(c.nc, c.ncol) +
+    return (size_t) nst * fast_cbs(c.nc) +
            (xg ? 0 : (size_t) (c.xf32 ? 2 : 1) * c.ncol * fast_xstride(c.cols, S)) +
            (size_t) W * kRedStride * 4 + kXrBytes;
 }

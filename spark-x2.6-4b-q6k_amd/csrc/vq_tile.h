@@ -97,18 +97,16 @@ __device__ __forceinline__ h4 cw_read(uint32_t a) {
     return *(lds_h4 *) (size_t) a;
 }
 
-/* cbs: LDS bytes from one stage's codebook to the next (a constant in the
- * several-column 12-bit kernels, so the second stage's offset is an
- * immediate). ABS: gather by absolute LDS address (cw_read); otherwise from
- * the array `lds` (a base add per gather). The several-column kernels gather
- * by absolute address (verify step 2087 -> 2060 us); the one-column kernels
- * measured slower that way and keep the base add. */
-template <int NST, int XF32, int EXT, int XG = 0, int SCX = 0, int ABS = 0>
-__device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, const uint8_t * lds, uint32_t cbs,
-                                      const uint8_t * xb, const uint8_t * xbl, f4 * acc, float sc = 1.0f,
-                                      u16x2 * xm = nullptr) {
+/* cbs: LDS bytes from one stage's codebook to the next (32 KB for 12-bit
+ * indices, so the second stage's offset is an immediate). Every gather goes
+ * by absolute LDS address (cw_read): against a base add per gather, the
+ * several-column verify step went 2087 -> 2060 us and, once two codewords
+ * shared an MFMA, the one-column decode set 1534-1538 -> 1516-1520 us. */
+template <int NST, int XF32, int EXT, int XG = 0, int SCX = 0>
+__device__ __forceinline__ void mstep(const Words<NST, EXT, XG> & W, uint32_t cbs, const uint8_t * xb,
+                                      const uint8_t * xbl, f4 * acc, float sc = 1.0f, u16x2 * xm = nullptr) {
     h4 cw[8][NST], b[8], bl[8];
-    auto rd = [&](uint32_t a) -> h4 { return ABS ? cw_read(a) : *(const h4 *) (lds + a); };
+    auto rd = [](uint32_t a) -> h4 { return cw_read(a); };
 #pragma unroll
     for (int s = 0; s < NST; s++) {
         cw[0][s] = rd(step_addr<0, NST, EXT, XG>(W, s, cbs));
