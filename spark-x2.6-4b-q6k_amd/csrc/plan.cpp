@@ -114,9 +114,10 @@ int sparkmv_plan_add_vq(void * plan, const sparkmv_vq_matrix * mats, int nmat, i
     c.variant = variant;
     if (nmat == 1 && ncols > 1 && mats[0].rows > 0) {
         /* words for workgroups that share a tile (the kernel leaves them
-         * zero): allocated here, so running the plan allocates nothing, and
-         * cleared on the stream of the plan's next run or capture */
-        const size_t n = (size_t) mats[0].rows * ncols;
+         * zero), enough for the deepest chunk tree: allocated here, so
+         * running the plan allocates nothing, and cleared on the stream of
+         * the plan's next run or capture */
+        const size_t n = (size_t) mats[0].rows * ncols * (size_t) vq_ck_words(kVqCkMaxGroups);
         void * q = nullptr;
         hipError_t e = hipMalloc(&q, n * sizeof(uint64_t));
         if (e != hipSuccess) return fail_hip("plan shared-tile words", e);

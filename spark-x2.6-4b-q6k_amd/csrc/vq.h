@@ -28,14 +28,27 @@ struct VqCall {
     int variant;   /* 0 auto, 1 generic, 2 LDS-codebook wave kernel, 3 MFMA block kernel */
     int threads;   /* workgroup width, a multiple of 64; 0 = the default */
     int grid;      /* workgroups; 0 = the default */
-    /* Zeroed 64-bit words, at least rows * ncol of them, through which two
-     * workgroups that share a tile's K chunks meet (several columns with x
-     * read from global memory, one matrix); null keeps every tile inside one
-     * workgroup. They are zero again when a launch ends; launches that share
-     * them must not overlap. */
+    /* Zeroed 64-bit words (kslot_cap of them) through which workgroups that
+     * share a tile's K chunks meet (several columns, one matrix): two of
+     * them per element with x read from global memory (rows * ncol words),
+     * or chunk groups in a tree with x staged per group (rows * ncol *
+     * vq_ck_words(groups)); null keeps every tile inside one workgroup. They are
+     * zero again when a launch ends; launches that share them must not
+     * overlap. */
     uint64_t * kslot = nullptr;
     long kslot_cap = 0;
 };
+
+/* Chunk-split tiles: at most this many chunk groups per tile, whose sums
+ * meet in a binary tree of vq_ck_words(groups) exchange words per output
+ * element (the nodes of each level: half the subtrees of the level below,
+ * rounded up). */
+constexpr int kVqCkMaxGroups = 8;
+inline int vq_ck_words(int C) {
+    int t = 0;
+    for (int n = C; n > 1; n = (n + 1) >> 1) t += (n + 1) >> 1;
+    return t;
+}
 
 /* The kernel a profile's gemv entry (tools/vq/gpu/vq-profile.h, the
  * reference's variant numbering) asks for on one geometry, re-checked for

@@ -107,11 +107,26 @@ struct FastArgs {
      * on which comes second), writes y and clears the word. */
     int sk;
     uint64_t * kslot;
+    /* Chunk-split tiles (MC == 3, several columns, one matrix): a tile's K
+     * is ck * C chunks; workgroup b works chunk group g = b % ck (chunks
+     * g * C .. g * C + C - 1, one wave each, added in LDS in order) of the T
+     * tiles from (b / ck) * T, with x staged for that group only. A tile's
+     * ck group sums meet in a binary tree of exchange words: at each level
+     * the two sides of a node exchange their sums in kslot[(node_base +
+     * node) * rows * ncol + row * ncol + col], and the one that finds the
+     * other's adds the two (addition commutes), clears the word and carries
+     * the sum to the next level; the root's carrier writes y. The tree's
+     * shape is fixed by ck, so the bits do not depend on the order of
+     * arrival. */
+    int ck;
 };
 
 constexpr int kFastMats = 4;
 /* several-column launches read x from global memory when a shape allows */
 constexpr int kFastXg = 1;
+/* several-column launches of one matrix split tiles by K chunk when the
+ * caller gives exchange words */
+constexpr int kFastCk = 1;
 
 constexpr int kRedStride = 16 * 17;   /* floats per wave of the LDS reduction area */
 /* LDS stride between the stages' codebooks for 12-bit indices (nc <= 4096) */
@@ -139,6 +154,8 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * so the norm needs no launch of its own. */
     static_assert(!XN || (MC == 0 && MSC > 0 && !XF32), "the fused norm stages one bf16 column");
     constexpr int XG = MC == 2 ? 1 : 0;
+    constexpr int CK = MC == 3 ? 1 : 0;
+    static_assert(!CK || (MSC > 0 && !XF32 && !XN), "chunk-split tiles run straight-line bf16 units");
     constexpr int D = MSC > 0 ? MSC : 8;
     /* straight-line units keep at most kLook macro steps of index words in
      * flight per wave: with every step requested up front the memory system
@@ -185,21 +202,26 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
      * or, with shared tiles, this wave's one (tile, chunk) unit */
     const bool sk = XG && A.sk;
     const int W = A.threads >> 6;
-    const int usk = ((int) blockIdx.x - M.wg0) * W + wave;
-    const int t0 = sk ? usk / C : ((int) blockIdx.x - M.wg0) * A.T;
+    const int wb = (int) blockIdx.x - M.wg0;       /* the workgroup within its matrix */
+    const int usk = wb * W + wave;
+    /* chunk-split tiles: chunk group cg of the workgroup's tiles */
+    const int cg = CK ? wb % A.ck : 0;
+    const int t0 = sk ? usk / C : (CK ? wb / A.ck : wb) * A.T;
     const int t1 = sk ? M.tiles : min(t0 + A.T, M.tiles);
     const int j = sk ? 0 : wave / C;               /* tile slot */
-    const int c = sk ? usk - t0 * C : wave - j * C;  /* K chunk */
+    const int c = sk ? usk - t0 * C : wave - j * C;  /* K chunk (of the group with chunk-split tiles) */
     const int MP = A.M >> A.lgS;                   /* macro steps per part */
     const int MS = MSC > 0 ? MSC : MP / C;         /* macro steps per unit */
     const int r_in = m16 >> A.lgS, h = m16 & (S - 1);  /* A side: tile row, part */
     const int hp = m16 / ncol, cn = m16 - hp * ncol;   /* B side: part, activation column */
     const bool bval = hp < S;
-    const int msa = h * MP + c * MS;
+    const int msa = h * MP + (cg * C + c) * MS;
     const int msb = (bval ? hp : 0) * MP + c * MS;
     /* x in LDS: 128 columns (one macro step) per 264 bytes, the 8-byte pad
-     * putting the parts that lanes read at once on different banks */
-    const uint8_t * xb = lx + (bval ? cn : 0) * A.xstride + 264 * msb + 64 * q;
+     * putting the parts that lanes read at once on different banks. With
+     * chunk-split tiles only the group's C * MS steps of each part are
+     * staged, part after part. */
+    const uint8_t * xb = lx + (bval ? cn : 0) * A.xstride + 264 * (CK ? ((bval ? hp : 0) * C + c) * MS : msb) + 64 * q;
     const uint8_t * xbl = xb + ncol * A.xstride;
     const int iters = sk ? 1 : (t1 - t0 + T - 1) / T;
     const uint32_t stream_off = A.gain_off + (uint32_t) rows * 2u;
@@ -324,7 +346,15 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                 for (int k = 0; k < KS; k++)
                     ((u4v *) (lds + s * cbs))[min(k * bd + tid, n16 - 1)] = cv[s][k];
         }
-        const int xq = A.cols >> 3, nx = XG ? 0 : ncol * xq;
+        /* 8-column pieces of x per activation column; chunk-split tiles
+         * stage the group's C * MS steps of each part, whose piece cc comes
+         * from piece xsrc(cc) of the row */
+        const int xq = CK ? S * C * MS * 16 : A.cols >> 3, nx = XG ? 0 : ncol * xq;
+        auto xsrc = [&](int cc) {
+            if constexpr (!CK) return cc;
+            const int hh = cc / (C * MS * 16);
+            return (hh * MP + cg * C * MS) * 16 + cc - hh * C * MS * 16;
+        };
         for (int base = 0; base < nx; base += KXM * bd) {
             u4v xv[KXM];
             int ci[KXM];
@@ -333,7 +363,8 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                 ci[k] = min(base + k * bd + tid, nx - 1);
                 const int n = ci[k] / xq, cc = ci[k] - n * xq;
                 /* a slot wholly past x (uniform) would only repeat the last chunk */
-                if (base + k * bd < nx) xv[k] = *(const u4v *) ((const uint16_t *) A.x + (size_t) n * A.ldx + 8 * cc);
+                if (base + k * bd < nx)
+                    xv[k] = *(const u4v *) ((const uint16_t *) A.x + (size_t) n * A.ldx + 8 * xsrc(cc));
             }
 #pragma unroll
             for (int k = 0; k < KXM; k++) {
@@ -580,18 +611,27 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
     int xk = 0;
     if constexpr (XG == 0) {
         if (xr_out(xr)) {
+            /* staged columns per activation column (chunk-split tiles: the
+             * group's steps of each part; staged column kl is row column
+             * xcol(kl)) */
+            const int xl = CK ? S * C * MS * 128 : A.cols;
+            auto xcol = [&](int kl) {
+                if constexpr (!CK) return kl;
+                const int hh = kl / (C * MS * 128);
+                return (hh * MP + cg * C * MS) * 128 + kl - hh * C * MS * 128;
+            };
             auto xval = [&](int e) {
-                const int n = e / A.cols, kk = e - n * A.cols;
+                const int n = e / xl, kk = xcol(e - n * xl);
                 const size_t xi = (size_t) n * A.ldx + kk;
                 if (XN) return __uint_as_float(bf16_rne((((const float *) A.x)[kk] * xinv) * A.nw[kk]) << 16);
                 return XF32 ? ((const float *) A.x)[xi] : bf16_to_f32(((const uint16_t *) A.x)[xi]);
             };
             uint32_t fm = 0;   /* the largest finite |x| of this thread's elements */
-            for (int e = tid; e < ncol * A.cols; e += bd) fm = max(fm, xr_fin(xr_mag(xval(e))));
+            for (int e = tid; e < ncol * xl; e += bd) fm = max(fm, xr_fin(xr_mag(xval(e))));
             xk = xr_shift(xr, fm);
             if (xk) {
-                for (int e = tid; e < ncol * A.cols; e += bd) {
-                    const int n = e / A.cols, kk = e - n * A.cols;
+                for (int e = tid; e < ncol * xl; e += bd) {
+                    const int n = e / xl, kk = e - n * xl;
                     const float f = __builtin_ldexpf(xval(e), -xk);
                     const _Float16 hi = (_Float16) f;
                     const int off = 264 * (kk >> 7) + 2 * (kk & 127);
@@ -757,7 +797,8 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
         }
         /* with one wave per tile the wave only reads its own area back: its
          * LDS operations complete in order, no workgroup barrier needed */
-        if (C > 1) {
+        const int Cw = C;
+        if (Cw > 1) {
             __syncthreads();
         } else {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -769,14 +810,14 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
          * tiles the tile's first wave in this workgroup adds the nin chunk
          * waves that follow it here; a tile split over two workgroups then
          * meets the other half's sum through kslot. */
-        const int nin = sk ? min(C - c, W - wave) : C;
+        const int nin = sk ? min(C - c, W - wave) : Cw;
         const bool split = sk && (c != 0 || nin < C);
         if (active && (c == 0 || (sk && wave == 0))) {
             for (int e = lane; e < rpt * ncol; e += 64) {
                 const int r = ncol == 1 ? e : e / ncol, col = e - r * ncol;
                 const int row = tile * rpt + r;
                 float sum = 0.0f;
-                if (C == 1) {
+                if (Cw == 1) {
                     /* all S reads issued together (parts past S re-read the
                      * last one and add nothing), added in part order */
                     float part[16];
@@ -808,11 +849,33 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                             __hip_atomic_store(sl, (uint64_t) 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         }
                     }
+                    if constexpr (CK) {
+                        /* the group sums' tree: idx is this sum's subtree
+                         * among n at the level, whose nodes start at base;
+                         * a subtree without a sibling passes up unchanged */
+                        const size_t nrc = (size_t) rows * ncol, at = (size_t) row * ncol + col;
+                        int idx = cg, n = A.ck, base = 0;
+                        while (last && n > 1) {
+                            if ((idx ^ 1) < n) {
+                                uint64_t * sl = A.kslot + (size_t) (base + (idx >> 1)) * nrc + at;
+                                const uint64_t old = __hip_atomic_exchange(sl, (1ull << 32) | __float_as_uint(sum),
+                                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                last = (uint32_t) (old >> 32) == 1u;
+                                if (last) {
+                                    sum = __uint_as_float((uint32_t) old) + sum;
+                                    __hip_atomic_store(sl, (uint64_t) 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                }
+                            }
+                            base += (n + 1) >> 1;
+                            idx >>= 1;
+                            n = (n + 1) >> 1;
+                        }
+                    }
                     if (last) *yp = (A.accumulate ? *yp : 0.0f) + sum;
                 }
             }
         }
-        if (C > 1) {
+        if (Cw > 1) {
             __syncthreads();
         } else {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1019,6 +1082,7 @@ struct FastShape {
     size_t lds;
     int xg;   /* several columns with x read from global memory (no x in LDS) */
     int sk;   /* shared tiles: W (tile, chunk) units per workgroup */
+    int ck;   /* chunk-split tiles: groups of C chunks per tile (0: none) */
 };
 
 /* LDS bytes per activation column: 264 bytes per 128 columns (256 of f16
@@ -1107,8 +1171,64 @@ static int fast_shape_xg(const VqCall & c, int nst, FastShape & sh) {
     return 0;
 }
 
+/* Chunk-split tiles: several bf16 columns of one matrix whose x is too large
+ * to stage whole (the same 48 KB as above), when the caller gave exchange
+ * words for the tree (vq_ck_words(ck) per output element). A tile's K is ck
+ * groups of C chunks; each workgroup stages one group's x and runs it for T
+ * tiles (T * C waves, the group's chunks added in LDS), and the ck group
+ * sums of a tile meet in the tree, whose levels are memory round trips
+ * (about 0.65 us each, measured). Shape: fewest rounds of workgroups over
+ * the CUs, then the shortest unit plus tree, then the fewest waves. */
+static int fast_shape_ck(const VqCall & c, int nst, FastShape & sh) {
+    if (!kFastCk || !c.kslot || c.nmat != 1 || c.ncol < 2 || c.xf32 || c.nc % 2 || ((uintptr_t) c.x & 15u) ||
+        c.ldx % 8)
+        return -1;
+    if ((long) c.ncol * c.cols < 24576) return -1;
+    const int M = c.cols / 128, G = cu_count(), n16 = c.nc * 8 / 16;
+    long best = -1;
+    for (int s = 1; s <= 16; s *= 2) {
+        if (s * c.ncol > 16 || M % s) continue;
+        const int MP = M / s;
+        const long tiles = (c.mats[0].rows * (long) s + 15) / 16;
+        for (int gk = 2; gk <= kVqCkMaxGroups; gk++) {
+            if ((long) c.mats[0].rows * c.ncol * vq_ck_words(gk) > c.kslot_cap) continue;
+            int lv = 0;
+            for (int n = gk; n > 1; n = (n + 1) >> 1) lv++;
+            for (int cc = 1; cc <= 10; cc++) {
+                if (MP % (gk * cc)) continue;
+                const int ms = MP / (gk * cc);
+                if (ms != 2 && ms != 4 && ms != 5 && ms != 8 && (ms != 10 || c.nc > 4096)) continue;
+                for (int tt = 1; tt * cc <= 10; tt++) {
+                    if (5 * 64 * tt * cc < n16) continue;   /* the codebooks in 5 chunks per thread */
+                    const long nwg = (tiles + tt - 1) / tt * gk;
+                    const size_t lds = (size_t) nst * fast_cbs(c.nc) +
+                                       (size_t) c.ncol * fast_xstride(s * cc * ms * 128, s) +
+                                       (size_t) tt * cc * kRedStride * 4 + kXrBytes;
+                    if (lds > (size_t) kLdsMax) continue;
+                    const long cost = (nwg + G - 1) / G * (8 + ms * cc + 2 * lv) * 64 + tt * cc;
+                    if (best < 0 || cost < best) {
+                        best = cost;
+                        sh.S = s; sh.C = cc; sh.T = tt; sh.W = tt * cc; sh.nwg = (int) nwg; sh.lds = lds;
+                        sh.xg = 0; sh.sk = 0; sh.ck = gk;
+                    }
+                }
+            }
+        }
+    }
+    return best < 0 ? -1 : 0;
+}
+
 static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
-    if (kFastXg && fast_shape_xg(c, nst, sh) == 0) return 0;
+    sh.ck = 0;
+    if (kFastXg && fast_shape_xg(c, nst, sh) == 0) {
+        /* where x from global memory would take shared tiles (whole tiles
+         * leave CUs idle), chunk-split tiles instead: N = 8 down 14.7 ->
+         * 13.1-13.6 us, measured; for o (whole tiles on 160 CUs) they gave
+         * -0.45 and +0.2 us on two boxes, and o keeps its shape */
+        FastShape ck;
+        if (sh.sk && fast_shape_ck(c, nst, ck) == 0) sh = ck;
+        return 0;
+    }
     sh.xg = 0;
     sh.sk = 0;
     const int M = c.cols / 4 / 32;
@@ -1208,6 +1328,21 @@ static int launch_ms_norm(const FastArgs & A, int MS, int grid, int threads, siz
 template <int NST, int XF32, int EXT>
 static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, size_t lds, hipStream_t s) {
     if constexpr (!XF32) {
+        if (mc == 3) {
+            /* chunk-split tiles: the search kept to these unit lengths */
+            switch (MS) {
+                case 2: return launch_fast_t<NST, 0, EXT, 2, 3>(A, grid, threads, lds, s);
+                case 4: return launch_fast_t<NST, 0, EXT, 4, 3>(A, grid, threads, lds, s);
+                case 5: return launch_fast_t<NST, 0, EXT, 5, 3>(A, grid, threads, lds, s);
+                case 8: return launch_fast_t<NST, 0, EXT, 8, 3>(A, grid, threads, lds, s);
+                case 10:
+                    if constexpr (!EXT) return launch_fast_t<NST, 0, EXT, 10, 3>(A, grid, threads, lds, s);
+                    break;
+                default: break;
+            }
+            set_error("no chunk-split kernel for units of %d macro steps", MS);
+            return -1;
+        }
         if (mc == 2) {
             /* x from global memory: the shape search kept to these unit lengths */
             switch (MS) {
@@ -1316,10 +1451,11 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     while ((1 << A.lgS) < sh.S) A.lgS++;
     A.C = sh.C; A.T = sh.T;
     A.sk = sh.sk;
-    A.kslot = sh.sk ? c.kslot : nullptr;
+    A.ck = sh.ck;
+    A.kslot = sh.sk || sh.ck ? c.kslot : nullptr;
     A.M = mk;
     A.kofs = k0;
-    A.xstride = sh.xg ? 0 : fast_xstride(part.cols, sh.S);
+    A.xstride = sh.xg ? 0 : sh.ck ? fast_xstride(mk * 128 / sh.ck, sh.S) : fast_xstride(part.cols, sh.S);
     int wg = 0;
     for (int m = 0; m < c.nmat; m++) {
         for (int s = 0; s < nst; s++) A.mat[m].st[s] = (const uint8_t *) c.mats[m].stages[st0 + s];
@@ -1327,7 +1463,9 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
         A.mat[m].rows = c.mats[m].rows;
         A.mat[m].tiles = (int) ((c.mats[m].rows * (long) sh.S + 15) / 16);
         A.mat[m].wg0 = wg;
-        A.mat[m].nwg = sh.sk ? (A.mat[m].tiles * sh.C + sh.W - 1) / sh.W : (A.mat[m].tiles + sh.T - 1) / sh.T;
+        A.mat[m].nwg = sh.sk   ? (A.mat[m].tiles * sh.C + sh.W - 1) / sh.W
+                       : sh.ck ? (A.mat[m].tiles + sh.T - 1) / sh.T * sh.ck
+                               : (A.mat[m].tiles + sh.T - 1) / sh.T;
         wg += A.mat[m].nwg;
     }
     const int threads = sh.W * 64;
@@ -1342,12 +1480,12 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
     const int one_col = sh.C == 1 && !((uintptr_t) A.x & 15u) && n16 <= 5 * threads && part.cols <= 16 * threads;
     const int multi_col = c.ncol > 1 && !((uintptr_t) A.x & 15u) && c.ldx % 8 == 0 && n16 <= 5 * threads;
     const int straight = (!c.xf32 || c.ncol == 1) && c.nc % 2 == 0 && (c.ncol > 1 ? multi_col : one_col);
-    const int MS = sh.xg ? A.M / sh.S / sh.C : straight ? A.M / sh.S / sh.C : 0;
+    const int MS = sh.xg ? A.M / sh.S / sh.C : sh.ck ? A.M / sh.S / sh.C / sh.ck : straight ? A.M / sh.S / sh.C : 0;
     /* the multi-column kernels: x from global memory (2) or staged in LDS (1;
      * MS without its own instantiation runs their ring form); any other
      * several-column call runs the generic kernel, which the shape search
      * kept within 10 waves */
-    const int mc = sh.xg ? 2 : c.ncol > 1 && straight;
+    const int mc = sh.ck ? 3 : sh.xg ? 2 : c.ncol > 1 && straight;
     if (pair) {
         /* the pair's activation is written by the one-column straight-line
          * kernels over the whole row, both stages in this launch */

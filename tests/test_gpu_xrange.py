@@ -172,6 +172,61 @@ def test_vq_gemv_non_finite_x(sm, ref, dev, rows, cols, ncol):
         assert per_col_err(got[1:], xf[1:], W) <= TIGHT
 
 
+def run_vq_plan(sm, dev, dc, xf, rows):
+    """One several-column op in a plan (the plan gives it exchange words, so
+    a matrix whose x is too large to stage whole splits its tiles by K chunk
+    and stages each chunk's x)."""
+    import torch
+    ncol = xf.shape[0]
+    x = to_dev(xf, dev, False)
+    y = torch.full((ncol, rows), float("nan"), device=dev)
+    plan = sm.Plan()
+    plan.add_vq([dc], x, [y], ncols=ncol)
+    plan.run(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def test_vq_plan_chunk_split_range(sm, ref, dev):
+    """Chunk-split tiles (the verify set's down shape, 2560 x 10240 at N = 8,
+    in a plan): every workgroup checks the range of the x chunk it staged and
+    rescales it by a power of two of its own, and the chunk sums are brought
+    back before they meet. Scaling x by 2^20 and 2^-30 scales y bit for bit;
+    one element of 2^18 (1 + 2^-7) per column, and column 0 alone 2^20 times
+    larger, meet the bar; an infinity gives non-finite y exactly where the
+    f64 product does and leaves the other columns at the bar."""
+    rows, cols, ncol = 2560, 10240, 8
+    data = sm.synth_container(0x6C01, rows, cols)
+    W = ref.decode(data).astype(np.float64)
+    dc = sm.DeviceContainer(data)
+    xf = base_x(sm, 0x6C02, ncol, cols)
+    y0 = run_vq_plan(sm, dev, dc, xf, rows)
+    assert per_col_err(y0, xf, W) <= TIGHT
+    for sh in (20, -30):
+        xs = np.ldexp(xf, sh).astype(np.float32)
+        ys = run_vq_plan(sm, dev, dc, xs, rows)
+        err = per_col_err(ys, xs, W)
+        same = np.array_equal(ys, np.ldexp(y0, sh).astype(np.float32))
+        print(f"chunk-split x*2^{sh}: relL2 {err:.2e}, bit-exact scaling {same}")
+        assert err <= TIGHT and same
+    xp = xf.copy()
+    xp[:, 7] = 264192.0
+    err = per_col_err(run_vq_plan(sm, dev, dc, xp, rows), xp, W)
+    xm = base_x(sm, 0x6C03, ncol, cols)
+    xm[0] = np.ldexp(xm[0], 20)
+    err_m = per_col_err(run_vq_plan(sm, dev, dc, xm, rows), xm, W)
+    print(f"chunk-split spike relL2 {err:.2e}, mixed columns {err_m:.2e}")
+    assert err <= TIGHT and err_m <= TIGHT
+    xn = xf.copy()
+    xn[0, 5000] = np.inf
+    got = run_vq_plan(sm, dev, dc, xn, rows)
+    with np.errstate(invalid="ignore"):
+        want = xn.astype(np.float64) @ W.T
+    assert not np.isfinite(got[0]).any()
+    assert np.array_equal(np.isfinite(got), np.isfinite(want))
+    assert per_col_err(got[1:], xn[1:], W) <= TIGHT
+
+
 # kind, rows, cols, columns, f32 x: Q8_0 one column and four rows per lane;
 # Q6_K staged rows (even superblocks per row), the wide form (odd, at most
 # 12288 columns) and the plain one (odd, wider).
