@@ -923,6 +923,11 @@ struct Model {
     float * h, * xn, * qkv, * g, * attn, * mg, * mu, * act, * kv;
     uint16_t * xn16, * attn16, * act16;
     uint64_t * pslot;                    /* the gate/up launch's row exchange, intermediate words, kept zero */
+    /* exchange words of the several-column launches over hidden rows (the
+     * chunk-split tiles' tree), kept zero; the launches share them, one at
+     * a time on the model's stream */
+    uint64_t * kslot;
+    long kslot_cap;
     /* gelu * up written by the gate/up launch (1), or by the activation
      * kernel (0: SPARKMV_SEPARATE_ACT=1 at creation; the same bits, slower) */
     int fuse_act = 1;
@@ -981,6 +986,10 @@ int gemv(const Model & m, const void * const * st, int rows, int cols, const voi
     c.mats = &d; c.nmat = 1;
     c.x = x; c.ldx = cols; c.xf32 = m.c.x_dtype == SPARKMV_X_F32; c.ncol = ncol; c.ldy = ldy ? ldy : rows;
     c.accumulate = acc; c.stream = s;
+    if (ncol > 1) {
+        c.kslot = m.kslot;
+        c.kslot_cap = m.kslot_cap;
+    }
     const auto it = m.picks.find({rows, cols});
     if (it != m.picks.end()) { c.variant = it->second.first; c.threads = it->second.second; }
     return vq_launch(c);
@@ -1124,6 +1133,8 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     const size_t o_part = take((size_t) c.heads * nch_max * (c.head_dim + 2) * 4);
     const size_t o_rtab = take(512 * 4);
     const size_t o_pslot = take((size_t) c.intermediate * 8);
+    const size_t n_kslot = (size_t) c.hidden * kMaxCols * vq_ck_words(kVqCkMaxGroups);
+    const size_t o_kslot = take(n_kslot * 8);
     hipError_t e = hipMalloc(&m->mem, off);
     if (e != hipSuccess) {
         fail_hip("model buffers", e);
@@ -1132,13 +1143,16 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     }
     uint8_t * b = (uint8_t *) m->mem;
     e = hipMemset(b + o_pslot, 0, (size_t) c.intermediate * 8);
+    if (e == hipSuccess) e = hipMemset(b + o_kslot, 0, n_kslot * 8);
     if (e != hipSuccess) {
-        fail_hip("model pair slots", e);
+        fail_hip("model exchange words", e);
         (void) hipFree(m->mem);
         delete m;
         return nullptr;
     }
     m->pslot = (uint64_t *) (b + o_pslot);
+    m->kslot = (uint64_t *) (b + o_kslot);
+    m->kslot_cap = (long) n_kslot;
     const char * sep = getenv("SPARKMV_SEPARATE_ACT");
     m->fuse_act = !(sep && sep[0] == '1');
     m->h = (float *) (b + o_h); m->xn = (float *) (b + o_xn); m->qkv = (float *) (b + o_qkv);
