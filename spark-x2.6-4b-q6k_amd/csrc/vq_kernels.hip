@@ -1271,8 +1271,9 @@ static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
         /* Several columns: codebooks plus N columns of x leave room for one
          * workgroup per CU, so the shape that matters is the number of rounds
          * of workgroups over the CUs. Search parts S, K chunks C and tiles T
-         * (up to 16 waves) for the fewest rounds, then the shortest unit,
-         * preferring unit lengths with a straight-line kernel. */
+         * (up to 16 waves) for the fewest rounds, then the shortest unit plus
+         * chunk partials, preferring unit lengths with a straight-line
+         * kernel. */
         /* 16 waves only in the multi-column kernels (bf16 x, even codebook,
          * 16-byte aligned x rows, at least 5 codebook chunks' worth of threads) */
         const int mc_ok = !c.xf32 && c.nc % 2 == 0 && !((uintptr_t) c.x & 15u) && c.ldx % 8 == 0;
@@ -1292,7 +1293,11 @@ static int fast_shape(const VqCall & c, int nst, FastShape & sh) {
                     if (lds > (size_t) kLdsMax) continue;
                     const long rounds = (nwg + G - 1) / G;
                     const int straight = ms == 2 || ms == 4 || ms == 5 || ms == 8 || ms == 10;
-                    const long cost = rounds * (8 + ms + (straight ? 0 : ms)) * 64 + tt * cc;
+                    /* each chunk beyond the first adds an LDS partial and a
+                     * barrier to the tile's epilogue (N = 8 q+k+v+g: 8-row
+                     * tiles of 2 chunks, 9.15 us, against 16-row tiles of
+                     * 5 shorter chunks, 9.63 us) */
+                    const long cost = rounds * (8 + ms + (straight ? 0 : ms) + cc - 1) * 64 + tt * cc;
                     if (best < 0 || cost < best) {
                         best = cost;
                         sh.S = s; sh.C = cc; sh.T = tt; sh.W = tt * cc; sh.nwg = (int) nwg; sh.lds = lds;
