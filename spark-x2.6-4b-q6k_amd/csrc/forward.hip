@@ -922,7 +922,7 @@ struct Model {
     void * mem = nullptr;
     float * h, * xn, * qkv, * g, * attn, * mg, * mu, * act, * kv;
     uint16_t * xn16, * attn16, * act16;
-    uint64_t * pslot;                    /* the gate/up launch's row exchange, intermediate words, kept zero */
+    uint64_t * pslot;                    /* the gate/up launches' exchange, intermediate * kMaxCols words, kept zero */
     /* exchange words of the several-column launches over hidden rows (the
      * chunk-split tiles' tree), kept zero; the launches share them, one at
      * a time on the model's stream */
@@ -1023,6 +1023,35 @@ int gemv2(const Model & m, const void * const * st0, int rows0, float * y0, cons
  * norm launch and gemv2. */
 int rmsnorm(const Model & m, const float * x, const float * w, hipStream_t s, int ncol = 1, float * out = nullptr,
             uint16_t * out16 = nullptr);
+
+/* gate and up over the N columns of x (bf16 or f32 [N][cols]) into mg / mu
+ * [N][rows], then act / act16 = gelu(gate) * up: written by the gate/up
+ * launch itself where the several-column kernel takes the shape (bf16
+ * activations, no tuning profile, the activation not switched apart), else
+ * by the activation kernel. */
+int gate_up_act_n(const Model & m, const void * const * gate, const void * const * up, int rows, int cols,
+                  const void * x, float * mg, float * mu, float * act, uint16_t * act16, hipStream_t s, int N) {
+    const bool b16 = m.c.x_dtype == SPARKMV_X_BF16;
+    if (b16 && m.fuse_act && m.picks.empty()) {
+        VqMatDesc d[2];
+        memset(d, 0, sizeof d);
+        for (int i = 0; i < m.c.nstages; i++) { d[0].stages[i] = gate[i]; d[1].stages[i] = up[i]; }
+        d[0].y = mg; d[0].rows = rows;
+        d[1].y = mu; d[1].rows = rows;
+        VqCall c;
+        memset(&c, 0, sizeof c);
+        c.dim = m.c.dim; c.nc = m.c.nc; c.cols = cols; c.v3 = m.c.v3; c.nst = m.c.nstages;
+        c.mats = d; c.nmat = 2;
+        c.x = x; c.ldx = cols; c.xf32 = 0; c.ncol = N; c.ldy = rows;
+        c.accumulate = 0; c.stream = s;
+        const VqPair pair{m.pslot, rows * kMaxCols, act, act16};
+        const int rc = vq_pair_launch(c, pair);
+        if (rc <= 0) return rc;
+    }
+    if (gemv2(m, gate, rows, mg, up, rows, mu, cols, x, s, N, rows)) return -1;
+    hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * rows + 255) / 256), dim3(256), 0, s, mg, mu, act, act16, N * rows);
+    return check_launch("gelu launch");
+}
 
 int norm_gemv2(const Model & m, const float * h, const float * w, const void * const * st0, int rows0, float * y0,
                const void * const * st1, int rows1, float * y1, int cols, hipStream_t s, const VqPair * pair = nullptr,
@@ -1132,7 +1161,8 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
     const size_t o_st = take(2 * sizeof(int));
     const size_t o_part = take((size_t) c.heads * nch_max * (c.head_dim + 2) * 4);
     const size_t o_rtab = take(512 * 4);
-    const size_t o_pslot = take((size_t) c.intermediate * 8);
+    const size_t n_pslot = (size_t) c.intermediate * kMaxCols;
+    const size_t o_pslot = take(n_pslot * 8);
     const size_t n_kslot = (size_t) c.hidden * kMaxCols * vq_ck_words(kVqCkMaxGroups);
     const size_t o_kslot = take(n_kslot * 8);
     hipError_t e = hipMalloc(&m->mem, off);
@@ -1142,7 +1172,7 @@ void * sparkmv_model_create(const sparkmv_model_cfg * cfg) {
         return nullptr;
     }
     uint8_t * b = (uint8_t *) m->mem;
-    e = hipMemset(b + o_pslot, 0, (size_t) c.intermediate * 8);
+    e = hipMemset(b + o_pslot, 0, n_pslot * 8);
     if (e == hipSuccess) e = hipMemset(b + o_kslot, 0, n_kslot * 8);
     if (e != hipSuccess) {
         fail_hip("model exchange words", e);
@@ -1443,12 +1473,9 @@ int block(Model * m, const uint32_t * tokens, int N, int pos, float * logits, hi
                  c.hidden))
             return -1;
         if (rmsnorm(*m, m->vh, L.post_norm, s, N, m->vxn, m->vxn16)) return -1;
-        if (gemv2(*m, L.gate, c.intermediate, m->vmg, L.up, c.intermediate, m->vmu, c.hidden, xin, s, N,
-                  c.intermediate))
+        if (gate_up_act_n(*m, L.gate, L.up, c.intermediate, c.hidden, xin, m->vmg, m->vmu, m->vact,
+                          b16 ? m->vact16 : nullptr, s, N))
             return -1;
-        hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * c.intermediate + 255) / 256), dim3(256), 0, s, m->vmg, m->vmu,
-                           m->vact, b16 ? m->vact16 : nullptr, N * c.intermediate);
-        if (check_launch("gelu launch")) return -1;
         if (gemv(*m, L.down, c.hidden, c.intermediate, b16 ? (const void *) m->vact16 : (const void *) m->vact, m->vh,
                  1, s, N, c.hidden))
             return -1;
@@ -1523,16 +1550,16 @@ int prompt(Model * m, int N, int pos, float * logits, hipStream_t s) {
             return -1;
         if (rmsnorm(*m, m->vh, L.post_norm, s, N, m->vxn, m->vxn16)) return -1;
         if (N <= kMaxCols) {
-            if (gemv2(*m, L.gate, c.intermediate, m->vmg, L.up, c.intermediate, m->vmu, c.hidden, xin, s, N,
-                      c.intermediate))
+            if (gate_up_act_n(*m, L.gate, L.up, c.intermediate, c.hidden, xin, m->vmg, m->vmu, m->vact,
+                              b16 ? m->vact16 : nullptr, s, N))
                 return -1;
         } else {
             if (mat_n(*m, L.gate, c.intermediate, c.hidden, xin, m->vmg, 0, s, N, c.intermediate)) return -1;
             if (mat_n(*m, L.up, c.intermediate, c.hidden, xin, m->vmu, 0, s, N, c.intermediate)) return -1;
+            hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * c.intermediate + 255) / 256), dim3(256), 0, s, m->vmg,
+                               m->vmu, m->vact, b16 ? m->vact16 : nullptr, N * c.intermediate);
+            if (check_launch("gelu launch")) return -1;
         }
-        hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * c.intermediate + 255) / 256), dim3(256), 0, s, m->vmg, m->vmu,
-                           m->vact, b16 ? m->vact16 : nullptr, N * c.intermediate);
-        if (check_launch("gelu launch")) return -1;
         if (mat_n(*m, L.down, c.hidden, c.intermediate, b16 ? (const void *) m->vact16 : (const void *) m->vact, m->vh,
                   1, s, N, c.hidden))
             return -1;

@@ -63,11 +63,11 @@ int vq_variant_ready(int dim, int nc, int rows, int cols, int v3, int variant);
 /* Validate and launch; returns 0, or -1 with the message set. */
 int vq_launch(const VqCall & c);
 /* A gate/up pair's activation written by the launch that computes the pair
- * (c.nmat == 2, equal rows, one bf16 column): besides y of both matrices,
- * act[r] = gelu(gate[r]) * up[r] (f32, when act is set) and its bf16
- * (act16, when set), the bits the separate activation kernel would write.
- * slot holds cap zeroed 64-bit words (cap >= rows) through which the two
- * matrices' rows meet; they are zero again when the launch ends, and
+ * (c.nmat == 2, equal rows, bf16 columns: one, or several staged in LDS):
+ * besides y of both matrices, act[n * rows + r] = gelu(gate[n][r]) *
+ * up[n][r] (f32, when act is set) and its bf16 (act16, when set), the bits
+ * the separate activation kernel would write. slot holds cap zeroed 64-bit
+ * words (cap >= rows * ncol) through which the two matrices' elements meet; they are zero again when the launch ends, and
  * launches that share them must not overlap. vq_norm_launch with a pair
  * does the same from the f32 residual. Both return 1 without launching when
  * the call's shape has no kernel that writes the activation; the caller

@@ -140,14 +140,16 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
 }
 
 template <int NST, int XF32, int EXT, int MSC, int MC, int XN = 0>
-__global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const FastArgs A) {
+__global__ __launch_bounds__(MC == 1 || MC == 4 ? 1024 : 640) void vq_mfma_kernel(const FastArgs A) {
     /* MSC > 0: a unit is exactly MSC macro steps, known at compile time, so
      * the whole unit runs as straight-line code and each step waits only for
      * its own index words (a loop would make the compiler wait for all of a
      * wave's loads at its head). MSC == 0: any unit length, a ring of D steps.
      * MC: the kernel for several activation columns, with x staged in LDS
-     * (1) or, XG (2), read from global memory (the L2) with each step's index
-     * words, so no x is staged and any column count fits LDS.
+     * (1; 4: the same for a gate/up pair that also writes the activation)
+     * or, XG (2), read from global memory (the L2) with each step's index
+     * words, so no x is staged and any column count fits LDS; 3: chunk-split
+     * tiles.
      * XN (one column, straight-line units): x is the f32 residual h and the
      * workgroup stages bf16(rms_norm(h) * nw) (model.rs:236-245: sum of
      * squares in f64, 1 / sqrt rounded once to f32, (h * inv) * w in f32),
@@ -872,6 +874,28 @@ __global__ __launch_bounds__(MC == 1 ? 1024 : 640) void vq_mfma_kernel(const Fas
                         }
                     }
                     if (last) *yp = (A.accumulate ? *yp : 0.0f) + sum;
+                    if constexpr (MC == 4) {
+                        {
+                            /* a gate/up pair over several columns: the two
+                             * matrices' sums of (row, col) meet in
+                             * pslot[row * ncol + col] as in the one-column
+                             * form, and the second to arrive writes
+                             * gelu(gate) * up to act [ncol][rows] */
+                            const uint32_t mi = (int) blockIdx.x >= A.mat[1].wg0 ? 1u : 0u;
+                            uint64_t * sl = A.pslot + (size_t) row * ncol + col;
+                            const uint64_t mine = ((uint64_t) (1u + mi) << 32) | __float_as_uint(sum);
+                            const uint64_t old =
+                                __hip_atomic_exchange(sl, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            if ((uint32_t) (old >> 32) == 2u - mi) {
+                                const float o = __uint_as_float((uint32_t) old);
+                                const float v = mi ? gelu_mul(o, sum) : gelu_mul(sum, o);
+                                const size_t ai = (size_t) col * rows + row;
+                                if (A.pact) A.pact[ai] = v;
+                                if (A.pact16) A.pact16[ai] = (uint16_t) bf16_rne(v);
+                                __hip_atomic_store(sl, (uint64_t) 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            }
+                        }
+                    }
                 }
             }
         }
@@ -1333,6 +1357,21 @@ static int launch_ms_norm(const FastArgs & A, int MS, int grid, int threads, siz
 template <int NST, int XF32, int EXT>
 static int launch_ms(const FastArgs & A, int MS, int mc, int grid, int threads, size_t lds, hipStream_t s) {
     if constexpr (!XF32) {
+        if (mc == 4) {
+            /* several columns of a gate/up pair that writes the activation */
+            if constexpr (!EXT) {
+                switch (MS) {
+                    case 2: return launch_fast_t<NST, 0, EXT, 2, 4>(A, grid, threads, lds, s);
+                    case 4: return launch_fast_t<NST, 0, EXT, 4, 4>(A, grid, threads, lds, s);
+                    case 5: return launch_fast_t<NST, 0, EXT, 5, 4>(A, grid, threads, lds, s);
+                    case 8: return launch_fast_t<NST, 0, EXT, 8, 4>(A, grid, threads, lds, s);
+                    case 10: return launch_fast_t<NST, 0, EXT, 10, 4>(A, grid, threads, lds, s);
+                    default: break;
+                }
+            }
+            set_error("no several-column pair kernel for units of %d macro steps", MS);
+            return -1;
+        }
         if (mc == 3) {
             /* chunk-split tiles: the search kept to these unit lengths */
             switch (MS) {
@@ -1490,14 +1529,19 @@ static int launch_fast_part(const VqCall & c, int st0, int nst, int accumulate, 
      * MS without its own instantiation runs their ring form); any other
      * several-column call runs the generic kernel, which the shape search
      * kept within 10 waves */
-    const int mc = sh.ck ? 3 : sh.xg ? 2 : c.ncol > 1 && straight;
+    int mc = sh.ck ? 3 : sh.xg ? 2 : c.ncol > 1 && straight;
     if (pair) {
-        /* the pair's activation is written by the one-column straight-line
-         * kernels over the whole row, both stages in this launch */
-        if (c.ncol != 1 || c.nmat != 2 || c.mats[0].rows != c.mats[1].rows || mc || !straight ||
-            !straight_ms(MS, ext, nrm != nullptr) || k0 != 0 || mk * 128 != c.cols || accumulate || st0 != 0 ||
-            nst != c.nst || c.mats[0].rows > pair->cap)
+        /* the pair's activation is written by the straight-line kernels over
+         * the whole row, both stages in this launch: one column, or several
+         * staged in LDS (no K split, so each tile's sum is whole in one
+         * workgroup) */
+        if (c.nmat != 2 || c.mats[0].rows != c.mats[1].rows || !straight || k0 != 0 || mk * 128 != c.cols ||
+            accumulate || st0 != 0 || nst != c.nst || (long) c.mats[0].rows * c.ncol > pair->cap)
             return 1;
+        if (c.ncol > 1 ? mc != 1 || ext || nrm || (MS != 2 && MS != 4 && MS != 5 && MS != 8 && MS != 10)
+                       : mc || !straight_ms(MS, ext, nrm != nullptr))
+            return 1;
+        if (mc == 1) mc = 4;   /* the several-column pair's own kernel */
         A.pslot = pair->slot;
         A.pact = pair->act;
         A.pact16 = pair->act16;
@@ -1612,9 +1656,10 @@ int vq_norm_launch(const VqCall & c, const float * norm_w, float eps, uint16_t *
 }
 
 int vq_pair_launch(const VqCall & c, const VqPair & pair) {
-    /* one bf16 column in one K range, both matrices on the block kernel */
-    if (!pair.slot || pair.cap < 1 || c.ncol != 1 || !c.x || c.xf32 || ((uintptr_t) c.x & 15u) || c.nst < 1 ||
-        c.nst > 2 || c.nmat != 2 || c.variant || c.threads || c.grid || c.dim != 4 || c.cols % 128 || c.accumulate)
+    /* bf16 columns in one K range, both matrices on the block kernel */
+    if (!pair.slot || pair.cap < 1 || c.ncol < 1 || c.ncol > kMaxCols || !c.x || c.xf32 || ((uintptr_t) c.x & 15u) ||
+        c.nst < 1 || c.nst > 2 || c.nmat != 2 || c.variant || c.threads || c.grid || c.dim != 4 || c.cols % 128 ||
+        c.accumulate)
         return 1;
     for (int m = 0; m < c.nmat; m++) {
         if (!c.mats[m].y || c.mats[m].rows <= 0) return 1;

@@ -156,6 +156,43 @@ def test_fused_activation_is_bit_exact(sm, ref, dev, head_kind, monkeypatch):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("head_kind", ["q8_0", "vq"])
+def test_fused_activation_blocks_are_bit_exact(sm, ref, dev, head_kind, monkeypatch):
+    """Several columns: a short prompt chunk (3 tokens) and a verify block (4
+    tokens) write gelu(gate) * up from their gate/up launch, the two
+    matrices' sums meeting per (row, column); a model made with
+    SPARKMV_SEPARATE_ACT=1 runs the activation kernel instead. Both call the
+    same gelu, so every logit agrees bit for bit, and the fused model stays
+    within the bf16 bar of the oracle stepping the same tokens."""
+    import torch
+    fused, oracle = build(sm, ref, dev, head_kind, sm.X_BF16, FA_CFG)
+    monkeypatch.setenv("SPARKMV_SEPARATE_ACT", "1")
+    separate, _ = build(sm, ref, dev, head_kind, sm.X_BF16, FA_CFG)
+    monkeypatch.delenv("SPARKMV_SEPARATE_ACT")
+    V = FA_CFG["vocab"]
+    prompt, block = TOKENS[:3], TOKENS[3:7]
+    a = torch.zeros(V, device=dev)
+    b = torch.zeros(V, device=dev)
+    fused.forward_batch(prompt, 0, a)
+    separate.forward_batch(prompt, 0, b)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
+    for p, t in enumerate(prompt):
+        want = oracle.forward(t, p)
+    assert rel_l2(a.cpu().numpy(), want) <= BF16_RUN_BAR
+    la = torch.full((len(block), V), float("nan"), device=dev)
+    lb = torch.full((len(block), V), float("nan"), device=dev)
+    fused.verify(block, len(prompt), la)
+    separate.verify(block, len(prompt), lb)
+    torch.cuda.synchronize()
+    assert np.array_equal(la.cpu().numpy().view(np.uint32), lb.cpu().numpy().view(np.uint32))
+    got = la.cpu().numpy()
+    for i, t in enumerate(block):
+        err = rel_l2(got[i], oracle.forward(t, len(prompt) + i))
+        print(f"head {head_kind} fused-activation block row {i}: relL2 {err:.2e}")
+        assert err <= BF16_RUN_BAR
+
+
 def test_forward_refusals(sm, ref, dev):
     import torch
     model, _ = build(sm, ref, dev, "q8_0", sm.X_F32)
