@@ -193,6 +193,41 @@ def test_fused_activation_blocks_are_bit_exact(sm, ref, dev, head_kind, monkeypa
         assert err <= BF16_RUN_BAR
 
 
+# the reference model's hidden and FFN widths: a verify block's down launch
+# (2560 rows over 10240 columns at N = 8) takes chunk-split tiles through the
+# model's own exchange words
+REAL_FFN_CFG = dict(CFG, hidden=2560, intermediate=10240, layers=2)
+
+
+def test_verify_block_real_ffn_shape(sm, ref, dev):
+    """A verify block at the reference model's FFN shape (bf16 activations):
+    down's 8 columns split their K over chunk groups whose sums meet in the
+    model's exchange words, shared by the launches one at a time. Three
+    tokens one at a time, then a block of 4 twice (rolled back between):
+    every row against the oracle stepping the same tokens, and the two
+    blocks bit-equal (the words are zero again after each launch)."""
+    import torch
+    model, oracle = build(sm, ref, dev, "q8_0", sm.X_BF16, REAL_FFN_CFG)
+    V = REAL_FFN_CFG["vocab"]
+    prefix, block = TOKENS[:3], TOKENS[3:7]
+    one = torch.empty(V, device=dev)
+    for p, t in enumerate(prefix):
+        model.forward(t, p, one)
+        oracle.forward(t, p)
+    outs = []
+    for _ in range(2):
+        lg = torch.full((len(block), V), float("nan"), device=dev)
+        model.verify(block, len(prefix), lg)
+        torch.cuda.synchronize()
+        outs.append(lg.cpu().numpy())
+        model.rollback(len(prefix))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    for i, t in enumerate(block):
+        err = rel_l2(outs[0][i], oracle.forward(t, len(prefix) + i))
+        print(f"real FFN shape, block row {i}: relL2 {err:.2e}")
+        assert err <= BF16_RUN_BAR
+
+
 def test_forward_refusals(sm, ref, dev):
     import torch
     model, _ = build(sm, ref, dev, "q8_0", sm.X_F32)
