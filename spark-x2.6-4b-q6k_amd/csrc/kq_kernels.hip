@@ -902,7 +902,8 @@ static int kq_q8_mfma_k(const uint8_t * bp, int rows, int cols, const void * x, 
  *    91.6 and two chunks ahead 85);
  *  - several columns: at most one workgroup of eight waves per CU, each
  *    wave a strided share of the tiles, two chunks ahead (8 columns:
- *    88.4-89.2 us; one tile per wave would stage 41 KB of x per tile). */
+ *    88.4-89.2 us; one tile per wave would stage 41 KB of x per tile;
+ *    twelve waves, whose slots LDS also holds, 103.5 us). */
 static int kq_q8_mfma(const uint8_t * bp, int rows, int cols, const void * x, int xf32, int ldx, int ncol, float * y,
                       int ldy, int accumulate, hipStream_t s) {
     if (cols % (32 * kQ8Chunk) || ((uintptr_t) bp & 15u)) return 1;
