@@ -407,6 +407,49 @@ __global__ __launch_bounds__(256) void fw_rope_kv_n_kernel(float * qkv, int ldq,
     }
 }
 
+/* fw_rope_kv_n_kernel's work for up to kMaxCols tokens, spread over
+ * N x (heads + kv_heads) workgroups: token t = blockIdx.x, head h =
+ * blockIdx.y (query heads, then kv heads), thread i < pdim / 2 computing
+ * pair i's cos and sin with the same expressions and rotating the head's
+ * pair in place; a kv head's rotated pair, its elements past pdim and its v
+ * go to the cache too. One load, rotation and store per thread: an 8-token
+ * verify block 3141-3145 -> 3061 us against fw_rope_kv_n_kernel's eight
+ * workgroups looping over the heads (5.8 us per launch). Long chunks keep
+ * fw_rope_kv_n_kernel: this shape (or head groups looped per workgroup)
+ * made a 512-token chunk 100-260 us slower. blockDim.x = 128 >= pdim / 2. */
+__global__ __launch_bounds__(128) void fw_rope_kv_heads_kernel(float * qkv, int ldq, int qd, int kvd, int heads,
+                                                                int hd, int pdim, float theta, int pos0, float * kc,
+                                                                float * vc) {
+    const int half = pdim / 2, t = blockIdx.x, h = blockIdx.y, i = threadIdx.x, pos = pos0 + t;
+    float * row = qkv + (size_t) t * ldq;
+    const bool kv = h >= heads;
+    const int kh = h - heads;
+    float * base = kv ? row + qd + (size_t) kh * hd : row + (size_t) h * hd;
+    float * kr = kv ? kc + (size_t) pos * kvd + (size_t) kh * hd : nullptr;
+    if (kv) {
+        /* elements past pdim and v (neither is written by the rotation) */
+        const float * vr = row + qd + kvd + (size_t) kh * hd;
+        float * vo = vc + (size_t) pos * kvd + (size_t) kh * hd;
+        for (int e = i; e < hd; e += blockDim.x) {
+            vo[e] = vr[e];
+            if (e >= 2 * half) kr[e] = base[e];
+        }
+    }
+    if (i < half) {
+        const float freq = 1.0f / powf(theta, (float) (2 * i) / (float) pdim);
+        const float a = (float) pos * freq;
+        const float c = cosf(a), sn = sinf(a);
+        const float x0 = base[i], x1 = base[i + half];
+        const float r0 = x0 * c - x1 * sn, r1 = x1 * c + x0 * sn;
+        base[i] = r0;
+        base[i + half] = r1;
+        if (kv) {
+            kr[i] = r0;
+            kr[i + half] = r1;
+        }
+    }
+}
+
 /* Attention partials of token t = blockIdx.z (query rotated in qkv, every
  * key in the cache), as fw_attn_part_kernel otherwise. */
 template <int VPL>
@@ -1414,6 +1457,19 @@ int mat_n(const Model & m, const void * const * st, int rows, int cols, const vo
     return prefill_simple_launch(st, m.c.nstages, L, x, xf32, (size_t) cols, 1, N, y, ldy, acc, s);
 }
 
+/* Rope and the KV store of N tokens at pos0 .. pos0 + N - 1 (rows of qkv at
+ * stride ldq), the shape chosen by N. */
+int rope_kv_launch(float * qkv, int N, int ldq, int qd, int kvd, int heads, int kv_heads, int hd, int pdim,
+                          float theta, int pos0, float * kc, float * vc, hipStream_t s) {
+    if (N <= kMaxCols)
+        hipLaunchKernelGGL(fw_rope_kv_heads_kernel, dim3(N, heads + kv_heads), dim3(128), 0, s, qkv, ldq, qd, kvd,
+                           heads, hd, pdim, theta, pos0, kc, vc);
+    else
+        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3(N), dim3(256), 0, s, qkv, ldq, qd, kvd, heads, kv_heads, hd,
+                           pdim, theta, pos0, kc, vc);
+    return check_launch("rope launch");
+}
+
 /* A verify block: the forward of ntok consecutive tokens at pos .. pos + ntok - 1
  * with every matvec over ntok columns (weights decoded once for the block),
  * then the head over the same columns; logits are [ntok][vocab]. */
@@ -1448,9 +1504,8 @@ int block(Model * m, const uint32_t * tokens, int N, int pos, float * logits, hi
         if (gemv2(*m, L.qkv, ldq, m->vqkv, L.attn_gate, c.heads, m->vg, c.hidden, xin, s, N, ldq)) return -1;
         const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
         const int pdim = rope_dim(hd, full ? c.rope_full_partial : c.rope_slide_partial);
-        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3(N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd, c.heads, c.kv_heads, hd,
-                           pdim, (float) theta, pos, kc, vc);
-        if (check_launch("rope launch")) return -1;
+        if (rope_kv_launch(m->vqkv, N, ldq, qd, kvd, c.heads, c.kv_heads, hd, pdim, (float) theta, pos, kc, vc, s))
+            return -1;
         const int window = full ? 0 : c.sliding_window;
         const int last = pos + N - 1;
         const int span = full || c.sliding_window > last + 1 ? last + 1 : c.sliding_window;
@@ -1524,9 +1579,8 @@ int prompt(Model * m, int N, int pos, float * logits, hipStream_t s) {
         }
         const double theta = full ? c.rope_full_theta : c.rope_slide_theta;
         const int pdim = rope_dim(hd, full ? c.rope_full_partial : c.rope_slide_partial);
-        hipLaunchKernelGGL(fw_rope_kv_n_kernel, dim3(N), dim3(256), 0, s, m->vqkv, ldq, qd, kvd, c.heads, c.kv_heads, hd,
-                           pdim, (float) theta, pos, kc, vc);
-        if (check_launch("rope launch")) return -1;
+        if (rope_kv_launch(m->vqkv, N, ldq, qd, kvd, c.heads, c.kv_heads, hd, pdim, (float) theta, pos, kc, vc, s))
+            return -1;
         const int window = full ? 0 : c.sliding_window;
         const dim3 ag((unsigned) c.kv_heads, (unsigned) N), ab((unsigned) (64 * (c.heads / c.kv_heads)));
         uint16_t * a16 = b16 ? m->vattn16 : nullptr;
