@@ -251,19 +251,22 @@ __global__ __launch_bounds__(256) void fw_attn_part_kernel(const float * qkv, in
     }
 }
 
+/* The combine of one query head from its nch chunk partials P (o, m, l per
+ * chunk at stride hd + 2), four waves: M = max m_c, L = sum_c l_c e^(m_c - M)
+ * (threads over chunks), wave w summing e^(m_c - M) o_c over chunks w,
+ * w + 4, ... in increasing order, then out = the waves' sum / L times the
+ * head's sigmoid gate gl. Each wave's first kPre chunk vectors are requested
+ * before the m_c reductions, so up to 4 * kPre chunks cost one memory round
+ * trip (a wave had taken one or four chunks per round trip: at context 1024
+ * five of them). wts: 2 * nch floats of dynamic LDS. */
 template <int VPL>
-__global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part, const float * gate, const int * st,
-                                                              int window, int nch_max, float * out, uint16_t * out16) {
-    constexpr int hd = 64 * VPL;
+__device__ __forceinline__ void attn_combine_head(const float * P, int nch, float gl, float * out, uint16_t * out16,
+                                                  float * wts) {
+    constexpr int hd = 64 * VPL, kPre = 20;
     typedef float fv __attribute__((ext_vector_type(VPL)));
-    extern __shared__ float wts[];             /* per chunk: m_c, then e^(m_c - M); then l_c */
     __shared__ float red[8];
     __shared__ fv acc[4][64];
-    const int pos = st[1];
-    const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
-    const int nch = (pos + 1 - start + kAttnChunk - 1) / kAttnChunk;
-    const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const float * P = part + (size_t) h * nch_max * (hd + 2);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     float * ls = wts + nch;
     float M = -INFINITY;
     for (int c = t; c < nch; c += 256) {
@@ -271,6 +274,15 @@ __global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part
         wts[c] = mc;
         ls[c] = lc;
         M = fmaxf(M, mc);
+    }
+    const float * Pl = P + lane * VPL;
+    fv pre[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; k++) {
+        /* chunks past nch re-read the last one (no branch between the
+         * loads) and are not added */
+        const int c = min(wave + 4 * k, nch - 1);
+        pre[k] = *(const fv *) (Pl + (size_t) c * (hd + 2));
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
@@ -287,11 +299,11 @@ __global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part
     for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
     if (lane == 0) red[4 + wave] = L;
     __syncthreads();
-    /* wave w sums chunks w, w + 4, ... over the lane's VPL elements, four
-     * chunks' loads in flight at a time */
     fv o = (fv) 0.0f;
-    const float * Pl = P + lane * VPL;
-    int c = wave;
+#pragma unroll
+    for (int k = 0; k < kPre; k++)
+        if (wave + 4 * k < nch) o += wts[wave + 4 * k] * pre[k];
+    int c = wave + 4 * kPre;
     for (; c + 12 < nch; c += 16) {
         const fv a0 = *(const fv *) (Pl + (size_t) c * (hd + 2)), a1 = *(const fv *) (Pl + (size_t) (c + 4) * (hd + 2));
         const fv a2 = *(const fv *) (Pl + (size_t) (c + 8) * (hd + 2)), a3 = *(const fv *) (Pl + (size_t) (c + 12) * (hd + 2));
@@ -305,14 +317,27 @@ __global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part
     __syncthreads();
     if (wave == 0) {
         const float inv = 1.0f / ((red[4] + red[5]) + (red[6] + red[7]));
-        const float g = 1.0f / (1.0f + expf(-gate[h]));
+        const float g = 1.0f / (1.0f + expf(-gl));
         const fv r = ((acc[0][lane] + acc[1][lane]) + (acc[2][lane] + acc[3][lane])) * inv * g;
 #pragma unroll
         for (int v = 0; v < VPL; v++) {
-            out[(size_t) h * hd + lane * VPL + v] = r[v];
-            if (out16) out16[(size_t) h * hd + lane * VPL + v] = fw_bf16(r[v]);
+            out[lane * VPL + v] = r[v];
+            if (out16) out16[lane * VPL + v] = fw_bf16(r[v]);
         }
     }
+}
+
+template <int VPL>
+__global__ __launch_bounds__(256) void fw_attn_combine_kernel(const float * part, const float * gate, const int * st,
+                                                              int window, int nch_max, float * out, uint16_t * out16) {
+    constexpr int hd = 64 * VPL;
+    extern __shared__ float wts[];             /* per chunk: m_c, then e^(m_c - M); then l_c */
+    const int pos = st[1];
+    const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
+    const int nch = (pos + 1 - start + kAttnChunk - 1) / kAttnChunk;
+    const int h = blockIdx.x;
+    attn_combine_head<VPL>(part + (size_t) h * nch_max * (hd + 2), nch, gate[h], out + (size_t) h * hd,
+                           out16 ? out16 + (size_t) h * hd : nullptr, wts);
 }
 
 /* ---- a verify block: ntok <= 8 consecutive tokens at positions pos0 .. ----
@@ -514,54 +539,14 @@ __global__ __launch_bounds__(256) void fw_attn_combine_n_kernel(const float * pa
                                                                 int pos0, int window, int heads, int nch_max,
                                                                 float * out, uint16_t * out16) {
     constexpr int hd = 64 * VPL;
-    typedef float fv __attribute__((ext_vector_type(VPL)));
     extern __shared__ float wts[];
-    __shared__ float red[8];
-    __shared__ fv acc[4][64];
     const int t = blockIdx.y, pos = pos0 + t;
     const int start = window > 0 && pos + 1 > window ? pos + 1 - window : 0;
     const int nch = (pos + 1 - start + kAttnChunk - 1) / kAttnChunk;
-    const int h = blockIdx.x, th = threadIdx.x, lane = th & 63, wave = th >> 6;
-    const float * P = part + ((size_t) t * heads + h) * nch_max * (hd + 2);
-    float * ls = wts + nch;
-    float M = -INFINITY;
-    for (int c = th; c < nch; c += 256) {
-        const float mc = P[(size_t) c * (hd + 2) + hd], lc = P[(size_t) c * (hd + 2) + hd + 1];
-        wts[c] = mc;
-        ls[c] = lc;
-        M = fmaxf(M, mc);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if (lane == 0) red[wave] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float L = 0.0f;
-    for (int c = th; c < nch; c += 256) {
-        const float w = expf(wts[c] - M);
-        wts[c] = w;
-        L += w * ls[c];
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
-    if (lane == 0) red[4 + wave] = L;
-    __syncthreads();
-    fv o = (fv) 0.0f;
-    const float * Pl = P + lane * VPL;
-    for (int c = wave; c < nch; c += 4) o += wts[c] * *(const fv *) (Pl + (size_t) c * (hd + 2));
-    acc[wave][lane] = o;
-    __syncthreads();
-    if (wave == 0) {
-        const float inv = 1.0f / ((red[4] + red[5]) + (red[6] + red[7]));
-        const float g = 1.0f / (1.0f + expf(-gate[(size_t) t * ldg + h]));
-        const fv r = ((acc[0][lane] + acc[1][lane]) + (acc[2][lane] + acc[3][lane])) * inv * g;
-        const size_t ob = (size_t) t * heads * hd + (size_t) h * hd + lane * VPL;
-#pragma unroll
-        for (int v = 0; v < VPL; v++) {
-            out[ob + v] = r[v];
-            if (out16) out16[ob + v] = fw_bf16(r[v]);
-        }
-    }
+    const int h = blockIdx.x;
+    const size_t ob = (size_t) t * heads * hd + (size_t) h * hd;
+    attn_combine_head<VPL>(part + ((size_t) t * heads + h) * nch_max * (hd + 2), nch, gate[(size_t) t * ldg + h],
+                           out + ob, out16 ? out16 + ob : nullptr, wts);
 }
 
 /* act = gelu(g) * u with torch's exact gelu, erf in f64 as model.rs:253-258
