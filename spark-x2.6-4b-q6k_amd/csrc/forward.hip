@@ -179,9 +179,21 @@ __global__ __launch_bounds__(256) void fw_attn_part_kernel(const float * qkv, in
     const int h = kvh * G + wave;               /* h * kv_heads / heads == kvh */
     const int half = pdim / 2;                  /* a multiple of VPL (the host checks) */
     /* x rotated by position pos: element e < half pairs with e + half,
-     * e in [half, pdim) with e - half (apply_rope, model.rs:430-438) */
+     * e in [half, pdim) with e - half (apply_rope, model.rs:430-438). The
+     * lane's cos and sin are read unconditionally (elements past pdim read
+     * entry 0 and do not use it) and before the K and V rows: read inside
+     * the per-element branch, each took a memory round trip of its own,
+     * after the query's, ahead of the rows' loads. */
+    const int e0 = lane * VPL;
+    fv cv, sv;
+#pragma unroll
+    for (int v = 0; v < VPL; v++) {
+        const int e = e0 + v;
+        const int i = e < half ? e : (e < 2 * half ? e - half : 0);
+        cv[v] = rtab[i];
+        sv[v] = rtab[128 + i];
+    }
     auto rope = [&](fv x) -> fv {
-        const int e0 = lane * VPL;
         const int pl = e0 < half ? lane + half / VPL : (e0 < pdim ? lane - half / VPL : lane);
         fv p, r = x;
 #pragma unroll
@@ -189,24 +201,22 @@ __global__ __launch_bounds__(256) void fw_attn_part_kernel(const float * qkv, in
 #pragma unroll
         for (int v = 0; v < VPL; v++) {
             const int e = e0 + v;
-            if (e < 2 * half) {
-                const int i = e < half ? e : e - half;
-                const float c = rtab[i], sn = rtab[128 + i];
-                r[v] = e < half ? x[v] * c - p[v] * sn : x[v] * c + p[v] * sn;
-            }
+            if (e < 2 * half) r[v] = e < half ? x[v] * cv[v] - p[v] * sv[v] : x[v] * cv[v] + p[v] * sv[v];
         }
         return r;
     };
-    const fv q = rope(*(const fv *) (qkv + (size_t) h * hd + lane * VPL));
+    const fv qx = *(const fv *) (qkv + (size_t) h * hd + lane * VPL);
     const float * kb = kc + (size_t) (start + j0) * kvd + (size_t) kvh * hd + lane * VPL;
     const float * vb = vc + (size_t) (start + j0) * kvd + (size_t) kvh * hd + lane * VPL;
     /* every K and V row of the chunk requested at once (rows past the
-     * window re-read the last one and get weight zero) */
+     * window re-read the last one and get weight zero), then the query
+     * rotated while they are in flight */
     fv kr[C], vr[C];
 #pragma unroll
     for (int j = 0; j < C; j++) kr[j] = *(const fv *) (kb + (size_t) min(j, jn - 1) * kvd);
 #pragma unroll
     for (int j = 0; j < C; j++) vr[j] = *(const fv *) (vb + (size_t) min(j, jn - 1) * kvd);
+    const fv q = rope(qx);
     if (j0 + jn == n) {
         /* this chunk ends at pos: the new key and value, from qkv */
         const fv kn = rope(*(const fv *) (qkv + qd + (size_t) kvh * hd + lane * VPL));
