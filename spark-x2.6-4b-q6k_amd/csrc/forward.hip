@@ -290,7 +290,9 @@ __device__ __forceinline__ void attn_combine_head(const float * P, int nch, floa
 #pragma unroll
     for (int k = 0; k < kPre; k++) {
         /* chunks past nch re-read the last one (no branch between the
-         * loads) and are not added */
+         * loads) and are not added. After the m_c loads on purpose: their
+         * round trip then overlaps the reductions below (issued first, all
+         * of them waited for together: decode token 2093 -> 2111 us) */
         const int c = min(wave + 4 * k, nch - 1);
         pre[k] = *(const fv *) (Pl + (size_t) c * (hd + 2));
     }
