@@ -564,9 +564,28 @@ __global__ __launch_bounds__(256) void fw_attn_combine_n_kernel(const float * pa
 /* act = gelu(g) * u with torch's exact gelu, erf in f64 as model.rs:253-258
  * calls it. */
 __global__ void fw_gelu_mul_kernel(const float * g, const float * u, float * act, uint16_t * act16, int n) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += blockDim.x * gridDim.x) {
+    /* four elements per thread through 16-byte loads (g, u and act 16-byte
+     * aligned, act16 8-byte aligned: the callers' buffers), the tail apart;
+     * act null: only act16 is written (the bf16 model reads nothing else) */
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    typedef uint16_t u4v __attribute__((ext_vector_type(4)));
+    const int n4 = n / 4;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += blockDim.x * gridDim.x) {
+        const f4v a = ((const f4v *) g)[i], b = ((const f4v *) u)[i];
+        f4v r;
+        u4v r16;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            r[k] = gelu_mul(a[k], b[k]);
+            r16[k] = fw_bf16(r[k]);
+        }
+        if (act) ((f4v *) act)[i] = r;
+        if (act16) ((u4v *) act16)[i] = r16;
+    }
+    const int i = 4 * n4 + blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
         const float r = gelu_mul(g[i], u[i]);
-        act[i] = r;
+        if (act) act[i] = r;
         if (act16) act16[i] = fw_bf16(r);
     }
 }
@@ -1089,7 +1108,8 @@ int gate_up_act_n(const Model & m, const void * const * gate, const void * const
         if (rc <= 0) return rc;
     }
     if (gemv2(m, gate, rows, mg, up, rows, mu, cols, x, s, N, rows)) return -1;
-    hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * rows + 255) / 256), dim3(256), 0, s, mg, mu, act, act16, N * rows);
+    hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * rows / 4 + 255) / 256 + 1), dim3(256), 0, s, mg, mu, act, act16,
+                       N * rows);
     return check_launch("gelu launch");
 }
 
@@ -1392,8 +1412,8 @@ int chain(Model * m, float * logits, hipStream_t s) {
                        m->fuse_act ? &pair : nullptr, &act_done))
             return -1;
         if (!act_done) {
-            hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((c.intermediate + 255) / 256), dim3(256), 0, s, m->mg, m->mu,
-                               m->act, b16 ? m->act16 : nullptr, c.intermediate);
+            hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((c.intermediate / 4 + 255) / 256 + 1), dim3(256), 0, s, m->mg,
+                               m->mu, m->act, b16 ? m->act16 : nullptr, c.intermediate);
             if (check_launch("gelu launch")) return -1;
         }
         if (gemv(*m, L.down, c.hidden, c.intermediate, b16 ? (const void *) m->act16 : (const void *) m->act, m->h,
@@ -1607,8 +1627,10 @@ int prompt(Model * m, int N, int pos, float * logits, hipStream_t s) {
         } else {
             if (mat_n(*m, L.gate, c.intermediate, c.hidden, xin, m->vmg, 0, s, N, c.intermediate)) return -1;
             if (mat_n(*m, L.up, c.intermediate, c.hidden, xin, m->vmu, 0, s, N, c.intermediate)) return -1;
-            hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * c.intermediate + 255) / 256), dim3(256), 0, s, m->vmg,
-                               m->vmu, m->vact, b16 ? m->vact16 : nullptr, N * c.intermediate);
+            /* bf16: down reads act16 only, so the f32 copy is not written */
+            hipLaunchKernelGGL(fw_gelu_mul_kernel, dim3((N * c.intermediate / 4 + 255) / 256 + 1), dim3(256), 0, s,
+                               m->vmg, m->vmu, b16 ? nullptr : m->vact, b16 ? m->vact16 : nullptr,
+                               N * c.intermediate);
             if (check_launch("gelu launch")) return -1;
         }
         if (mat_n(*m, L.down, c.hidden, c.intermediate, b16 ? (const void *) m->vact16 : (const void *) m->vact, m->vh,
